@@ -1,0 +1,364 @@
+"""Pins the CPU oracle before anything is compared against it.
+
+Each oracle function is checked against the reference's own known answers
+where they exist (the writer goldens: sha256[:16] of packed codes and of the
+skipzero tensors), and otherwise against a structurally different
+formulation: bit-serial unpacking, brute-force loops, an independent C
+restatement, closed forms and invariants chosen so a dropped term, a wrong
+shift or a transposed operand fails.
+"""
+import numpy as np
+import pytest
+
+from golden import writer_fixture as wf
+from oracle import vq_oracle as vo
+
+
+# ------------------------------------------------ reference golden vectors
+@pytest.fixture(scope="module")
+def fx():
+    return wf.vq_tensors(K=16, seed=1)
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return wf.golden()
+
+
+def test_fixture_regenerates_reference_tensors(fx, gold):
+    """The unpacked codes, codebooks and scales the reference hashed."""
+    g = gold["sz_pack"]["tensors"]
+    n = 0
+    for m, t in fx.items():
+        for name in ("codes", "codebook", "vq_scales"):
+            key = f"{m}.{name}"
+            if key in g:
+                assert wf.sha16(t[name]) == g[key]["sha"], key
+                assert list(t[name].shape) == g[key]["shape"]
+                n += 1
+    assert n >= 24
+
+
+@pytest.mark.parametrize("golden_name", ["pack", "pack_straddle"])
+def test_pack_matches_reference_golden(fx, gold, golden_name, oracle_c):
+    g = gold[golden_name]["tensors"]
+    for m, t in fx.items():
+        spec = gold[golden_name]["vq_modules"][m]
+        bits = vo.pack_bits_for(spec["k"], spec["in"] // spec["dim"])
+        assert bits == spec["pack_bits"] == 4
+        packed = vo.pack(t["codes"], bits)
+        assert packed.dtype == np.uint32 and list(packed.shape) == g[m + ".codes"]["shape"]
+        assert wf.sha16(packed) == g[m + ".codes"]["sha"], m
+        assert wf.sha16(oracle_c.pack(t["codes"], bits)) == g[m + ".codes"]["sha"], m
+        # the untouched tensors pass through unchanged
+        assert wf.sha16(t["codebook"]) == g[m + ".codebook"]["sha"]
+        assert wf.sha16(t["vq_scales"]) == g[m + ".vq_scales"]["sha"]
+        back = vo.unpack(packed, t["codes"].shape[-1], bits)
+        assert np.array_equal(back, t["codes"])
+
+
+def test_skipzero_matches_reference_golden(fx, gold):
+    g = gold["sz_pack"]["tensors"]
+    meta = gold["sz_pack"]["vq_skipzero"]
+    m = "model.language_model.layers.0.mlp.switch_mlp.up_proj"
+    t = fx[m]
+    sz = vo.skipzero_compact(t["codes"], t["vq_scales"])
+    for name in ("sz_codes", "sz_scales", "sz_rowmask", "sz_shape"):
+        assert wf.sha16(sz[name]) == g[f"{m}.{name}"]["sha"], name
+        assert list(sz[name].shape) == g[f"{m}.{name}"]["shape"]
+    assert sz["sz_codes"].shape[0] == meta[m]["live_rows"] == 251
+    # expansion restores the live rows byte for byte and zeroes the dead
+    full = vo.skipzero_expand(sz["sz_shape"], sz["sz_rowmask"], sz["sz_codes"])
+    live = ~(t["vq_scales"].astype(np.float32) < vo.SZ_TINY).all(-1)
+    assert np.array_equal(full[live], t["codes"][live])
+    assert not full[~live].any()
+
+
+# ------------------------------------------------------- widths and layout
+def test_widths_at_baseline_shapes():
+    assert vo.bits_for_k(256) == 8 and vo.bits_for_k(4096) == 12
+    assert vo.bits_for_k(16384) == 14 and vo.bits_for_k(65536) == 16
+    # SURVEY shapes: c2 gate/up NSUB 512 -> 192, down NSUB 128 -> 48;
+    # c3 NSUB 512 -> 224, 128 -> 56; c5 NSUB 640 at 16 bits == 640 u16.
+    assert vo.words_per_row(512, 12) == 192 and vo.words_per_row(128, 12) == 48
+    assert vo.words_per_row(512, 14) == 224 and vo.words_per_row(128, 14) == 56
+    assert vo.words_per_row(640, 16) * 4 == 640 * 2
+    assert vo.words_per_row(80, 14) == 42          # ragged tail (Flash-2.1 shape)
+    with pytest.raises(ValueError):
+        vo.bits_for_k(3000)
+
+
+def test_pack_bits_for_rule():
+    assert vo.pack_bits_for(256, 512) == 0         # byte aligned stays unpacked
+    assert vo.pack_bits_for(65536, 512) == 0
+    assert vo.pack_bits_for(4096, 512) == 12
+    assert vo.pack_bits_for(4096, 80) == 0         # unaligned NSUB
+    assert vo.pack_bits_for(4096, 80, pack_unaligned=True) == 12
+
+
+@pytest.mark.parametrize("bits", list(range(1, 17)))
+@pytest.mark.parametrize("nsub", [1, 31, 32, 33, 80, 96])
+def test_pack_unpack_brute_force(bits, nsub, oracle_c):
+    rng = np.random.default_rng(bits * 1000 + nsub)
+    codes = rng.integers(0, 1 << bits, (3, 2, nsub)).astype(np.uint16)
+    packed = vo.pack(codes, bits)
+    assert packed.shape == (3, 2, vo.words_per_row(nsub, bits))
+    assert np.array_equal(vo.unpack(packed, nsub, bits), codes)
+    assert np.array_equal(vo.unpack_bitserial(packed, nsub, bits), codes)
+    assert np.array_equal(oracle_c.pack(codes, bits), packed)
+    assert np.array_equal(oracle_c.unpack(packed, nsub, bits), codes)
+    # padded tail words hold zeros only
+    nblk = (nsub + 31) // 32
+    if nsub % 32:
+        used_bits = (nsub % 32) * bits
+        tail = packed[..., (nblk - 1) * bits:].reshape(-1, bits)
+        for w in range(bits):
+            lo = w * 32
+            if lo >= used_bits:
+                assert not tail[:, w].any()
+
+
+def test_widths_8_16_are_byte_arrays():
+    rng = np.random.default_rng(7)
+    c8 = rng.integers(0, 256, (4, 64)).astype(np.uint8)
+    assert np.array_equal(vo.pack(c8, 8).view(np.uint8), c8)
+    c16 = rng.integers(0, 65536, (4, 64)).astype(np.uint16)
+    assert np.array_equal(vo.pack(c16, 16).view(np.uint16), c16)
+
+
+def test_pack_rejects_wide_codes():
+    with pytest.raises(ValueError):
+        vo.pack(np.array([[16]], np.uint16), 4)
+
+
+# ------------------------------------------------------------------ dequant
+def test_fp16_rounding_matches_ieee(oracle_c):
+    """The C restatement's RNE conversion vs numpy's IEEE conversion over
+    random bit patterns and every tie/edge class."""
+    rng = np.random.default_rng(3)
+    pats = rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32)
+    specials = np.array([0x00000000, 0x80000000, 0x7f800000, 0xff800000,
+                         0x477fe000, 0x477ff000, 0x477fefff, 0x47800000,  # 65504 / tie / below / 65536
+                         0x33800000, 0x33000000, 0x33000001, 0x387fc000,  # 2^-24, 2^-25 tie, min normal edge
+                         0x38800000, 0x00000001, 0x3f801000, 0x3f803000],  # ties to even
+                        np.uint32)
+    vals = np.concatenate([pats, specials]).view(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    got = oracle_c.f32_to_f16_bits(vals)
+    nan = np.isnan(vals)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all((got[nan] & 0x7c00) == 0x7c00) and np.all(got[nan] & 0x3ff)
+
+
+def _dequant_case(rng, rows, nsub, d, K, G):
+    codes = rng.integers(0, K, (rows, nsub)).astype(np.uint16)
+    cb = (rng.standard_normal((K, d)) * 0.02).astype(np.float16)
+    sc = rng.uniform(0.5, 1.5, (rows, nsub * d // G)).astype(np.float16)
+    return codes, cb, sc
+
+
+@pytest.mark.parametrize("d", [2, 4, 8])
+def test_dequant_numpy_vs_c(d, oracle_c):
+    rng = np.random.default_rng(d)
+    codes, cb, sc = _dequant_case(rng, 16, 64, d, 256, 64)
+    # special values: subnormal codebook, +-inf and NaN scales, zero scales
+    cb[0] = np.float16(2.0**-20)
+    cb[1] = -cb[1]
+    sc[0, 0] = np.inf
+    sc[1, 0] = -np.inf
+    sc[2, 0] = np.nan
+    sc[3, :] = 0
+    codes[:4, :4] = [0, 1, 2, 3]
+    a = vo.dequant(codes, cb, sc, 64).view(np.uint16)
+    b = oracle_c.dequant(codes, cb, sc, 64).view(np.uint16)
+    nan = np.isnan(a.view(np.float16))
+    assert np.array_equal(nan, np.isnan(b.view(np.float16)))
+    assert np.array_equal(a[~nan], b[~nan])
+
+
+def test_dequant_single_rounding():
+    """fp16*fp16 is exact in fp32, so the result equals the float64 product
+    rounded once to fp16."""
+    rng = np.random.default_rng(11)
+    codes, cb, sc = _dequant_case(rng, 8, 32, 4, 64, 64)
+    w = vo.dequant(codes, cb, sc, 64)
+    exact = (cb.astype(np.float64)[codes.astype(np.int64)].reshape(8, -1)
+             * np.repeat(sc.astype(np.float64), 64, axis=1))
+    assert np.array_equal(w.view(np.uint16), exact.astype(np.float16).view(np.uint16))
+
+
+# -------------------------------------------------------- decode-then-matmul
+def test_decode_matmul_brute_force(oracle_c):
+    rng = np.random.default_rng(5)
+    codes, cb, sc = _dequant_case(rng, 6, 16, 4, 32, 32)
+    w = vo.dequant(codes, cb, sc, 32)
+    x = rng.standard_normal((3, 64)).astype(np.float32)
+    y = vo.decode_matmul(x, w)
+    ref = np.zeros((3, 6))
+    for t in range(3):
+        for r in range(6):
+            for i in range(64):
+                ref[t, r] += float(x[t, i]) * float(w[r, i])
+    assert np.allclose(y, ref, rtol=1e-12, atol=1e-12)
+    assert np.allclose(oracle_c.gemv_f32(x, w), ref, rtol=1e-5, atol=1e-6)
+
+
+def test_decode_matmul_closed_forms():
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((2, 128)).astype(np.float32)
+    codes = np.zeros((4, 32), np.uint16)
+    cb = np.zeros((8, 4), np.float16)
+    cb[0] = 1.0
+    sc = np.ones((4, 2), np.float16)
+    y = vo.decode_matmul(x, vo.dequant(codes, cb, sc, 64))
+    assert np.allclose(y, np.repeat(x.astype(np.float64).sum(1, keepdims=True), 4, 1))
+    sc[:, 1] = 2.0                         # second group doubled
+    y2 = vo.decode_matmul(x, vo.dequant(codes, cb, sc, 64))
+    want = x[:, :64].sum(1) + 2 * x[:, 64:].sum(1)
+    assert np.allclose(y2, want[:, None], rtol=1e-6)
+
+
+def test_expert_gemv_xkrep_and_row_table():
+    rng = np.random.default_rng(8)
+    E, OUT, NSUB, d, K, G = 3, 8, 16, 4, 64, 64
+    codes = rng.integers(0, K, (E, OUT, NSUB)).astype(np.uint16)
+    cb = (rng.standard_normal((K, d)) * 0.05).astype(np.float16)
+    sc = rng.uniform(0.5, 1.5, (E, OUT, NSUB * d // G)).astype(np.float16)
+    x = rng.standard_normal((2, NSUB * d)).astype(np.float32)
+    eidx = np.array([2, 0, 1, 2])
+    y = vo.expert_gemv(x, eidx, codes, cb, sc, G, xkrep=2)
+    for n in range(4):
+        w = vo.dequant(codes[eidx[n]], cb, sc[eidx[n]], G)
+        assert np.allclose(y[n], x[n // 2].astype(np.float64) @ w.astype(np.float64).T)
+    # skipzero: dead rows -> exact zero, live rows identical to expanded form
+    sc2 = sc.copy()
+    sc2[0, :3] = 0
+    sc2[2, 5] = 0
+    sz = vo.skipzero_compact(codes, sc2)
+    rt = vo.skipzero_row_table(sz["sz_rowmask"], E, OUT)
+    yc = vo.expert_gemv(x, eidx, sz["sz_codes"], cb, sz["sz_scales"], G, xkrep=2, row_table=rt)
+    ye = vo.expert_gemv(x, eidx, codes, cb, sc2, G, xkrep=2)
+    assert np.array_equal(yc, ye)
+    assert (yc[1, :3] == 0).all() and (yc[0, 5] == 0)
+
+
+def test_row_table_brute_force():
+    rng = np.random.default_rng(9)
+    E, OUT = 5, 37
+    live = rng.random((E, OUT)) > 0.4
+    live[2] = False
+    rm = np.packbits(live, axis=-1, bitorder="little")
+    rt = vo.skipzero_row_table(rm, E, OUT)
+    k = 0
+    for e in range(E):
+        for r in range(OUT):
+            if live[e, r]:
+                assert rt[e, r] == k
+                k += 1
+            else:
+                assert rt[e, r] == -1
+
+
+# --------------------------------------------------------------- MoE block
+def test_route_brute_force():
+    rng = np.random.default_rng(10)
+    lg = rng.standard_normal((5, 64)).astype(np.float32)
+    ids, w = vo.route(lg, 8)
+    for t in range(5):
+        order = sorted(range(64), key=lambda e: -float(lg[t, e]))[:8]
+        assert list(ids[t]) == order
+        p = np.exp(lg[t].astype(np.float64) - lg[t].max())
+        assert np.allclose(w[t], p[order] / p[order].sum())
+    assert np.allclose(w.sum(1), 1.0)
+    ids2, w2 = vo.route(lg + 3.0, 8)          # softmax shift invariance
+    assert np.array_equal(ids, ids2) and np.allclose(w, w2)
+
+
+def _proj(rng, E, OUT, IN, d=4, K=64, G=64):
+    return {"codes": rng.integers(0, K, (E, OUT, IN // d)).astype(np.uint16),
+            "codebook": (rng.standard_normal((K, d)) * 0.05).astype(np.float16),
+            "scales": rng.uniform(0.5, 1.5, (E, OUT, IN // G)).astype(np.float16),
+            "group": G}
+
+
+def test_moe_identical_experts_collapse():
+    """Equal experts + renormalised weights -> the layer is one expert."""
+    rng = np.random.default_rng(12)
+    E, H, I = 6, 128, 64
+    g, u, dn = (_proj(rng, 1, I, H), _proj(rng, 1, I, H), _proj(rng, 1, H, I))
+    for p in (g, u, dn):
+        p["codes"] = np.repeat(p["codes"], E, 0)
+        p["scales"] = np.repeat(p["scales"], E, 0)
+    x = rng.standard_normal((3, H)).astype(np.float32)
+    lg = rng.standard_normal((3, E)).astype(np.float32)
+    y, ids, w = vo.moe_layer(x, lg, g, u, dn, top_k=4)
+    Wg = vo.dequant(g["codes"][0], g["codebook"], g["scales"][0], 64).astype(np.float64)
+    Wu = vo.dequant(u["codes"][0], u["codebook"], u["scales"][0], 64).astype(np.float64)
+    Wd = vo.dequant(dn["codes"][0], dn["codebook"], dn["scales"][0], 64).astype(np.float64)
+    xs = x.astype(np.float64)
+    h = xs @ Wg.T
+    want = ((h / (1 + np.exp(-h))) * (xs @ Wu.T)) @ Wd.T
+    assert np.allclose(y, want, rtol=1e-10, atol=1e-12)
+
+
+def test_moe_layer_matches_pair_composition():
+    rng = np.random.default_rng(13)
+    E, H, I, k = 8, 128, 64, 3
+    g, u, dn = (_proj(rng, E, I, H), _proj(rng, E, I, H), _proj(rng, E, H, I))
+    sh = {"gate": _proj(rng, 1, I, H), "up": _proj(rng, 1, I, H), "down": _proj(rng, 1, H, I)}
+    sg = rng.standard_normal(H).astype(np.float32) * 0.1
+    x = rng.standard_normal((2, H)).astype(np.float32)
+    lg = rng.standard_normal((2, E)).astype(np.float32)
+    y, ids, w = vo.moe_layer(x, lg, g, u, dn, k, shared=sh, shared_gate=sg)
+    # independent composition through expert_gemv
+    eidx = ids.reshape(-1)
+    gy = vo.expert_gemv(x, eidx, g["codes"], g["codebook"], g["scales"], 64, xkrep=k)
+    uy = vo.expert_gemv(x, eidx, u["codes"], u["codebook"], u["scales"], 64, xkrep=k)
+    h = gy / (1 + np.exp(-gy)) * uy
+    dy = np.stack([vo.expert_gemv(h[n:n + 1], [eidx[n]], dn["codes"], dn["codebook"],
+                                  dn["scales"], 64)[0] for n in range(len(eidx))])
+    want = (dy.reshape(2, k, H) * w[:, :, None]).sum(1)
+    sgy = vo.expert_gemv(x, [0, 0], sh["gate"]["codes"], sh["gate"]["codebook"], sh["gate"]["scales"], 64)
+    suy = vo.expert_gemv(x, [0, 0], sh["up"]["codes"], sh["up"]["codebook"], sh["up"]["scales"], 64)
+    shh = sgy / (1 + np.exp(-sgy)) * suy
+    sdy = np.stack([vo.expert_gemv(shh[t:t + 1], [0], sh["down"]["codes"], sh["down"]["codebook"],
+                                   sh["down"]["scales"], 64)[0] for t in range(2)])
+    gate = 1 / (1 + np.exp(-(x.astype(np.float64) @ sg.astype(np.float64))))
+    want = want + gate[:, None] * sdy
+    # expert_gemv takes its activation in float32, so h is rounded once here
+    assert np.allclose(y, want, rtol=1e-5, atol=1e-7)
+
+
+# ------------------------------------------------------- tile metadata
+def test_tile_meta_vs_vectorized_form():
+    """The loop restatement vs the reference's vectorised construction
+    (vq_switch.py:4590-4610), over ragged routings."""
+    rng = np.random.default_rng(0)
+    for _ in range(100):
+        E = int(rng.integers(1, 65))
+        n = int(rng.integers(1, 2049))
+        rt = int(rng.choice([32, 64]))
+        idx = np.sort(rng.integers(0, E, n))
+        counts = np.bincount(idx, minlength=E)
+        touched = np.nonzero(counts)[0]
+        starts = np.zeros(E + 1, np.int64)
+        starts[1:] = np.cumsum(counts)
+        tc = counts[touched]
+        per = (tc + rt - 1) // rt
+        eids = np.repeat(touched, per)
+        cum = np.cumsum(per)
+        within = (np.arange(int(cum[-1])) - np.repeat(cum - per, per)) * rt
+        vec = np.stack([eids, starts[eids] + within,
+                        np.minimum(rt, counts[eids] - within)], 1).astype(np.int32)
+        assert np.array_equal(vo.tile_meta(idx, E, rt), vec)
+
+
+def test_sort_routing_inverse():
+    rng = np.random.default_rng(4)
+    idx = rng.integers(0, 16, (8, 4))
+    order, inv, src, srt = vo.sort_routing(idx, 4)
+    flat = idx.reshape(-1)
+    assert np.array_equal(flat[order], srt) and np.all(np.diff(srt) >= 0)
+    assert np.array_equal(srt[inv], flat)
+    assert np.array_equal(src, order // 4)
