@@ -1,0 +1,205 @@
+/* vqk.h -- C ABI of the MI355X (gfx950) VQ weight-decode library, libvqk.so.
+ *
+ * Plain pointers and sizes only. Device pointers are HIP device memory;
+ * `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ * Every entry point validates its arguments on the host and returns a status
+ * before anything is launched; no entry point allocates device memory --
+ * callers that need scratch pass a workspace sized by the matching
+ * *_workspace query. Kernels are re-entrant; the library keeps no mutable
+ * global state besides a per-thread error message.
+ *
+ * Each entry point cites the reference interface it replaces (paths are
+ * relative to the reference checkout; vq_switch.py, vq_dense.py and vq_pack.py
+ * live in src/vqlab/runtime/).
+ */
+#ifndef VQK_H
+#define VQK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: map 1:1 onto the reference's exceptions --------------
+ * VQK_ENOTIMPL  NotImplementedError: unsupported d / bits / geometry
+ *               (vq_switch.py:3106-3109, 3350-3362)
+ * VQK_EINVAL    ValueError: WPR / column / shape mismatch
+ *               (vq_switch.py:3124-3128, 3365-3368; vq_dense.py:330-331)
+ * VQK_ESHARDED  RuntimeError: codebook rows differ from the module's K
+ *               (vq_switch.py:5285-5296; vq_dense.py:349-353)
+ * VQK_EDEVICE   a HIP runtime call failed (launch, stream)
+ * VQK_ENOSPACE  the workspace passed is smaller than *_workspace reported */
+#define VQK_OK        0
+#define VQK_ENOTIMPL  1
+#define VQK_EINVAL    2
+#define VQK_ESHARDED  3
+#define VQK_EDEVICE   4
+#define VQK_ENOSPACE  5
+
+/* ---- element types ------------------------------------------------------ */
+#define VQK_F16   0
+#define VQK_BF16  1
+#define VQK_F32   2
+#define VQK_U8    3
+#define VQK_U16   4
+#define VQK_U32   5
+
+/* One VQ-coded linear, or a stack of E expert linears sharing one codebook
+ * (VQSwitchLinear, vq_switch.py:5198-5234; VQLinear, vq_dense.py:322-334).
+ *
+ *   codes      pack_bits == 0: VQK_U8 / VQK_U16 [E, OUT, NSUB], NSUB = IN / D
+ *              pack_bits  > 0: VQK_U32 [E, OUT, WPR] words, WPR =
+ *                              ceil(NSUB / 32) * pack_bits (vq_pack.py:11-27)
+ *              with row_table: compact live rows [n_live, NSUB or WPR]
+ *   code_cols  the codes tensor's last dimension as stored; it must equal
+ *              NSUB (unpacked) or WPR (packed), else VQK_EINVAL
+ *              (vq_switch.py:3124-3128)
+ *   codebook   fp16 [K, D], D in {2, 4, 8}; ONE per module, shared by all
+ *              experts (vq_switch.py:5-8)
+ *   scales     fp16 [E, OUT, IN / group] (compact [n_live, IN / group])
+ *   row_table  int32 [E, OUT]: compact row of (expert, row), -1 = dead row
+ *              (skipzero, vq_switch.py:5206-5214); NULL = expanded tensors
+ *   k_expect   the codebook row count the module was built with; a
+ *              different K is a sharded codebook (VQK_ESHARDED). 0 = K.
+ * A dense linear is E = 1. */
+typedef struct vqk_weights {
+    const void     *codes;
+    int64_t         code_cols;
+    int32_t         code_type;
+    int32_t         pack_bits;
+    const uint16_t *codebook;
+    int64_t         K;
+    int32_t         D;
+    int32_t         group;
+    const uint16_t *scales;
+    int64_t         E;
+    int64_t         OUT;
+    int64_t         IN;
+    const int32_t  *row_table;
+    int64_t         n_live;
+    int64_t         k_expect;
+} vqk_weights;
+
+/* Library identification and the calling thread's last error message. */
+const char *vqk_version(void);
+const char *vqk_last_error(void);
+
+/* ---- a1: widths ----------------------------------------------------------
+ * bits_for_k: vq_pack.py:34-38. words_per_row: vq_pack.py:41-45 (returns -1
+ * for bad arguments). pack_bits_for: codepack.py:22-30 (0 = stays unpacked). */
+int     vqk_bits_for_k(int64_t k, int32_t *bits);
+int64_t vqk_words_per_row(int64_t nsub, int32_t bits);
+int     vqk_pack_bits_for(int64_t k, int64_t nsub, int32_t pack_unaligned,
+                          int32_t *bits);
+
+/* ---- a2/a3: index packing (vq_pack.pack / vq_pack.unpack, vq_pack.py:48-97)
+ * rows = E * OUT flattened. Codes are uint16 on input (any width 1..16);
+ * unpack writes uint8 when bits <= 8 else uint16, like vq_pack.unpack.
+ * *_host work on host memory, the others launch on `stream`. */
+int vqk_pack_host(const uint16_t *codes, int64_t rows, int64_t nsub,
+                  int32_t bits, uint32_t *packed);
+int vqk_unpack_host(const uint32_t *packed, int64_t rows, int64_t nsub,
+                    int32_t bits, void *codes);
+int vqk_pack(const uint16_t *codes, int64_t rows, int64_t nsub, int32_t bits,
+             uint32_t *packed, void *stream);
+int vqk_unpack(const uint32_t *packed, int64_t rows, int64_t nsub,
+               int32_t bits, void *codes, void *stream);
+
+/* ---- a4: dequantisation, bit-exact W = fp16(f32(cb[c]) * f32(s)) ----------
+ * vqk_dequant: wdec_decode (vq_switch.py:3517-3544) -- rows [r0, r0 + rows)
+ *   of the flattened [E * OUT] module into out [rows, IN] fp16.
+ * vqk_dequant_experts: _decode_chunk (vq_switch.py:4725-4782) -- experts
+ *   eidx[0..ne) (device uint32) into out [ne, OUT, IN] fp16.
+ * Dead skipzero rows decode to +0. */
+int vqk_dequant(const vqk_weights *w, int64_t r0, int64_t rows,
+                uint16_t *out, void *stream);
+int vqk_dequant_experts(const vqk_weights *w, const uint32_t *eidx,
+                        int64_t ne, uint16_t *out, void *stream);
+
+/* ---- a10: dense fused GEMV, _dense_fused (vq_switch.py:3339-3434) ----------
+ * y[N, OUT] = x[N, IN] . W^T for E == 1, fp32 accumulation; x and y types in
+ * {VQK_F16, VQK_BF16, VQK_F32}. */
+int vqk_dense_gemv(const vqk_weights *w, const void *x, int32_t x_type,
+                   int64_t N, void *y, int32_t y_type, void *stream);
+
+/* ---- a5-a9: routed-expert fused GEMV, _fused (vq_switch.py:2919-3249) -------
+ * Pair n (n < N) multiplies token row n / xkrep of x [T, IN] with expert
+ * eidx[n] (device uint32): y[n, :] = x[n / xkrep] . W_eidx[n]^T. xkrep = 1
+ * is the historical contract (x already has N rows); xkrep = k is the XKREP
+ * form (vq_switch.py:4422-4451). Requires N == T * xkrep. */
+int vqk_moe_expert_gemv(const vqk_weights *w, const void *x, int32_t x_type,
+                        int64_t T, const uint32_t *eidx, int64_t N,
+                        int64_t xkrep, void *y, int32_t y_type, void *stream);
+
+/* ---- a12: routed-expert grouped GEMM, _gemmseg_prefill (vq_switch.py:4569-4722)
+ * Same contract and output order as vqk_moe_expert_gemv, for large N: the
+ * pairs are count-sorted by expert ON DEVICE (no host sync, replacing the
+ * host argsort at vq_switch.py:5383-5388 and the tile build at 4590-4610),
+ * each expert segment is dequantised tile by tile into LDS and multiplied on
+ * the bf16/fp16 matrix cores. */
+int vqk_grouped_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes);
+int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type,
+                     int64_t T, const uint32_t *eidx, int64_t N, int64_t xkrep,
+                     void *y, int32_t y_type, void *workspace, size_t ws_bytes,
+                     void *stream);
+
+/* ---- a11: dense large-N path, _decode_matmul (vq_dense.py:262-312) ---------
+ * y[N, OUT] = x[N, IN] . W^T for E == 1 with W dequantised tile by tile into
+ * LDS and fed to the matrix cores (no materialised fp16 weight). */
+int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type,
+                   int64_t N, void *y, int32_t y_type, void *stream);
+
+/* ---- a15: fused MoE decode layer (SwitchGLU + SparseMoeBlock routing) -------
+ * mlx-lm's SparseMoeBlock around VQSwitchLinear (restated in
+ * bench/decode_ladder.py:107-119 and tests/test_qwen3_5_parity.py:180-205):
+ *   ids, w = top_k(softmax(logits[t])), renormalised when norm_topk != 0
+ *   y[t] = sum_j w[t, j] * down_e(silu(gate_e(x_t)) * up_e(x_t))
+ *          + sigmoid(shared_gate_vec . x_t) * shared(x_t)      (if shared)
+ * Routing happens on device from `logits` [T, E] fp32; nothing syncs to the
+ * host. gate/up/down are the routed projections (E experts each; gate and up
+ * share one format); sh_* are the shared expert (E == 1, same formats), or
+ * NULL. topk_ids / topk_w (device, [T, top_k] int32 / fp32) receive the
+ * routing when non-NULL. */
+typedef struct vqk_moe_desc {
+    const vqk_weights *gate;
+    const vqk_weights *up;
+    const vqk_weights *down;
+    const vqk_weights *sh_gate;
+    const vqk_weights *sh_up;
+    const vqk_weights *sh_down;
+    const void        *sh_gate_vec;
+    int32_t            sh_gate_vec_type;
+    int32_t            top_k;
+    int32_t            norm_topk;
+} vqk_moe_desc;
+
+int vqk_moe_decode_layer_workspace(const vqk_moe_desc *m, int64_t T,
+                                   size_t *bytes);
+int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type,
+                         int64_t T, const float *logits, void *y,
+                         int32_t y_type, int32_t *topk_ids, float *topk_w,
+                         void *workspace, size_t ws_bytes, void *stream);
+
+/* ---- capability predicates (1 = this build has a kernel for the shape) -----
+ * dense_fits (vq_switch.py:3290-3306), wdec_fits (3505-3514),
+ * gemmseg_fits (4469-4507). Same arguments and meaning, answered for the
+ * gfx950 kernels of this library. */
+int vqk_dense_fits(int64_t K, int64_t IN, int32_t G, int32_t D);
+int vqk_wdec_fits(int32_t D, int64_t NSUB, int32_t G, int32_t pack_bits);
+int vqk_gemmseg_fits(int32_t D, int64_t K, int32_t G, int32_t pack_bits,
+                     int64_t IN);
+
+/* ---- a14: skipzero row table (skipzero_row_table, vq_switch.py:4958-4973) --
+ * rowmask uint8 [E, ceil(OUT / 8)] little bit order -> int32 [E, OUT],
+ * compact row of each live (expert, row), -1 = dead. Host memory, like the
+ * reference's CPU-stream build. Returns the live-row count in *n_live. */
+int vqk_skipzero_row_table_host(const uint8_t *rowmask, int64_t E,
+                                int64_t OUT, int32_t *table, int64_t *n_live);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VQK_H */

@@ -1,0 +1,144 @@
+"""The C ABI without a GPU: libvqk.so loads, exports every function
+include/vqk.h declares, and its host-side logic (widths, host pack/unpack,
+predicates, row table, argument validation) agrees with the oracle. Nothing
+here launches a kernel: every error path below is refused on the host."""
+import ctypes
+import pathlib
+import re
+
+import numpy as np
+import pytest
+
+from oracle import vq_oracle as vo
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+@pytest.fixture(scope="module")
+def L():
+    from vqlab_amd import _lib
+    return _lib
+
+
+def _declared():
+    txt = (ROOT / "include" / "vqk.h").read_text()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(vqk_\w+)\s*\(", txt)))
+
+
+def test_exports_every_declared_symbol(L):
+    lib = L.lib()
+    names = _declared()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(L.SIGNATURES), set(names) ^ set(L.SIGNATURES)
+
+
+def test_widths(L):
+    from vqlab_amd import vq_pack
+    for k in (2, 16, 256, 4096, 16384, 65536):
+        assert vq_pack.bits_for_k(k) == vo.bits_for_k(k)
+    with pytest.raises(AssertionError):
+        vq_pack.bits_for_k(3000)
+    for nsub, bits in ((512, 12), (128, 12), (512, 14), (128, 14), (80, 14), (640, 16)):
+        assert vq_pack.words_per_row(nsub, bits) == vo.words_per_row(nsub, bits)
+    b = ctypes.c_int32()
+    for k, nsub, un in ((256, 512, 0), (4096, 512, 0), (4096, 80, 0), (4096, 80, 1), (65536, 64, 0)):
+        assert L.lib().vqk_pack_bits_for(k, nsub, un, ctypes.byref(b)) == 0
+        assert b.value == vo.pack_bits_for(k, nsub, bool(un))
+
+
+@pytest.mark.parametrize("bits", list(range(1, 17)))
+def test_host_pack_unpack_vs_oracle(L, bits):
+    from vqlab_amd import vq_pack
+    rng = np.random.default_rng(bits)
+    for nsub in (32, 80, 96):
+        codes = rng.integers(0, 1 << bits, (2, 3, nsub)).astype(np.uint16)
+        p = vq_pack.pack(codes, bits)
+        assert np.array_equal(p, vo.pack(codes, bits))
+        u = vq_pack.unpack(p, nsub, bits)
+        assert u.dtype == (np.uint8 if bits <= 8 else np.uint16)
+        assert np.array_equal(u, codes)
+    with pytest.raises(AssertionError):
+        vq_pack.pack(np.full((1, 1, 32), 1 << bits, np.uint32), bits)
+
+
+def test_host_pack_matches_reference_golden(L):
+    from golden import writer_fixture as wf
+    from vqlab_amd import vq_pack
+    gold = wf.golden()["pack"]["tensors"]
+    for m, t in wf.vq_tensors().items():
+        assert wf.sha16(vq_pack.pack(t["codes"], 4)) == gold[m + ".codes"]["sha"]
+
+
+def test_row_table_host_vs_oracle(L):
+    from vqlab_amd import vq_switch as VS
+    rng = np.random.default_rng(2)
+    E, OUT = 7, 45
+    live = rng.random((E, OUT)) > 0.3
+    rm = np.packbits(live, axis=-1, bitorder="little")
+    t = VS.skipzero_row_table(rm, E, OUT).numpy()
+    assert np.array_equal(t, vo.skipzero_row_table(rm, E, OUT))
+
+
+def test_predicates(L):
+    from vqlab_amd import vq_switch as VS
+    assert VS.dense_fits(256, 4096, 64, 2) and VS.dense_fits(65536, 5120, 64, 8)
+    assert not VS.dense_fits(256, 4096, 64, 3)
+    assert not VS.dense_fits(256, 4096, 48, 8)      # 48 does not divide IN
+    assert not VS.dense_fits(256, 4096, 4, 8)       # a group smaller than one subvector
+    assert VS.wdec_fits(4, 512, 64, 12) and not VS.wdec_fits(3, 512, 64, 12)
+
+
+def _w(L, **kw):
+    w = L.VQKWeights()
+    w.codes, w.codebook, w.scales = 16, 16, 16       # never dereferenced: refused first
+    w.code_type, w.pack_bits, w.K, w.D, w.group = L.VQK_U32, 12, 4096, 4, 64
+    w.E, w.OUT, w.IN = 1, 8, 256
+    w.code_cols = vo.words_per_row(64, 12)
+    for k, v in kw.items():
+        setattr(w, k, v)
+    return w
+
+
+@pytest.mark.parametrize("kw,rc", [
+    ({"D": 3}, 1),                          # NotImplementedError: no kernel for d=3
+    ({"code_cols": 5}, 2),                  # ValueError: WPR mismatch
+    ({"k_expect": 2048}, 3),                # RuntimeError: sharded codebook
+    ({"pack_bits": 17}, 1),
+    ({"code_type": 3, "pack_bits": 0, "code_cols": 64}, 2),   # uint8 codes, K=4096
+    ({"group": 48}, 2),                     # 48 does not divide IN=256
+    ({"group": 6, "IN": 240, "code_cols": vo.words_per_row(60, 12)}, 1),  # G % D != 0
+])
+def test_validation_refuses_before_launch(L, kw, rc):
+    w = _w(L, **kw)
+    got = L.lib().vqk_dense_gemv(ctypes.byref(w), ctypes.c_void_p(16), L.VQK_BF16, 1,
+                                 ctypes.c_void_p(16), L.VQK_BF16, None)
+    assert got == rc, L.last_error()
+    assert L.last_error()
+
+
+def test_status_maps_to_reference_exceptions(L):
+    with pytest.raises(NotImplementedError):
+        L.check(L.VQK_ENOTIMPL)
+    with pytest.raises(ValueError):
+        L.check(L.VQK_EINVAL)
+    with pytest.raises(RuntimeError):
+        L.check(L.VQK_ESHARDED)
+
+
+def test_gemv_argument_errors(L):
+    w = _w(L)
+    lib = L.lib()
+    # N != T * xkrep
+    assert lib.vqk_moe_expert_gemv(ctypes.byref(w), ctypes.c_void_p(16), L.VQK_BF16, 2,
+                                   ctypes.c_void_p(16), 5, 2, ctypes.c_void_p(16), L.VQK_BF16,
+                                   None) == L.VQK_EINVAL
+    # bad activation type
+    assert lib.vqk_dense_gemv(ctypes.byref(w), ctypes.c_void_p(16), 7, 1, ctypes.c_void_p(16),
+                              L.VQK_BF16, None) == L.VQK_EINVAL
+    # dense takes E == 1
+    w2 = _w(L, E=2)
+    assert lib.vqk_dense_gemv(ctypes.byref(w2), ctypes.c_void_p(16), L.VQK_BF16, 1,
+                              ctypes.c_void_p(16), L.VQK_BF16, None) == L.VQK_EINVAL

@@ -1,0 +1,241 @@
+"""Parity of the HIP kernels with the CPU oracle, through the C ABI.
+
+Bit-exact: unpack, pack, dequantised weights (uint16 patterns). Tolerance
+(rtol 2e-2, atol 1e-3 against the float64 decode-then-matmul oracle, the
+north star's bar): the fused GEMVs. Shapes are the BASELINE.json configs'
+row shapes (fewer experts where the expert count does not change what a
+kernel computes), plus ragged / unaligned / skipzero / dtype edge cases.
+"""
+import numpy as np
+import pytest
+
+from oracle import vq_oracle as vo
+from vq_cases import assert_close, make_module, skipzero, to_device
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _u16(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+# ------------------------------------------------------------ pack / unpack
+@pytest.mark.parametrize("bits", list(range(1, 17)))
+def test_unpack_pack_device(bits):
+    from vqlab_amd import vq_pack
+    rng = np.random.default_rng(100 + bits)
+    for nsub in (32, 80, 512):
+        print(f"unpack/pack bits={bits} nsub={nsub}", flush=True)
+        codes = rng.integers(0, 1 << bits, (3, 5, nsub)).astype(np.uint16)
+        packed = vo.pack(codes, bits)
+        dp = torch.from_numpy(packed.view(np.int32)).cuda()
+        got = vq_pack.unpack(dp, nsub, bits)
+        torch.cuda.synchronize()
+        g = got.cpu().numpy()
+        g = g.view(np.uint16) if bits > 8 else g
+        assert np.array_equal(g, codes)
+        dc = torch.from_numpy(codes.view(np.int16)).cuda()
+        rp = vq_pack.pack(dc, bits)
+        assert np.array_equal(rp.cpu().numpy().view(np.uint32), packed)
+
+
+def test_device_pack_matches_reference_golden():
+    from golden import writer_fixture as wf
+    from vqlab_amd import vq_pack
+    gold = wf.golden()["pack"]["tensors"]
+    for m, t in wf.vq_tensors().items():
+        dc = torch.from_numpy(t["codes"].astype(np.int16)).cuda()
+        got = vq_pack.pack(dc, 4).cpu().numpy().view(np.uint32)
+        assert wf.sha16(got) == gold[m + ".codes"]["sha"], m
+
+
+# ----------------------------------------------------------------- dequant
+@pytest.mark.parametrize("D", [2, 4, 8])
+@pytest.mark.parametrize("K,packed", [(16, True), (256, False), (512, True), (4096, True),
+                                      (16384, True), (65536, False), (1000, False)])
+def test_wdec_bit_exact(D, K, packed):
+    from vqlab_amd import vq_switch as VS
+    print(f"wdec D={D} K={K} packed={packed}", flush=True)
+    rng = np.random.default_rng(D * 7 + K)
+    m = make_module(rng, 2, 24, 256, D, K, packed=packed and K & (K - 1) == 0)
+    # special values: subnormal and negative-zero codebook rows, inf / nan / zero scales
+    m["codebook"][0] = np.float16(2.0 ** -20)
+    m["codebook"][1] = -0.0
+    m["scales"][0, 0, 0] = np.inf
+    m["scales"][0, 1, 1] = np.nan
+    m["scales"][1, 2, :] = 0
+    m["codes"][0, :3, :3] = [0, 1, 0]
+    if m["pack_bits"]:
+        m["stored"] = vo.pack(m["codes"], m["pack_bits"])
+    else:
+        m["stored"] = m["codes"].astype(np.uint8) if K <= 256 else m["codes"]
+    codes, cb, sc = to_device(m)
+    want = vo.dequant(m["codes"].reshape(48, -1), m["codebook"], m["scales"].reshape(48, -1), 64)
+    got = VS.wdec_decode(codes, cb, sc, 48, 256, 64, m["pack_bits"])
+    g, w = _u16(got), want.view(np.uint16)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got.float().cpu().numpy()), nan)
+    assert np.array_equal(g[~nan], w[~nan])
+    # a row slice: rows [r0, r0 + 10)
+    part = VS.wdec_decode(codes, cb, sc, 10, 256, 64, m["pack_bits"], r0=30)
+    assert np.array_equal(_u16(part), w[30:40])
+
+
+def test_decode_chunk_experts_and_skipzero():
+    from vqlab_amd import vq_switch as VS
+    rng = np.random.default_rng(5)
+    m = make_module(rng, 6, 40, 512, 4, 4096, dead_frac=0.2)
+    codes, cb, sc = to_device(m)
+    eidx = torch.tensor([5, 0, 3, 3], dtype=torch.int32, device="cuda")
+    got = VS._decode_chunk(codes, cb, sc, eidx, pack_bits=12, in_features=512)
+    for i, e in enumerate([5, 0, 3, 3]):
+        want = vo.dequant(m["codes"][e], m["codebook"], m["scales"][e], 64)
+        assert np.array_equal(_u16(got[i]), want.view(np.uint16))
+    sz, rt = skipzero(m)
+    zc = torch.from_numpy(sz["sz_codes"].view(np.int32)).cuda()
+    zs = torch.from_numpy(sz["sz_scales"]).cuda()
+    rtd = torch.from_numpy(rt).cuda()
+    got2 = VS._decode_chunk(zc, cb, zs, eidx, pack_bits=12, in_features=512, rowtbl=rtd)
+    # live rows: byte for byte. Dead rows: +0 from the compact form; the
+    # expanded form decodes fp16(0 * cb[0]), which is -0 where cb[0] < 0.
+    live = (rt[[5, 0, 3, 3]] >= 0)
+    assert np.array_equal(_u16(got2)[live], _u16(got)[live])
+    assert (_u16(got2)[~live] == 0).all()
+    assert (got[torch.from_numpy(~live).cuda()] == 0).all()
+
+
+# -------------------------------------------------------------- dense GEMV
+def _dense_case(rng, OUT, IN, D, K, G=64, packed=False, xdt=torch.bfloat16, N=1):
+    m = make_module(rng, 1, OUT, IN, D, K, G=G, packed=packed)
+    codes, cb, sc = to_device(m)
+    x = torch.from_numpy(rng.standard_normal((N, IN)).astype(np.float32)).to("cuda", xdt)
+    return m, codes[0], cb, sc[0], x
+
+
+@pytest.mark.parametrize("case", [
+    # (OUT, IN, D, K, G, packed): c1 is the first row
+    (4096, 4096, 2, 256, 64, False),
+    (512, 2048, 4, 4096, 64, True),
+    (1024, 4096, 8, 16384, 64, True),
+    (300, 1024, 8, 4096, 64, True),      # d8 K4096: 64 KB codebook table in LDS
+    (96, 640, 8, 65536, 64, False),      # uint16 codes, NSUB 80: generic kernel
+    (128, 512, 2, 512, 128, True),       # a group spans two blocks
+    (64, 1024, 4, 256, 1024, False),     # one scale per row (G = IN)
+    (70, 256, 4, 1000, 32, False),       # G=32 -> generic kernel, K not a power of 2
+])
+def test_dense_gemv(case):
+    from vqlab_amd import vq_switch as VS
+    OUT, IN, D, K, G, packed = case
+    print(f"dense gemv {case}", flush=True)
+    rng = np.random.default_rng(OUT + IN + D)
+    m, codes, cb, sc, x = _dense_case(rng, OUT, IN, D, K, G, packed)
+    y = VS._dense_fused(x, codes, cb, sc, pack_bits=m["pack_bits"], in_features=IN)
+    assert y.dtype == x.dtype and y.shape == (1, OUT)
+    w = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], G)
+    ref = vo.decode_matmul(x.float().cpu().numpy(), w)
+    assert_close(_np(y), ref, what=f"dense {case}")
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.float32])
+def test_dense_gemv_dtypes_and_batch(xdt):
+    from vqlab_amd import vq_switch as VS
+    rng = np.random.default_rng(3)
+    m, codes, cb, sc, x = _dense_case(rng, 256, 2048, 4, 4096, packed=True, xdt=xdt, N=5)
+    y = VS._dense_fused(x, codes, cb, sc, pack_bits=12, in_features=2048)
+    assert y.dtype == xdt
+    w = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], 64)
+    assert_close(_np(y), vo.decode_matmul(x.float().cpu().numpy(), w), what=str(xdt))
+
+
+# ------------------------------------------------------------ expert GEMV
+@pytest.mark.parametrize("shape", [
+    # (E, OUT, IN, D, K): c2 gate/up, c2 down, c3 gate/up, c3 down
+    (16, 512, 2048, 4, 4096),
+    (16, 2048, 512, 4, 4096),
+    (12, 1024, 4096, 8, 16384),
+    (12, 4096, 1024, 8, 16384),
+])
+def test_expert_gemv_baseline_shapes(shape):
+    from vqlab_amd import vq_switch as VS
+    E, OUT, IN, D, K = shape
+    print(f"expert gemv {shape}", flush=True)
+    rng = np.random.default_rng(sum(shape))
+    m = make_module(rng, E, OUT, IN, D, K)
+    codes, cb, sc = to_device(m)
+    T, k = 2, 5
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).reshape(-1)
+    x = torch.from_numpy(rng.standard_normal((T, IN)).astype(np.float32)).to("cuda", torch.bfloat16)
+    eidx = torch.from_numpy(ids.astype(np.int32)).cuda()
+    y = VS._fused(x, eidx, codes, cb, sc, pack_bits=m["pack_bits"], xkrep=k)
+    ref = vo.expert_gemv(x.float().cpu().numpy(), ids, m["codes"], m["codebook"], m["scales"],
+                         64, xkrep=k)
+    assert_close(_np(y), ref, what=f"expert {shape}")
+    # the historical contract (one x row per pair) computes the same bits
+    xr = x.repeat_interleave(k, 0)
+    y1 = VS._fused(xr, eidx, codes, cb, sc, pack_bits=m["pack_bits"])
+    assert torch.equal(y1, y)
+
+
+def test_expert_gemv_skipzero_equals_expanded():
+    from vqlab_amd import vq_switch as VS
+    rng = np.random.default_rng(9)
+    m = make_module(rng, 8, 1024, 4096, 8, 16384, dead_frac=0.2)
+    codes, cb, sc = to_device(m)
+    sz, rt = skipzero(m)
+    zc = torch.from_numpy(sz["sz_codes"].view(np.int32)).cuda()
+    zs = torch.from_numpy(sz["sz_scales"]).cuda()
+    rtd = torch.from_numpy(rt).cuda()
+    ids = np.array([3, 7, 0, 3], np.int32)
+    x = torch.from_numpy(rng.standard_normal((1, 4096)).astype(np.float32)).to("cuda", torch.bfloat16)
+    e = torch.from_numpy(ids).cuda()
+    ye = VS._fused(x, e, codes, cb, sc, pack_bits=14, xkrep=4)
+    yc = VS._fused(x, e, zc, cb, zs, pack_bits=14, xkrep=4, rowtbl=rtd)
+    assert torch.equal(ye, yc)
+    dead = rt[ids] < 0
+    assert (yc.float().cpu().numpy()[dead] == 0).all() and dead.any()
+    ref = vo.expert_gemv(x.float().cpu().numpy(), ids, m["codes"], m["codebook"], m["scales"], 64,
+                         xkrep=4)
+    assert_close(_np(yc), ref, what="skipzero")
+
+
+def test_expert_gemv_unpacked_and_bad_ids():
+    from vqlab_amd import vq_switch as VS
+    rng = np.random.default_rng(11)
+    m = make_module(rng, 4, 256, 1024, 4, 256, packed=False)
+    codes, cb, sc = to_device(m)
+    x = torch.from_numpy(rng.standard_normal((3, 1024)).astype(np.float32)).to("cuda", torch.float16)
+    ids = np.array([1, 3, 9], np.int32)            # 9 is outside [0, E): zeros, no fault
+    y = VS._fused(x, torch.from_numpy(ids).cuda(), codes, cb, sc)
+    ref = vo.expert_gemv(x.float().cpu().numpy(), ids[:2], m["codes"], m["codebook"],
+                         m["scales"], 64)
+    assert_close(_np(y[:2]), ref, what="u8 d4")
+    assert (y[2] == 0).all()
+
+
+def test_switch_linear_module_and_errors():
+    from vqlab_amd import vq_switch as VS
+    rng = np.random.default_rng(12)
+    m = make_module(rng, 8, 512, 2048, 4, 4096)
+    codes, cb, sc = to_device(m)
+    mod = VS.VQSwitchLinear(codes, cb, sc, pack_bits=12, in_features=2048)
+    assert (mod.input_dims, mod.output_dims, mod.num_experts) == (2048, 512, 8)
+    x = torch.from_numpy(rng.standard_normal((1, 1, 2048)).astype(np.float32)).to("cuda", torch.bfloat16)
+    idx = torch.tensor([[[1, 4, 6, 2]]], dtype=torch.int32, device="cuda")
+    y = mod(x[:, :, None, None, :], idx)
+    assert y.shape == (1, 1, 4, 1, 512) and y.dtype == torch.bfloat16
+    ref = vo.expert_gemv(x.float().cpu().numpy().reshape(1, -1), [1, 4, 6, 2], m["codes"],
+                         m["codebook"], m["scales"], 64, xkrep=4)
+    assert_close(_np(y).reshape(4, 512), ref, what="module")
+    mod.codebook = cb[:2048]
+    with pytest.raises(RuntimeError, match="sharded"):
+        mod(x[:, :, None, None, :], idx)
+    with pytest.raises(ValueError):
+        VS._fused(x.reshape(1, -1), idx.reshape(-1), codes[:, :, :100], cb, sc, pack_bits=12)
+    with pytest.raises(ValueError):
+        VS.VQSwitchLinear(codes, cb, sc, pack_bits=12)

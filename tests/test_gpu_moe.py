@@ -1,0 +1,103 @@
+"""Fused MoE decode layer (routing + SwitchGLU + combine) against the oracle.
+
+Routing must select exactly the oracle's experts (continuous logits: no
+ties); weights agree to fp32 rounding; outputs are within rtol 2e-2 /
+atol 1e-3 of the float64 oracle with the SwiGLU intermediate rounded to
+fp16, the activation dtype down_proj receives.
+"""
+import numpy as np
+import pytest
+
+from oracle import vq_oracle as vo
+from vq_cases import assert_close, make_module, to_device
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _spec(m):
+    return {"codes": m["codes"], "codebook": m["codebook"], "scales": m["scales"], "group": 64}
+
+
+def _block(rng, E, H, I, D, K, k, shared=False, norm=True):
+    from vqlab_amd import moe
+    projs = {n: make_module(rng, E, o, i, D, K) for n, (o, i) in
+             (("gate", (I, H)), ("up", (I, H)), ("down", (H, I)))}
+    sh = shv = None
+    if shared:
+        sh = {n: make_module(rng, 1, o, i, D, K) for n, (o, i) in
+              (("gate", (I, H)), ("up", (I, H)), ("down", (H, I)))}
+        shv = (rng.standard_normal(H) * 0.02).astype(np.float32)
+    dev = lambda ms: {n: to_device(m) + (m["pack_bits"],) for n, m in ms.items()}
+    blk = moe.VQSparseMoeBlock.from_modules(
+        dev(projs), top_k=k, in_features={"gate": H, "up": H, "down": I},
+        shared=dev(sh) if shared else None,
+        shared_gate=torch.from_numpy(shv).to("cuda", torch.bfloat16) if shared else None,
+        norm_topk_prob=norm)
+    return blk, projs, sh, shv
+
+
+def _check(blk, projs, sh, shv, rng, T, E, H, k, norm=True):
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to("cuda", torch.bfloat16)
+    lg = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).cuda()
+    y, ids, w = blk.fused(x, lg, return_route=True)
+    torch.cuda.synchronize()
+    shared = None
+    sgv = None
+    if sh is not None:
+        shared = {n: _spec(m) for n, m in sh.items()}
+        sgv = torch.from_numpy(shv).to(torch.bfloat16).float().numpy()
+    ref, rids, rw = vo.moe_layer(x.float().cpu().numpy(), lg.cpu().numpy(), _spec(projs["gate"]),
+                                 _spec(projs["up"]), _spec(projs["down"]), k, norm=norm,
+                                 shared=shared, shared_gate=sgv, h_round=np.float16)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-6)
+    assert_close(y.float().cpu().numpy(), ref, what=f"moe T={T}")
+    # the composed path (per-projection kernels + torch routing) agrees
+    yc = blk.composed(x, lg)
+    assert_close(yc.float().cpu().numpy(), ref, what=f"composed T={T}")
+    return y
+
+
+def test_moe_layer_c2_shape():
+    """Qwen3.6-35B-A3B-shaped layer: H 2048, 256 experts of I 512, top-8,
+    d4 K4096 12-bit packed."""
+    print("moe c2 shape", flush=True)
+    rng = np.random.default_rng(2)
+    blk, projs, sh, shv = _block(rng, 256, 2048, 512, 4, 4096, 8)
+    _check(blk, projs, sh, shv, rng, 1, 256, 2048, 8)
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_moe_layer_c3_shape_shared(T):
+    """Qwen3.5-397B-A17B row shapes: H 4096, I 1024, d8 K16384 14-bit,
+    top-10 + a shared expert (64 experts instead of 512)."""
+    print(f"moe c3 shape T={T}", flush=True)
+    rng = np.random.default_rng(3 + T)
+    blk, projs, sh, shv = _block(rng, 64, 4096, 1024, 8, 16384, 10, shared=True)
+    _check(blk, projs, sh, shv, rng, T, 64, 4096, 10)
+
+
+def test_moe_layer_unnormalised_d2():
+    print("moe d2 norm=False", flush=True)
+    rng = np.random.default_rng(4)
+    blk, projs, sh, shv = _block(rng, 32, 1024, 256, 2, 512, 4, norm=False)
+    _check(blk, projs, sh, shv, rng, 2, 32, 1024, 4, norm=False)
+
+
+def test_moe_layer_workspace_too_small():
+    import ctypes
+    from vqlab_amd import _lib as L, _torch as Tt
+    rng = np.random.default_rng(5)
+    blk, *_ = _block(rng, 8, 256, 128, 4, 256, 2)
+    keep = []
+    d = blk._fused_desc(keep)
+    x = torch.zeros((1, 256), dtype=torch.bfloat16, device="cuda")
+    lg = torch.zeros((1, 8), dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    ws = torch.empty(16, dtype=torch.uint8, device="cuda")
+    rc = L.lib().vqk_moe_decode_layer(ctypes.byref(d), Tt.ptr(x), L.VQK_BF16, 1, Tt.ptr(lg),
+                                      Tt.ptr(y), L.VQK_BF16, None, None, Tt.ptr(ws), 16,
+                                      Tt.stream())
+    assert rc == L.VQK_ENOSPACE

@@ -1,0 +1,63 @@
+"""Seeded synthetic VQ modules for the parity tests (numpy side; the oracle
+consumes the unpacked codes, the kernels the stored form)."""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import vq_oracle as vo
+
+
+def make_module(rng, E, OUT, IN, D, K, G=64, packed=True, dead_frac=0.0, cb_std=0.02):
+    """Codes uniform in [0, K), codebook ~N(0, cb_std) fp16, scales ~U(0.5,1.5)
+    fp16 (BASELINE.json config conventions). packed=True stores log2(K)-bit
+    words (any width); False stores uint8 (K <= 256) or uint16. dead_frac
+    zeroes whole rows' scales (skipzero dead rows)."""
+    nsub = IN // D
+    codes = rng.integers(0, K, (E, OUT, nsub)).astype(np.uint16)
+    cb = (rng.standard_normal((K, D)) * cb_std).astype(np.float16)
+    sc = rng.uniform(0.5, 1.5, (E, OUT, IN // G)).astype(np.float16)
+    if dead_frac:
+        dead = rng.random((E, OUT)) < dead_frac
+        sc[dead] = 0
+        codes[dead] = 0
+    if packed:
+        bits = vo.bits_for_k(K) if K > 1 else 1
+        stored = vo.pack(codes, bits)
+        pack_bits = bits
+    else:
+        stored = codes.astype(np.uint8) if K <= 256 else codes
+        pack_bits = 0
+    return {"codes": codes, "stored": stored, "codebook": cb, "scales": sc, "pack_bits": pack_bits,
+            "group": G, "E": E, "OUT": OUT, "IN": IN, "D": D, "K": K}
+
+
+def to_device(m, dev="cuda"):
+    import torch
+    st = m["stored"]
+    if st.dtype == np.uint32:
+        codes = torch.from_numpy(st.view(np.int32)).to(dev)
+    elif st.dtype == np.uint16:
+        codes = torch.from_numpy(st.view(np.int16)).to(dev)
+    else:
+        codes = torch.from_numpy(st).to(dev)
+    cb = torch.from_numpy(m["codebook"]).to(dev)
+    sc = torch.from_numpy(m["scales"]).to(dev)
+    return codes, cb, sc
+
+
+def skipzero(m):
+    """Compact form of m (dead rows dropped) + its row table."""
+    sz = vo.skipzero_compact(m["stored"], m["scales"])
+    rt = vo.skipzero_row_table(sz["sz_rowmask"], m["E"], m["OUT"])
+    return sz, rt
+
+
+def assert_close(y, ref, rtol=2e-2, atol=1e-3, what=""):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert y.shape == ref.shape, (y.shape, ref.shape)
+    bad = ~np.isclose(y, ref, rtol=rtol, atol=atol)
+    if bad.any():
+        i = np.argwhere(bad)[0]
+        raise AssertionError(f"{what}: {bad.sum()} of {bad.size} outside rtol={rtol} "
+                             f"atol={atol}; first at {tuple(i)}: {y[tuple(i)]} vs {ref[tuple(i)]}")

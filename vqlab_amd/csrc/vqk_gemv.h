@@ -1,0 +1,293 @@
+// Fused VQ GEMV kernels: y[n, r] = sum_i x[n / xkrep, i] * W_e(n)[r, i], with
+// W decoded on the fly from packed indices, codebook and per-group scales.
+//
+// Serves the decode regime of VQSwitchLinear (_fused, vq_switch.py:2919-3249,
+// kernels such as the d4 device-codebook walk 925-990 and the d8 simd kernels
+// 1424-1660) and VQLinear (_dense_fused, 3339-3434). Arithmetic per row, as in
+// the reference: x is narrowed to fp16 (vq_switch.py:5306-5308; devx kernels
+// 2371-2441), each code's subvector dot <cb[c], x> is accumulated in fp32 per
+// scale group, and the group sum is scaled by its fp16 scale into an fp32
+// accumulator (vq_switch.py:958-985). Summation order differs from the
+// reference's serial walk (lane partials are added by a butterfly), which the
+// output tolerance covers.
+//
+// Fast kernel layout (gfx950, wave64):
+//   * one lane owns one 32-code packing block of a row: it loads the block's
+//     BITS words (plus its scales) and decodes the 32 codes with shifts fixed
+//     at compile time (BITS is a template parameter);
+//   * LPR = next_pow2(NB) lanes cover a row, 64 / LPR rows per wave step;
+//     a lane keeps the same block index for every row it visits, so its slice
+//     of x (32*D fp16 values) is read from LDS once into registers;
+//   * the codebook is staged into LDS as a 2^BITS-entry table when that fits
+//     kCbLdsMax, otherwise gathered from L2 / MALL (codes clamped to K-1);
+//   * each wave issues the loads of its next row step before it decodes the
+//     current one.
+// Shapes outside the fast kernel's reach (ragged NSUB, rows not word
+// aligned, NB > 64, unusual scale groups) run on the generic kernel: one
+// thread per row, walking its codes.
+#pragma once
+
+#include "vqk_common.h"
+
+namespace vqk {
+
+struct GemvParams {
+    const void *codes;         // code rows (u32 words when packed)
+    int64_t row_words;         // fast path: u32 words per code row
+    int64_t code_cols;         // generic path: row stride in code units (words if packed)
+    int32_t bits;              // packed width; 0 = unpacked (code_bytes 1 or 2)
+    int32_t code_bytes;
+    const uint16_t *codebook;  // fp16 [K, D]
+    int32_t K;
+    const uint16_t *scales;    // fp16, ngrp per code row
+    int32_t ngrp, bpg, G;
+    const int32_t *row_table;  // [E, OUT] or NULL
+    int64_t stored_rows;       // code rows present (bound for device indices)
+    const uint32_t *eidx;      // [N] expert per pair, NULL = expert 0
+    int32_t E, OUT, IN, NSUB, NB;
+    int32_t lpr_log2;          // lanes per row = 1 << lpr_log2
+    const void *x;
+    int32_t x_type;
+    int64_t x_stride;          // elements between token rows
+    int32_t pair0, xkrep;      // pair = pair0 + blockIdx.y, token = pair / xkrep
+    void *y;
+    int32_t y_type;
+    int64_t y_stride;          // elements between pair rows of y
+    int32_t rows_per_wg, steps;
+};
+
+// ---------------------------------------------------------------- helpers
+template <int D>
+__device__ __forceinline__ float dot_entry(const h2 *cb, uint32_t c, const h2 *x, float acc) {
+    if constexpr (D == 2) {
+        return __builtin_amdgcn_fdot2(cb[c], x[0], acc, false);
+    } else if constexpr (D == 4) {
+        const h4 e = reinterpret_cast<const h4 *>(cb)[c];
+        acc = __builtin_amdgcn_fdot2(h2{e[0], e[1]}, x[0], acc, false);
+        return __builtin_amdgcn_fdot2(h2{e[2], e[3]}, x[1], acc, false);
+    } else {
+        const h8 e = reinterpret_cast<const h8 *>(cb)[c];
+        acc = __builtin_amdgcn_fdot2(h2{e[0], e[1]}, x[0], acc, false);
+        acc = __builtin_amdgcn_fdot2(h2{e[2], e[3]}, x[1], acc, false);
+        acc = __builtin_amdgcn_fdot2(h2{e[4], e[5]}, x[2], acc, false);
+        return __builtin_amdgcn_fdot2(h2{e[6], e[7]}, x[3], acc, false);
+    }
+}
+
+// Field i (compile-time after unrolling) of a 32-code block held in registers.
+template <int BITS>
+__device__ __forceinline__ uint32_t block_field(const uint32_t (&w)[BITS], int i) {
+    constexpr uint32_t MASK = (1u << BITS) - 1u;
+    const int bit = i * BITS, wi = bit >> 5, sh = bit & 31;
+    if (sh + BITS <= 32) return (w[wi] >> sh) & MASK;
+    return __builtin_amdgcn_alignbit(w[wi + 1 < BITS ? wi + 1 : BITS - 1], w[wi], sh) & MASK;
+}
+
+// sum_g s[g] * sum_{codes i of group g} <cb[c_i], x_i> over one block.
+template <int D, int BITS, int GPB, bool CBL>
+__device__ __forceinline__ float block_dot(const uint32_t (&w)[BITS], const h2 (&xr)[16 * D],
+                                           const float (&s)[GPB], const h2 *cb, uint32_t kmax) {
+    constexpr int CPG = kBlock / GPB;
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < GPB; ++g) {
+        float ga = 0.f;
+#pragma unroll
+        for (int q = 0; q < CPG; ++q) {
+            const int i = g * CPG + q;
+            uint32_t c = block_field<BITS>(w, i);
+            if (!CBL) c = min(c, kmax);
+            ga = dot_entry<D>(cb, c, &xr[i * (D / 2)], ga);
+        }
+        acc = fmaf(s[g], ga, acc);
+    }
+    return acc;
+}
+
+template <int BITS, int GPB>
+__device__ __forceinline__ void load_block(const GemvParams &p, int64_t cr, int blk, int sidx,
+                                           uint32_t (&w)[BITS], float (&s)[GPB]) {
+    if (cr >= 0) {
+        const uint32_t *src = static_cast<const uint32_t *>(p.codes) + cr * p.row_words +
+                              int64_t(blk) * BITS;
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) w[i] = __builtin_nontemporal_load(src + i);
+        const uint16_t *sr = p.scales + cr * p.ngrp + sidx;
+#pragma unroll
+        for (int g = 0; g < GPB; ++g) s[g] = h_to_f32(__builtin_nontemporal_load(sr + g));
+    } else {
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) w[i] = 0u;
+#pragma unroll
+        for (int g = 0; g < GPB; ++g) s[g] = 0.f;
+    }
+}
+
+// Codebook -> LDS table of `entries` (>= K) rows of D halves, zero beyond K.
+template <int D>
+__device__ __forceinline__ void stage_codebook(const uint16_t *cb, int K, int entries, h2 *dst) {
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(cb);
+    uint32_t *d = reinterpret_cast<uint32_t *>(dst);
+    const int valid = K * (D / 2), total = entries * (D / 2);
+    for (int i = threadIdx.x; i < total; i += blockDim.x) d[i] = i < valid ? src[i] : 0u;
+}
+
+// One activation row -> fp16 in LDS, blocks of 32*D values at a padded stride.
+template <int XH, int XS>
+__device__ __forceinline__ void stage_x(const void *x, int32_t type, int64_t base, int IN, int NB,
+                                        f16 *xs) {
+    for (int i = threadIdx.x; i < NB * XH; i += blockDim.x) {
+        const float v = i < IN ? load_act(x, type, base + i) : 0.f;
+        xs[(i / XH) * XS + (i % XH)] = f16(v);
+    }
+}
+
+// The lane's 32*D staged activations -> 16*D half2 registers. Read as plain
+// 32-bit words (the compiler merges them into 128-bit LDS reads):
+// bit-casting elements of a u32x4 value miscompiled, every element read as
+// element 0.
+template <int D>
+__device__ __forceinline__ void load_xregs(const f16 *src, h2 (&xr)[16 * D]) {
+    const uint32_t *s = reinterpret_cast<const uint32_t *>(src);
+#pragma unroll
+    for (int j = 0; j < 16 * D; ++j) xr[j] = __builtin_bit_cast(h2, s[j]);
+}
+
+// ------------------------------------------------------------ fast kernel
+template <int D, int BITS, int GPB>
+__global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
+    constexpr bool CBL = cb_in_lds(D, BITS);
+    constexpr int CBN = CBL ? (1 << BITS) : 0;   // LDS table entries
+    constexpr int XH = kBlock * D;               // x halves per block
+    constexpr int XS = XH + 8;                   // padded LDS stride: 16 B skew per block
+    extern __shared__ __align__(16) uint8_t smem[];
+    h2 *cb_lds = reinterpret_cast<h2 *>(smem);
+    f16 *xs = reinterpret_cast<f16 *>(smem + CBN * D * 2);
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int lpr = 1 << p.lpr_log2, rpw = kWave >> p.lpr_log2;
+    const int sub = lane >> p.lpr_log2, blk = lane & (lpr - 1);
+    const bool on = blk < p.NB;
+    const int pair = p.pair0 + int(blockIdx.y);
+    const int tok = pair / p.xkrep;
+    const uint32_t e = p.eidx ? p.eidx[pair] : 0u;
+    const bool e_ok = e < uint32_t(p.E);
+    const int r_wg = int(blockIdx.x) * p.rows_per_wg;
+    const int sidx = GPB == 1 ? blk / p.bpg : blk * GPB;
+
+    auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * rpw + sub; };
+    auto code_row = [&](int st) -> int64_t {
+        const int r = row_at(st);
+        if (!on || !e_ok || r >= p.OUT) return -1;
+        int64_t f = int64_t(e) * p.OUT + r;
+        if (p.row_table) f = p.row_table[f];
+        return f < p.stored_rows ? f : -1;
+    };
+
+    uint32_t w[BITS];
+    float s[GPB];
+    int64_t cr = code_row(0);
+    load_block<BITS, GPB>(p, cr, blk, sidx, w, s);   // in flight during staging
+
+    if constexpr (CBL) stage_codebook<D>(p.codebook, p.K, CBN, cb_lds);
+    stage_x<XH, XS>(p.x, p.x_type, int64_t(tok) * p.x_stride, p.IN, p.NB, xs);
+    __syncthreads();
+
+    h2 xr[16 * D];
+    load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
+    const h2 *cb = CBL ? cb_lds : reinterpret_cast<const h2 *>(p.codebook);
+    const uint32_t kmax = uint32_t(p.K - 1);
+
+    for (int st = 0; st < p.steps; ++st) {
+        uint32_t wn[BITS];
+        float sn[GPB];
+        const int64_t crn = st + 1 < p.steps ? code_row(st + 1) : -1;
+        load_block<BITS, GPB>(p, crn, blk, sidx, wn, sn);
+        float v = 0.f;
+        if (cr >= 0) v = block_dot<D, BITS, GPB, CBL>(w, xr, s, cb, kmax);
+        v = group_sum(v, lpr);
+        const int r = row_at(st);
+        if (blk == 0 && r < p.OUT) store_act(p.y, p.y_type, int64_t(pair) * p.y_stride + r, v);
+        cr = crn;
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) w[i] = wn[i];
+#pragma unroll
+        for (int g = 0; g < GPB; ++g) s[g] = sn[g];
+    }
+}
+
+// --------------------------------------------------------- generic kernel
+__device__ __forceinline__ uint32_t generic_code(const GemvParams &p, int64_t cr, int j) {
+    if (p.bits) {
+        const uint32_t *row = static_cast<const uint32_t *>(p.codes) + cr * p.code_cols;
+        const int64_t bit = int64_t(j >> 5) * (int64_t(kBlock) * p.bits) + (j & 31) * p.bits;
+        const int sh = int(bit & 31);
+        uint32_t v = row[bit >> 5] >> sh;
+        if (sh + p.bits > 32) v |= row[(bit >> 5) + 1] << (32 - sh);
+        return v & ((1u << p.bits) - 1u);
+    }
+    if (p.code_bytes == 1) return static_cast<const uint8_t *>(p.codes)[cr * p.code_cols + j];
+    return static_cast<const uint16_t *>(p.codes)[cr * p.code_cols + j];
+}
+
+// One thread per (pair, row); x row staged once per workgroup as plain fp16.
+template <int D>
+__global__ void __launch_bounds__(kThreads) k_gemv_generic(const GemvParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    f16 *xs = reinterpret_cast<f16 *>(smem);
+    const int pair = p.pair0 + int(blockIdx.y);
+    const int tok = pair / p.xkrep;
+    for (int i = threadIdx.x; i < p.IN; i += blockDim.x)
+        xs[i] = f16(load_act(p.x, p.x_type, int64_t(tok) * p.x_stride + i));
+    __syncthreads();
+    const int r = int(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= p.OUT) return;
+    const uint32_t e = p.eidx ? p.eidx[pair] : 0u;
+    int64_t cr = -1;
+    if (e < uint32_t(p.E)) {
+        cr = int64_t(e) * p.OUT + r;
+        if (p.row_table) cr = p.row_table[cr];
+        if (cr >= p.stored_rows) cr = -1;
+    }
+    float acc = 0.f;
+    if (cr >= 0) {
+        const uint16_t *srow = p.scales + cr * p.ngrp;
+        float ga = 0.f;
+        int gcur = 0;
+        for (int j = 0; j < p.NSUB; ++j) {
+            const int g = (j * D) / p.G;
+            if (g != gcur) {
+                acc = fmaf(h_to_f32(srow[gcur]), ga, acc);
+                ga = 0.f;
+                gcur = g;
+            }
+            const uint32_t c = min(generic_code(p, cr, j), uint32_t(p.K - 1));
+            const uint16_t *ce = p.codebook + int64_t(c) * D;
+#pragma unroll
+            for (int u = 0; u < D; ++u) ga = fmaf(h_to_f32(ce[u]), float(xs[j * D + u]), ga);
+        }
+        acc = fmaf(h_to_f32(srow[gcur]), ga, acc);
+    }
+    store_act(p.y, p.y_type, int64_t(pair) * p.y_stride + r, acc);
+}
+
+// Per-D launchers of the fast kernel (one translation unit per D).
+int launch_gemv_fast_d2(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
+int launch_gemv_fast_d4(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
+int launch_gemv_fast_d8(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
+
+// Launch helper: raises the dynamic-LDS cap once per kernel instance.
+template <auto KERN, typename P>
+int launch_with_lds(dim3 grid, dim3 block, size_t smem, hipStream_t st, const P &p) {
+    static bool raised = false;   // idempotent attribute update; a race only repeats it
+    if (smem > 64 * 1024 && !raised) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(KERN),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(smem));
+        if (e != hipSuccess) return hip_status(e, "hipFuncSetAttribute");
+        raised = true;
+    }
+    hipLaunchKernelGGL(KERN, grid, block, smem, st, p);
+    return hip_status(hipGetLastError(), "kernel launch");
+}
+
+}  // namespace vqk

@@ -1,0 +1,549 @@
+// Fused MoE decode layer: routing + SwitchGLU + combine in two kernels.
+//
+// Reference: mlx-lm's SparseMoeBlock / SwitchGLU around VQSwitchLinear,
+// restated in bench/decode_ladder.py:107-119 (softmax(fp32) -> top-k ->
+// renormalise -> up/gate -> SiLU(gate)*up -> down -> sum_j w_j y_j) and
+// tests/test_qwen3_5_parity.py:180-205 (+ sigmoid(shared_gate . x) * shared(x)).
+//
+//   k_moe_up    grid (row tiles of I, T * P), P = top_k + shared pairs per token.
+//               Every wave computes its token's routing from the logits (no
+//               extra launch, no host sync), loads its gate AND up blocks for
+//               the same rows, decodes both against LDS/L2 codebooks and
+//               writes h = silu(g) * u as fp16 into the workspace. Workgroup
+//               (0, pair 0) of each token also writes the routing.
+//   k_moe_down  grid (row tiles of H, T). Lanes are (pair j, block b) of one
+//               token, so a wave covers whole output rows across all the
+//               token's experts; each lane scales its partial by the router
+//               weight and the butterfly reduction IS the combine -- no
+//               atomics, deterministic.
+#include "vqk_gemv.h"
+#include "vqk_internal.h"
+
+namespace vqk {
+
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxSlots = kMaxExperts / kWave;   // logits per lane
+constexpr int kMaxTopK = 64;
+
+struct MoeW {            // one projection of the layer, as the kernels see it
+    const uint32_t *codes;
+    const uint16_t *codebook;
+    const uint16_t *scales;
+    const int32_t *row_table;
+    int64_t row_words;
+    int64_t stored_rows;
+    int32_t K;
+};
+
+struct MoeParams {
+    MoeW gate, up, down, sgate, sup, sdown;   // s* = shared expert (E == 1)
+    int32_t shared;                           // 1 if the shared expert exists
+    int32_t E, top_k, norm;
+    int32_t H, I;                             // hidden (x, y) and intermediate widths
+    int32_t NB1, NB2;                         // blocks per row: gate/up (H) and down (I)
+    int32_t ngrp1, ngrp2, bpg1, bpg2;
+    int32_t lpr1_log2, lpr2_log2;
+    int32_t rows_per_wg1, steps1, rows_per_wg2, steps2;
+    int32_t T, P;
+    const void *x;
+    int32_t x_type;
+    const float *logits;
+    const void *sg_vec;
+    int32_t sg_type;
+    void *y;
+    int32_t y_type;
+    int32_t *ids;        // workspace [T, top_k]
+    float *wts;          // workspace [T, top_k]
+    float *sg;           // workspace [T]
+    uint16_t *h;         // workspace [T, P, I] fp16
+    int32_t *ids_out;    // optional user copies
+    float *wts_out;
+};
+
+// ------------------------------------------------------------ routing
+// Wave-level softmax + top-k of one token's logits. Every lane returns the
+// same results: the expert of pair `want` (or -1) in *e_want; lanes r < k
+// hold selection r in (*my_idx, *my_w). Ties go to the lower expert id.
+__device__ __forceinline__ void route_wave(const float *lg, int E, int k, int norm, int want,
+                                           int *e_want, int *my_idx, float *my_w) {
+    const int lane = threadIdx.x & (kWave - 1);
+    float v[kMaxSlots];
+#pragma unroll
+    for (int s = 0; s < kMaxSlots; ++s) {
+        const int i = s * kWave + lane;
+        v[s] = i < E ? lg[i] : -INFINITY;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kMaxSlots; ++s) m = fmaxf(m, v[s]);
+    for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+    float den = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxSlots; ++s) {
+        const int i = s * kWave + lane;
+        if (i < E) den += __expf(v[s] - m);
+    }
+    for (int off = kWave / 2; off > 0; off >>= 1) den += __shfl_xor(den, off, kWave);
+    float psel = 0.f, mine = -INFINITY;
+    int e_w = -1, midx = -1;
+    for (int r = 0; r < k; ++r) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int s = 0; s < kMaxSlots; ++s) {
+            const int i = s * kWave + lane;
+            if (i < E && (v[s] > bv || (v[s] == bv && i < bi))) { bv = v[s]; bi = i; }
+        }
+        for (int off = kWave / 2; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, kWave);
+            const int oi = __shfl_xor(bi, off, kWave);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+#pragma unroll
+        for (int s = 0; s < kMaxSlots; ++s)
+            if (s * kWave + lane == bi) v[s] = -INFINITY;   // taken
+        const float p = __expf(bv - m) / den;
+        psel += p;
+        if (r == want) e_w = bi;
+        if (lane == r) { midx = bi; mine = p; }
+    }
+    *e_want = e_w;
+    *my_idx = midx;
+    *my_w = norm ? mine / psel : mine;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.f + __expf(-g)); }
+
+template <int BITS, int GPB>
+__device__ __forceinline__ void moe_load(const MoeW &w, int64_t cr, int blk, int sidx, int ngrp,
+                                         uint32_t (&wd)[BITS], float (&s)[GPB]) {
+    if (cr >= 0) {
+        const uint32_t *src = w.codes + cr * w.row_words + int64_t(blk) * BITS;
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) wd[i] = __builtin_nontemporal_load(src + i);
+        const uint16_t *sr = w.scales + cr * ngrp + sidx;
+#pragma unroll
+        for (int g = 0; g < GPB; ++g) s[g] = h_to_f32(__builtin_nontemporal_load(sr + g));
+    } else {
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) wd[i] = 0u;
+#pragma unroll
+        for (int g = 0; g < GPB; ++g) s[g] = 0.f;
+    }
+}
+
+__device__ __forceinline__ int64_t moe_row(const MoeW &w, int64_t e, int OUT, int r) {
+    int64_t f = e * OUT + r;
+    if (w.row_table) f = w.row_table[f];
+    return f < w.stored_rows ? f : -1;
+}
+
+// ------------------------------------------------------------ K1: gate/up
+template <int D, int BITS, int GPB>
+__global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
+    constexpr bool CBL = cb_in_lds(D, BITS);
+    constexpr int CBN = CBL ? (1 << BITS) : 0;
+    constexpr int XH = kBlock * D, XS = XH + 8;
+    extern __shared__ __align__(16) uint8_t smem[];
+    h2 *cbg_lds = reinterpret_cast<h2 *>(smem);
+    h2 *cbu_lds = reinterpret_cast<h2 *>(smem + CBN * D * 2);
+    f16 *xs = reinterpret_cast<f16 *>(smem + 2 * CBN * D * 2);
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int lpr = 1 << p.lpr1_log2, rpw = kWave >> p.lpr1_log2;
+    const int sub = lane >> p.lpr1_log2, blk = lane & (lpr - 1);
+    const bool on = blk < p.NB1;
+    const int pair = blockIdx.y, t = pair / p.P, j = pair % p.P;
+    const bool is_shared = j >= p.top_k;
+    const MoeW &wg = is_shared ? p.sgate : p.gate;
+    const MoeW &wu = is_shared ? p.sup : p.up;
+    const float *lg = p.logits + int64_t(t) * p.E;
+
+    int e_pair, my_idx;
+    float my_w;
+    route_wave(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &e_pair, &my_idx, &my_w);
+    // a NaN logit can leave the argmax at its sentinel: such a pair reads nothing
+    const int64_t e = is_shared ? 0 : ((e_pair >= 0 && e_pair < p.E) ? e_pair : -1);
+    const int sidx = GPB == 1 ? blk / p.bpg1 : blk * GPB;
+    const int r_wg = int(blockIdx.x) * p.rows_per_wg1;
+    auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * rpw + sub; };
+
+    uint32_t ag[BITS], au[BITS];
+    float sg_[GPB], su_[GPB];
+    int64_t crg, cru;
+    {
+        const int r = row_at(0);
+        const bool ok = on && e >= 0 && r < p.I;
+        crg = ok ? moe_row(wg, e, p.I, r) : -1;
+        cru = ok ? moe_row(wu, e, p.I, r) : -1;
+        moe_load<BITS, GPB>(wg, crg, blk, sidx, p.ngrp1, ag, sg_);
+        moe_load<BITS, GPB>(wu, cru, blk, sidx, p.ngrp1, au, su_);
+    }
+    if constexpr (CBL) {
+        stage_codebook<D>(wg.codebook, wg.K, CBN, cbg_lds);
+        stage_codebook<D>(wu.codebook, wu.K, CBN, cbu_lds);
+    }
+    stage_x<XH, XS>(p.x, p.x_type, int64_t(t) * p.H, p.H, p.NB1, xs);
+
+    // routing / shared-gate outputs, once per token
+    if (blockIdx.x == 0 && j == 0 && wave == 0) {
+        if (lane < p.top_k) {
+            if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
+            p.ids[t * p.top_k + lane] = my_idx;
+            p.wts[t * p.top_k + lane] = my_w;
+            if (p.ids_out) p.ids_out[t * p.top_k + lane] = my_idx;
+            if (p.wts_out) p.wts_out[t * p.top_k + lane] = my_w;
+        }
+        if (p.shared) {
+            float acc = 0.f;
+            for (int i = lane; i < p.H; i += kWave)
+                acc += load_act(p.x, p.x_type, int64_t(t) * p.H + i) * load_act(p.sg_vec, p.sg_type, i);
+            for (int off = kWave / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+            if (lane == 0) p.sg[t] = 1.f / (1.f + __expf(-acc));
+        }
+    }
+    __syncthreads();
+
+    h2 xr[16 * D];
+    load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
+    const h2 *cbg = CBL ? cbg_lds : reinterpret_cast<const h2 *>(wg.codebook);
+    const h2 *cbu = CBL ? cbu_lds : reinterpret_cast<const h2 *>(wu.codebook);
+    uint16_t *hrow = p.h + (int64_t(t) * p.P + j) * p.I;
+
+    for (int st = 0; st < p.steps1; ++st) {
+        uint32_t ng[BITS], nu[BITS];
+        float nsg[GPB], nsu[GPB];
+        int64_t ncg = -1, ncu = -1;
+        if (st + 1 < p.steps1) {
+            const int r = row_at(st + 1);
+            const bool ok = on && e >= 0 && r < p.I;
+            ncg = ok ? moe_row(wg, e, p.I, r) : -1;
+            ncu = ok ? moe_row(wu, e, p.I, r) : -1;
+        }
+        moe_load<BITS, GPB>(wg, ncg, blk, sidx, p.ngrp1, ng, nsg);
+        moe_load<BITS, GPB>(wu, ncu, blk, sidx, p.ngrp1, nu, nsu);
+        float vg = 0.f, vu = 0.f;
+        if (crg >= 0) vg = block_dot<D, BITS, GPB, CBL>(ag, xr, sg_, cbg, uint32_t(wg.K - 1));
+        if (cru >= 0) vu = block_dot<D, BITS, GPB, CBL>(au, xr, su_, cbu, uint32_t(wu.K - 1));
+        vg = group_sum(vg, lpr);
+        vu = group_sum(vu, lpr);
+        const int r = row_at(st);
+        if (blk == 0 && r < p.I) hrow[r] = f32_to_h(silu(vg) * vu);
+        crg = ncg;
+        cru = ncu;
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) { ag[i] = ng[i]; au[i] = nu[i]; }
+#pragma unroll
+        for (int g = 0; g < GPB; ++g) { sg_[g] = nsg[g]; su_[g] = nsu[g]; }
+    }
+}
+
+// ------------------------------------------------------------ K2: down + combine
+template <int D, int BITS, int GPB>
+__global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
+    constexpr bool CBL = cb_in_lds(D, BITS);
+    constexpr int CBN = CBL ? (1 << BITS) : 0;
+    constexpr int XH = kBlock * D, XS = XH + 8;
+    extern __shared__ __align__(16) uint8_t smem[];
+    h2 *cbd_lds = reinterpret_cast<h2 *>(smem);
+    h2 *cbs_lds = reinterpret_cast<h2 *>(smem + CBN * D * 2);
+    f16 *xs = reinterpret_cast<f16 *>(smem + (1 + p.shared) * CBN * D * 2);
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int lpr = 1 << p.lpr2_log2, rpw = kWave >> p.lpr2_log2;
+    const int sub = lane >> p.lpr2_log2, v = lane & (lpr - 1);
+    const int j = v / p.NB2, blk = v % p.NB2;
+    const bool on = j < p.P;
+    const int t = blockIdx.y;
+    const bool is_shared = on && j >= p.top_k;
+    const MoeW &wd = is_shared ? p.sdown : p.down;
+    int64_t e = -1;
+    float wj = 0.f;
+    if (on) {
+        if (is_shared) { e = 0; wj = p.sg[t]; }
+        else {
+            const int id = p.ids[t * p.top_k + j];
+            e = (id >= 0 && id < p.E) ? id : -1;
+            wj = p.wts[t * p.top_k + j];
+        }
+    }
+    const int sidx = GPB == 1 ? blk / p.bpg2 : blk * GPB;
+    const int r_wg = int(blockIdx.x) * p.rows_per_wg2;
+    auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * rpw + sub; };
+    auto code_row = [&](int st) -> int64_t {
+        const int r = row_at(st);
+        return (e >= 0 && r < p.H) ? moe_row(wd, e, p.H, r) : -1;
+    };
+
+    uint32_t a[BITS];
+    float s[GPB];
+    int64_t cr = code_row(0);
+    moe_load<BITS, GPB>(wd, cr, blk, sidx, p.ngrp2, a, s);
+    if constexpr (CBL) {
+        stage_codebook<D>(p.down.codebook, p.down.K, CBN, cbd_lds);
+        if (p.shared) stage_codebook<D>(p.sdown.codebook, p.sdown.K, CBN, cbs_lds);
+    }
+    // the token's P intermediate rows (fp16), blocks at the padded stride
+    {
+        const uint16_t *hsrc = p.h + int64_t(t) * p.P * p.I;
+        const int nblk = p.P * p.NB2;
+        for (int i = tid; i < nblk * XH; i += blockDim.x) {
+            const int b = i / XH, o = i % XH;
+            const int jj = b / p.NB2, col = (b % p.NB2) * XH + o;
+            const uint16_t hv = col < p.I ? hsrc[int64_t(jj) * p.I + col] : uint16_t(0);
+            xs[b * XS + o] = __builtin_bit_cast(f16, hv);
+        }
+    }
+    __syncthreads();
+
+    h2 xr[16 * D];
+    load_xregs<D>(xs + (on ? j * p.NB2 + blk : 0) * XS, xr);
+    const h2 *cb = CBL ? (is_shared ? cbs_lds : cbd_lds)
+                       : reinterpret_cast<const h2 *>(wd.codebook);
+    const uint32_t kmax = uint32_t(wd.K - 1);
+
+    for (int st = 0; st < p.steps2; ++st) {
+        uint32_t n[BITS];
+        float ns[GPB];
+        const int64_t crn = st + 1 < p.steps2 ? code_row(st + 1) : -1;
+        moe_load<BITS, GPB>(wd, crn, blk, sidx, p.ngrp2, n, ns);
+        float acc = 0.f;
+        if (cr >= 0) acc = wj * block_dot<D, BITS, GPB, CBL>(a, xr, s, cb, kmax);
+        acc = group_sum(acc, lpr);
+        const int r = row_at(st);
+        if (v == 0 && r < p.H) store_act(p.y, p.y_type, int64_t(t) * p.H + r, acc);
+        cr = crn;
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) a[i] = n[i];
+#pragma unroll
+        for (int g = 0; g < GPB; ++g) s[g] = ns[g];
+    }
+}
+
+// ------------------------------------------------------------ host side
+static size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
+
+struct MoeLayout {
+    size_t ids, wts, sg, h, total;
+};
+
+static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I) {
+    MoeLayout L;
+    L.ids = 0;
+    L.wts = align_up(L.ids + sizeof(int32_t) * T * k);
+    L.sg = align_up(L.wts + sizeof(float) * T * k);
+    L.h = align_up(L.sg + sizeof(float) * T);
+    L.total = align_up(L.h + 2 * size_t(T) * P * I);
+    return L;
+}
+
+static bool same_format(const Geom &a, const Geom &b) {
+    return a.D == b.D && a.BITS == b.BITS && a.packed == b.packed && a.G == b.G &&
+           a.OUT == b.OUT && a.IN == b.IN && a.gpb == b.gpb && a.bpg == b.bpg;
+}
+
+static void fill_moew(const vqk_weights *w, const Geom &g, MoeW *m) {
+    m->codes = static_cast<const uint32_t *>(w->codes);
+    m->codebook = w->codebook;
+    m->scales = w->scales;
+    m->row_table = w->row_table;
+    m->row_words = g.row_words;
+    m->stored_rows = g.rows;
+    m->K = int32_t(g.K);
+}
+
+struct MoePlan {
+    Geom g1, g2;
+    MoeParams p;
+    MoeLayout lay;
+    size_t smem1, smem2;
+    dim3 grid1, grid2;
+};
+
+static int lg2(int64_t v) {
+    int l = 0;
+    while ((int64_t(1) << l) < v) ++l;
+    return l;
+}
+
+static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
+    if (!m || !m->gate || !m->up || !m->down)
+        return set_error(VQK_EINVAL, "moe layer: gate, up and down are required");
+    Geom gg, gu, gd;
+    int rc;
+    if ((rc = make_geom(m->gate, &gg)) || (rc = make_geom(m->up, &gu)) || (rc = make_geom(m->down, &gd)))
+        return rc;
+    if (!same_format(gg, gu) || gg.E != gu.E)
+        return set_error(VQK_ENOTIMPL, "fused layer: gate and up must share one format");
+    if (gd.E != gg.E || gd.OUT != gg.IN || gd.IN != gg.OUT)
+        return set_error(VQK_EINVAL, "fused layer: down must be [E, H, I] for gate/up [E, I, H]");
+    const bool shared = m->sh_gate != nullptr;
+    if (shared) {
+        Geom sg1, su1, sd1;
+        if (!m->sh_up || !m->sh_down || !m->sh_gate_vec)
+            return set_error(VQK_EINVAL, "shared expert needs gate, up, down and the gate vector");
+        if ((rc = make_geom(m->sh_gate, &sg1)) || (rc = make_geom(m->sh_up, &su1)) ||
+            (rc = make_geom(m->sh_down, &sd1)))
+            return rc;
+        if (sg1.E != 1 || su1.E != 1 || sd1.E != 1)
+            return set_error(VQK_EINVAL, "shared expert projections have E=1");
+        if (!same_format(sg1, gg) || !same_format(su1, gg) || !same_format(sd1, gd))
+            return set_error(VQK_ENOTIMPL, "fused layer: shared expert must share the routed formats");
+        if (!act_size(m->sh_gate_vec_type)) return set_error(VQK_EINVAL, "bad shared gate vector type");
+    }
+    const int64_t E = gg.E;
+    const int k = m->top_k;
+    if (E > kMaxExperts) return set_error(VQK_ENOTIMPL, "fused layer: E=%lld > %d", (long long)E, kMaxExperts);
+    if (k < 1 || k > E || k > kMaxTopK) return set_error(VQK_EINVAL, "top_k=%d outside [1, min(E, %d)]", k, kMaxTopK);
+    if (!gg.fast_ok || !gd.fast_ok)
+        return set_error(VQK_ENOTIMPL, "fused layer: shape outside the fast kernels (ragged / NB > 64)");
+    const int P = k + (shared ? 1 : 0);
+    if (P * gd.NB > kWave)
+        return set_error(VQK_ENOTIMPL, "fused layer: %d pairs x %lld blocks exceed one wave", P,
+                         (long long)gd.NB);
+    if (T < 0 || T > 65535) return set_error(VQK_EINVAL, "T=%lld", (long long)T);
+    pl->g1 = gg;
+    pl->g2 = gd;
+    MoeParams &p = pl->p;
+    memset(&p, 0, sizeof p);
+    fill_moew(m->gate, gg, &p.gate);
+    fill_moew(m->up, gu, &p.up);
+    fill_moew(m->down, gd, &p.down);
+    if (shared) {
+        Geom a;
+        make_geom(m->sh_gate, &a); fill_moew(m->sh_gate, a, &p.sgate);
+        make_geom(m->sh_up, &a);   fill_moew(m->sh_up, a, &p.sup);
+        make_geom(m->sh_down, &a); fill_moew(m->sh_down, a, &p.sdown);
+    } else {
+        p.sgate = p.gate; p.sup = p.up; p.sdown = p.down;
+    }
+    p.shared = shared;
+    p.E = int32_t(E);
+    p.top_k = k;
+    p.norm = m->norm_topk ? 1 : 0;
+    p.H = int32_t(gg.IN);
+    p.I = int32_t(gg.OUT);
+    p.NB1 = int32_t(gg.NB);
+    p.NB2 = int32_t(gd.NB);
+    p.ngrp1 = int32_t(gg.NGRP);
+    p.ngrp2 = int32_t(gd.NGRP);
+    p.bpg1 = gg.bpg;
+    p.bpg2 = gd.bpg;
+    p.lpr1_log2 = lg2(gg.NB);
+    p.lpr2_log2 = lg2(int64_t(P) * gd.NB);
+    p.T = int32_t(T);
+    p.P = P;
+    p.sg_vec = m->sh_gate_vec;
+    p.sg_type = m->sh_gate_vec_type;
+    const int64_t target = 2048;
+    {   // K1: T*P pairs x I rows
+        const int rpw = kWave >> p.lpr1_log2;
+        const int64_t steps_total = T * P * ((gg.OUT + rpw - 1) / rpw);
+        int64_t st = (steps_total + target - 1) / target;
+        st = st < 1 ? 1 : (st > 16 ? 16 : st);
+        p.steps1 = int32_t(st);
+        p.rows_per_wg1 = int32_t(4 * rpw * st);
+        pl->grid1 = dim3(unsigned((gg.OUT + p.rows_per_wg1 - 1) / p.rows_per_wg1), unsigned(T * P), 1);
+    }
+    {   // K2: T tokens x H rows
+        const int rpw = kWave >> p.lpr2_log2;
+        const int64_t steps_total = T * ((gd.OUT + rpw - 1) / rpw);
+        int64_t st = (steps_total + target - 1) / target;
+        st = st < 1 ? 1 : (st > 16 ? 16 : st);
+        p.steps2 = int32_t(st);
+        p.rows_per_wg2 = int32_t(4 * rpw * st);
+        pl->grid2 = dim3(unsigned((gd.OUT + p.rows_per_wg2 - 1) / p.rows_per_wg2), unsigned(T), 1);
+    }
+    const size_t cb1 = cb_in_lds(gg.D, gg.BITS) ? (size_t(1) << gg.BITS) * gg.D * 2 : 0;
+    const size_t cb2 = cb_in_lds(gd.D, gd.BITS) ? (size_t(1) << gd.BITS) * gd.D * 2 : 0;
+    pl->smem1 = 2 * cb1 + size_t(gg.NB) * (kBlock * gg.D + 8) * 2;
+    pl->smem2 = (shared ? 2 : 1) * cb2 + size_t(P) * gd.NB * (kBlock * gd.D + 8) * 2;
+    if (pl->smem1 > 160 * 1024 || pl->smem2 > 160 * 1024)
+        return set_error(VQK_ENOTIMPL, "fused layer: LDS need %zu / %zu B exceeds 160 KB",
+                         pl->smem1, pl->smem2);
+    pl->lay = moe_layout(T, k, P, gg.OUT);
+    return VQK_OK;
+}
+
+int launch_moe_up(const MoeParams &p, int D, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
+int launch_moe_down(const MoeParams &p, int D, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
+
+template <int D, int BITS, int GPB>
+static int go_up(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
+    return launch_with_lds<k_moe_up<D, BITS, GPB>>(grid, dim3(kThreads), smem, st, p);
+}
+template <int D, int BITS, int GPB>
+static int go_down(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
+    return launch_with_lds<k_moe_down<D, BITS, GPB>>(grid, dim3(kThreads), smem, st, p);
+}
+
+// Instances: every width for d in {2, 4, 8}, scale groups of 64 weights.
+#define VQK_MOE_BITS(X, D, G) \
+    X(D, 2, G) X(D, 3, G) X(D, 4, G) X(D, 5, G) X(D, 6, G) X(D, 7, G) X(D, 8, G) X(D, 9, G) \
+    X(D, 10, G) X(D, 11, G) X(D, 12, G) X(D, 13, G) X(D, 14, G) X(D, 15, G) X(D, 16, G)
+#define VQK_UP_CASE(D, B, G) if (d == D && bits == B && gpb == G) return go_up<D, B, G>(p, grid, smem, st);
+#define VQK_DN_CASE(D, B, G) if (d == D && bits == B && gpb == G) return go_down<D, B, G>(p, grid, smem, st);
+
+int launch_moe_up(const MoeParams &p, int d, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st) {
+    VQK_MOE_BITS(VQK_UP_CASE, 2, 1)
+    VQK_MOE_BITS(VQK_UP_CASE, 4, 2)
+    VQK_MOE_BITS(VQK_UP_CASE, 8, 4)
+    return set_error(VQK_ENOTIMPL, "fused layer: no kernel for d=%d bits=%d (%d groups/block); "
+                     "the fused layer takes scale groups of 64 weights", d, bits, gpb);
+}
+
+int launch_moe_down(const MoeParams &p, int d, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st) {
+    VQK_MOE_BITS(VQK_DN_CASE, 2, 1)
+    VQK_MOE_BITS(VQK_DN_CASE, 4, 2)
+    VQK_MOE_BITS(VQK_DN_CASE, 8, 4)
+    return set_error(VQK_ENOTIMPL, "fused layer: no kernel for d=%d bits=%d (%d groups/block); "
+                     "the fused layer takes scale groups of 64 weights", d, bits, gpb);
+}
+
+}  // namespace vqk
+
+using namespace vqk;
+
+extern "C" {
+
+int vqk_moe_decode_layer_workspace(const vqk_moe_desc *m, int64_t T, size_t *bytes) {
+    if (!bytes) return set_error(VQK_EINVAL, "bytes is NULL");
+    MoePlan pl;
+    int rc = moe_plan(m, T, &pl);
+    if (rc) return rc;
+    *bytes = pl.lay.total;
+    return VQK_OK;
+}
+
+int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, int64_t T,
+                         const float *logits, void *y, int32_t y_type, int32_t *topk_ids,
+                         float *topk_w, void *workspace, size_t ws_bytes, void *stream) {
+    MoePlan pl;
+    int rc = moe_plan(m, T, &pl);
+    if (rc) return rc;
+    if (!act_size(x_type) || !act_size(y_type))
+        return set_error(VQK_EINVAL, "x/y type must be VQK_F16, VQK_BF16 or VQK_F32");
+    if (!x || !y || !logits) return set_error(VQK_EINVAL, "x, logits and y are required");
+    if (!workspace || ws_bytes < pl.lay.total)
+        return set_error(VQK_ENOSPACE, "workspace %zu B < %zu B", ws_bytes, pl.lay.total);
+    if (T == 0) return VQK_OK;
+    MoeParams &p = pl.p;
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    p.ids = reinterpret_cast<int32_t *>(ws + pl.lay.ids);
+    p.wts = reinterpret_cast<float *>(ws + pl.lay.wts);
+    p.sg = reinterpret_cast<float *>(ws + pl.lay.sg);
+    p.h = reinterpret_cast<uint16_t *>(ws + pl.lay.h);
+    p.ids_out = topk_ids;
+    p.wts_out = topk_w;
+    p.x = x;
+    p.x_type = x_type;
+    p.logits = logits;
+    p.y = y;
+    p.y_type = y_type;
+    hipStream_t st = hipStream_t(stream);
+    rc = launch_moe_up(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.grid1, pl.smem1, st);
+    if (rc) return rc;
+    return launch_moe_down(p, pl.g2.D, pl.g2.BITS, pl.g2.gpb, pl.grid2, pl.smem2, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,221 @@
+// Index packing and dequantisation kernels (bit-exact paths).
+//
+//  vqk_pack / vqk_unpack          vq_pack.pack / vq_pack.unpack (vq_pack.py:48-97)
+//  vqk_dequant                    wdec_decode (vq_switch.py:3463-3544)
+//  vqk_dequant_experts            _decode_chunk / vq_decode (vq_switch.py:2542-2591, 4725-4782)
+//
+// Layout (vq_pack.py:11-27): each code row is ceil(NSUB/32) blocks of BITS
+// uint32 words; code i of a block starts at bit i*BITS of the block, LSB
+// first, and may straddle two words of its block. Widths 8 and 16 are
+// byte-identical to little-endian uint8 / uint16 arrays.
+//
+// The dequantised weight is W[r, j*D+u] = fp16(f32(cb[c_rj, u]) * f32(s[r, (j*D+u)/G])):
+// the product of two fp16 values is exact in fp32, so the one v_cvt_f16_f32
+// (round to nearest even) is the only rounding, as in the reference.
+#include "vqk_common.h"
+
+namespace vqk {
+
+// Field j of a packed row, for a runtime width (1..16).
+__device__ __forceinline__ uint32_t packed_code(const uint32_t *row, int64_t j, int bits) {
+    const int64_t bit = (j >> 5) * (int64_t(kBlock) * bits) + (j & 31) * bits;
+    const int sh = int(bit & 31);
+    const int64_t wi = bit >> 5;
+    uint32_t v = row[wi] >> sh;
+    if (sh + bits > 32) v |= row[wi + 1] << (32 - sh);
+    return v & ((1u << bits) - 1u);
+}
+
+// grid: x covers codes of a row, y strides over rows.
+__global__ void __launch_bounds__(256) k_unpack(const uint32_t *packed, int64_t rows, int64_t nsub,
+                                                int bits, void *codes) {
+    const int64_t wpr = (nsub + kBlock - 1) / kBlock * bits;
+    const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (j >= nsub) return;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const uint32_t c = packed_code(packed + r * wpr, j, bits);
+        if (bits <= 8) static_cast<uint8_t *>(codes)[r * nsub + j] = uint8_t(c);
+        else static_cast<uint16_t *>(codes)[r * nsub + j] = uint16_t(c);
+    }
+}
+
+// One thread per output word: gathers the (at most 32/bits + 2) fields that
+// overlap word wi of its block. Field bits above `bits` are dropped.
+__global__ void __launch_bounds__(256) k_pack(const uint16_t *codes, int64_t rows, int64_t nsub,
+                                              int bits, uint32_t *packed) {
+    const int64_t wpr = (nsub + kBlock - 1) / kBlock * bits;
+    const int64_t w = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (w >= wpr) return;
+    const int64_t blk = w / bits;
+    const int wi = int(w % bits);
+    const int lo = wi * 32;                 // first bit of this word inside the block
+    const int i0 = lo / bits;
+    const int i1 = min(kBlock - 1, (lo + 31) / bits);
+    const uint32_t mask = (1u << bits) - 1u;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        uint32_t v = 0;
+        for (int i = i0; i <= i1; ++i) {
+            const int64_t j = blk * kBlock + i;
+            const uint32_t c = j < nsub ? (uint32_t(codes[r * nsub + j]) & mask) : 0u;
+            const int p = i * bits;         // field start inside the block
+            v |= p >= lo ? (c << (p - lo)) : (c >> (lo - p));
+        }
+        packed[r * wpr + w] = v;
+    }
+}
+
+struct DequantArgs {
+    const void *codes;
+    int64_t code_cols;       // u32 words (packed) or codes (unpacked) per code row
+    int bits;                // packed width, 0 = unpacked
+    int code_bytes;          // 1 or 2 when unpacked
+    const uint16_t *codebook;
+    int64_t K;
+    const uint16_t *scales;
+    int64_t ngrp;
+    int G;
+    const int32_t *row_table;
+    const uint32_t *eidx;    // experts of the output chunk (NULL: flat rows)
+    int64_t E, stored_rows;  // experts, code rows actually stored (bounds for device indices)
+    int64_t OUT, IN, NSUB;
+    int64_t r0, rows;        // output rows: flat rows [r0, r0+rows) or ne*OUT
+    uint16_t *out;
+};
+
+// One thread per (output row, code): writes D halves with one vector store.
+template <int D>
+__global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
+    const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (j >= a.NSUB) return;
+    for (int64_t orow = blockIdx.y; orow < a.rows; orow += gridDim.y) {
+        int64_t flat;                       // row of the expanded [E*OUT] module
+        int64_t cr = -1;
+        if (a.eidx) {
+            const uint32_t e = a.eidx[orow / a.OUT];
+            flat = e < uint64_t(a.E) ? int64_t(e) * a.OUT + orow % a.OUT : -1;
+        } else {
+            flat = a.r0 + orow;
+        }
+        if (flat >= 0) cr = a.row_table ? int64_t(a.row_table[flat]) : flat;
+        if (cr >= a.stored_rows) cr = -1;   // corrupt table entry: never read past the codes
+        uint16_t vals[D];
+        if (cr < 0) {
+            // dead skipzero row (+0), or an expert id outside [0, E)
+#pragma unroll
+            for (int u = 0; u < D; ++u) vals[u] = 0;
+        } else {
+            uint32_t c;
+            if (a.bits) c = packed_code(static_cast<const uint32_t *>(a.codes) + cr * a.code_cols, j, a.bits);
+            else if (a.code_bytes == 1) c = static_cast<const uint8_t *>(a.codes)[cr * a.code_cols + j];
+            else c = static_cast<const uint16_t *>(a.codes)[cr * a.code_cols + j];
+            if (c >= uint32_t(a.K)) c = uint32_t(a.K - 1);   // never read past the table
+            const float s = h_to_f32(a.scales[cr * a.ngrp + (j * D) / a.G]);
+            const uint16_t *e = a.codebook + int64_t(c) * D;
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                // a group boundary can fall inside a subvector only if G % D != 0,
+                // which validation refuses; one scale serves all D values.
+                vals[u] = f32_to_h(s * h_to_f32(e[u]));
+            }
+        }
+        uint16_t *dst = a.out + orow * a.IN + j * D;
+        if constexpr (D == 2) {
+            *reinterpret_cast<uint32_t *>(dst) = uint32_t(vals[0]) | (uint32_t(vals[1]) << 16);
+        } else if constexpr (D == 4) {
+            u32x2 v = {uint32_t(vals[0]) | (uint32_t(vals[1]) << 16),
+                       uint32_t(vals[2]) | (uint32_t(vals[3]) << 16)};
+            *reinterpret_cast<u32x2 *>(dst) = v;
+        } else {
+            u32x4 v = {uint32_t(vals[0]) | (uint32_t(vals[1]) << 16),
+                       uint32_t(vals[2]) | (uint32_t(vals[3]) << 16),
+                       uint32_t(vals[4]) | (uint32_t(vals[5]) << 16),
+                       uint32_t(vals[6]) | (uint32_t(vals[7]) << 16)};
+            *reinterpret_cast<u32x4 *>(dst) = v;
+        }
+    }
+}
+
+static dim3 rows_grid(int64_t cols, int64_t rows) {
+    const int64_t gx = (cols + 255) / 256;
+    const int64_t gy = rows < 65535 ? (rows > 0 ? rows : 1) : 65535;
+    return dim3(unsigned(gx), unsigned(gy), 1);
+}
+
+static int launch_dequant(const vqk_weights *w, const Geom &g, const uint32_t *eidx, int64_t r0,
+                          int64_t rows, uint16_t *out, hipStream_t st) {
+    DequantArgs a;
+    a.codes = w->codes;
+    a.code_cols = w->code_cols;
+    a.bits = g.packed ? g.BITS : 0;
+    a.code_bytes = g.BITS / 8;
+    a.codebook = w->codebook;
+    a.K = g.K;
+    a.scales = w->scales;
+    a.ngrp = g.NGRP;
+    a.G = g.G;
+    a.row_table = w->row_table;
+    a.eidx = eidx;
+    a.E = g.E;
+    a.stored_rows = g.rows;
+    a.OUT = g.OUT; a.IN = g.IN; a.NSUB = g.NSUB;
+    a.r0 = r0; a.rows = rows;
+    a.out = out;
+    if (rows == 0) return VQK_OK;
+    const dim3 grid = rows_grid(g.NSUB, rows);
+    switch (g.D) {
+        case 2: hipLaunchKernelGGL(k_dequant<2>, grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(k_dequant<4>, grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL(k_dequant<8>, grid, dim3(256), 0, st, a); break;
+    }
+    return hip_status(hipGetLastError(), "dequant launch");
+}
+
+}  // namespace vqk
+
+using namespace vqk;
+
+extern "C" {
+
+int vqk_pack(const uint16_t *codes, int64_t rows, int64_t nsub, int32_t bits, uint32_t *packed,
+             void *stream) {
+    if (!codes || !packed || rows < 0 || nsub < 0 || bits < 1 || bits > 16)
+        return set_error(VQK_EINVAL, "vqk_pack: bad arguments");
+    const int64_t wpr = (nsub + kBlock - 1) / kBlock * bits;
+    if (rows == 0 || wpr == 0) return VQK_OK;
+    hipLaunchKernelGGL(k_pack, rows_grid(wpr, rows), dim3(256), 0, hipStream_t(stream), codes, rows,
+                       nsub, int(bits), packed);
+    return hip_status(hipGetLastError(), "pack launch");
+}
+
+int vqk_unpack(const uint32_t *packed, int64_t rows, int64_t nsub, int32_t bits, void *codes,
+               void *stream) {
+    if (!codes || !packed || rows < 0 || nsub < 0 || bits < 1 || bits > 16)
+        return set_error(VQK_EINVAL, "vqk_unpack: bad arguments");
+    if (rows == 0 || nsub == 0) return VQK_OK;
+    hipLaunchKernelGGL(k_unpack, rows_grid(nsub, rows), dim3(256), 0, hipStream_t(stream), packed,
+                       rows, nsub, int(bits), codes);
+    return hip_status(hipGetLastError(), "unpack launch");
+}
+
+int vqk_dequant(const vqk_weights *w, int64_t r0, int64_t rows, uint16_t *out, void *stream) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if (!out) return set_error(VQK_EINVAL, "vqk_dequant: out is NULL");
+    if (r0 < 0 || rows < 0 || r0 + rows > g.E * g.OUT)
+        return set_error(VQK_EINVAL, "rows [%lld, %lld) outside the module's %lld rows",
+                         (long long)r0, (long long)(r0 + rows), (long long)(g.E * g.OUT));
+    return launch_dequant(w, g, nullptr, r0, rows, out, hipStream_t(stream));
+}
+
+int vqk_dequant_experts(const vqk_weights *w, const uint32_t *eidx, int64_t ne, uint16_t *out,
+                        void *stream) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if (!out || (!eidx && ne > 0) || ne < 0)
+        return set_error(VQK_EINVAL, "vqk_dequant_experts: bad arguments");
+    return launch_dequant(w, g, eidx, 0, ne * g.OUT, out, hipStream_t(stream));
+}
+
+}  // extern "C"
