@@ -101,3 +101,20 @@ def test_moe_layer_workspace_too_small():
                                       Tt.ptr(y), L.VQK_BF16, None, None, Tt.ptr(ws), 16,
                                       Tt.stream())
     assert rc == L.VQK_ENOSPACE
+
+
+def test_routing_ties_pick_lower_ids():
+    """Tied logits: the kernel's argmax takes the lowest expert id first, the
+    oracle's stable descending sort does the same."""
+    print("routing ties", flush=True)
+    rng = np.random.default_rng(6)
+    blk, projs, sh, shv = _block(rng, 64, 256, 128, 4, 256, 6)
+    x = torch.from_numpy(rng.standard_normal((3, 256)).astype(np.float32)).to("cuda", torch.bfloat16)
+    lg = np.round(rng.standard_normal((3, 64)) * 2) / 2           # many exact ties
+    lg[1, :] = 0.0                                                  # all tied
+    lg[2, 10:] = -np.inf                                            # only 10 finite
+    lgt = torch.from_numpy(lg.astype(np.float32)).cuda()
+    _, ids, w = blk.fused(x, lgt, return_route=True)
+    rids, rw = vo.route(lg.astype(np.float32), 6)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-6)

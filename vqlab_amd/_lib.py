@@ -7,9 +7,12 @@ is no CPU fallback. Status codes map onto the reference's exceptions
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 
-LIB_PATH = pathlib.Path(__file__).resolve().parent / "libvqk.so"
+# VQK_LIBRARY points at another build of the same ABI (A/B of kernel variants).
+LIB_PATH = pathlib.Path(os.environ.get("VQK_LIBRARY") or
+                        pathlib.Path(__file__).resolve().parent / "libvqk.so")
 
 VQK_OK, VQK_ENOTIMPL, VQK_EINVAL, VQK_ESHARDED, VQK_EDEVICE, VQK_ENOSPACE = range(6)
 VQK_F16, VQK_BF16, VQK_F32, VQK_U8, VQK_U16, VQK_U32 = range(6)

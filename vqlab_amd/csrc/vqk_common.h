@@ -81,10 +81,74 @@ __device__ __forceinline__ void store_act(void *p, int32_t type, int64_t i, floa
     static_cast<uint16_t *>(p)[i] = type == VQK_BF16 ? f32_to_bf16(v) : f32_to_h(v);
 }
 
-// Butterfly sum over aligned groups of `width` lanes (width a power of two <= 64).
+// ---------------------------------------------------------- wave reductions
+// DPP (data-parallel primitives) move values between lanes inside the VALU,
+// without the LDS crossbar round trip of ds_bpermute. Lanes whose source is
+// masked off keep their own value (old operand = src).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL,
+                                                      ROW_MASK, 0xf, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+// Sum over aligned groups of `width` lanes (a power of two <= 64). The total
+// is valid in the LAST lane of each group (every lane of it for width <= 16).
 __device__ __forceinline__ float group_sum(float v, int width) {
-    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    if (width >= 2) v += dpp_f<kDppQuadXor1>(v);
+    if (width >= 4) v += dpp_f<kDppQuadXor2>(v);
+    if (width >= 8) v += dpp_f<kDppRowHalfMirror>(v);
+    if (width >= 16) v += dpp_f<kDppRowMirror>(v);
+    if (width >= 32) v += dpp_f<kDppRowBcast15, 0xA>(v);
+    if (width >= 64) v += dpp_f<kDppRowBcast31, 0xC>(v);
     return v;
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Unsigned max over the whole wave, returned uniformly.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u<kDppQuadXor1>(v));
+    v = max(v, dpp_u<kDppQuadXor2>(v));
+    v = max(v, dpp_u<kDppRowHalfMirror>(v));
+    v = max(v, dpp_u<kDppRowMirror>(v));
+    v = max(v, dpp_u<kDppRowBcast15, 0xA>(v));
+    v = max(v, dpp_u<kDppRowBcast31, 0xC>(v));
+    return uint32_t(__builtin_amdgcn_readlane(int(v), kWave - 1));
+}
+
+// Order-preserving map float -> uint32 (NaN maps below every number) and back.
+__device__ __forceinline__ uint32_t f32_key(float f) {
+    const uint32_t b = __float_as_uint(f);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return 0u;          // NaN: never selected
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_f32(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Max / sum of one value per lane over the whole wave, returned uniformly.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+    v = fmaxf(v, dpp_f<kDppRowBcast15, 0xA>(v));
+    v = fmaxf(v, dpp_f<kDppRowBcast31, 0xC>(v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), kWave - 1));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v = group_sum(v, kWave);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), kWave - 1));
 }
 
 }  // namespace vqk

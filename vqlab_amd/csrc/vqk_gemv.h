@@ -123,19 +123,120 @@ __device__ __forceinline__ void load_block(const GemvParams &p, int64_t cr, int 
     }
 }
 
+typedef __attribute__((address_space(1))) void global_void;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Asynchronous global -> LDS copy of `bytes` (a multiple of 4; src and dst
+// 16-byte aligned), then zero-fill up to `total` bytes. The 16-byte pieces go
+// through global_load_lds_dwordx4: each wave instruction moves 1 KB straight
+// into LDS without passing through VGPRs, so a 32 KB codebook costs one
+// memory latency. The caller waits (vmcnt 0) and barriers before reading.
+__device__ __forceinline__ void lds_copy_async(const void *src, void *dst, int bytes, int total) {
+    const uint8_t *s = static_cast<const uint8_t *>(src);
+    uint8_t *d = static_cast<uint8_t *>(dst);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const int n16 = bytes >> 4;
+    for (int c = wave * kWave; c < n16; c += nw * kWave) {    // c: first piece of a 1 KB chunk
+        if (c + lane < n16)
+            __builtin_amdgcn_global_load_lds((global_void *)(s + int64_t(c + lane) * 16),
+                                             (lds_void *)(d + int64_t(c) * 16), 16, 0, 0);
+    }
+    for (int i = n16 * 4 + threadIdx.x; i < total / 4; i += blockDim.x)
+        reinterpret_cast<uint32_t *>(d)[i] =
+            i < bytes / 4 ? reinterpret_cast<const uint32_t *>(s)[i] : 0u;
+}
+
 // Codebook -> LDS table of `entries` (>= K) rows of D halves, zero beyond K.
 template <int D>
 __device__ __forceinline__ void stage_codebook(const uint16_t *cb, int K, int entries, h2 *dst) {
-    const uint32_t *src = reinterpret_cast<const uint32_t *>(cb);
-    uint32_t *d = reinterpret_cast<uint32_t *>(dst);
-    const int valid = K * (D / 2), total = entries * (D / 2);
-    for (int i = threadIdx.x; i < total; i += blockDim.x) d[i] = i < valid ? src[i] : 0u;
+    lds_copy_async(cb, dst, K * D * 2, entries * D * 2);
 }
 
-// One activation row -> fp16 in LDS, blocks of 32*D values at a padded stride.
+// Same for a table of compile-time size CBN entries staged by NT threads:
+// every thread issues exactly CBN*D*2 / (16 * NT) direct-to-LDS loads
+// (predicated off past K), so the compiler's vmcnt waits on loads issued
+// before the copy stay exact instead of draining the whole copy.
+template <int D, int CBN, int NT>
+__device__ __forceinline__ void stage_codebook_fixed(const uint16_t *cb, int K, h2 *dst) {
+    constexpr int PIECES = CBN * D * 2 / 16;                 // 16-byte pieces of the table
+    constexpr int ROUNDS = (PIECES + NT - 1) / NT;
+    const uint8_t *s = reinterpret_cast<const uint8_t *>(cb);
+    uint8_t *d = reinterpret_cast<uint8_t *>(dst);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+    const int valid = (K * D * 2) >> 4;                      // whole valid pieces
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) {
+        const int c = (r * (NT / kWave) + wave) * kWave;     // first piece of this wave's chunk
+        if (c + lane < valid)                                // valid <= PIECES
+            __builtin_amdgcn_global_load_lds((global_void *)(s + int64_t(c + lane) * 16),
+                                             (lds_void *)(d + int64_t(c) * 16), 16, 0, 0);
+    }
+    // the sub-16-byte tail of the valid bytes, then zeros up to the table end
+    for (int i = valid * 4 + threadIdx.x; i < PIECES * 4; i += NT)
+        reinterpret_cast<uint32_t *>(d)[i] =
+            i < (K * D * 2) / 4 ? reinterpret_cast<const uint32_t *>(s)[i] : 0u;
+}
+
+// Wait for every outstanding vector-memory operation of this wave (the
+// asynchronous LDS copies included).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Eight activations starting at element i of row `base` -> fp16, as one
+// 16-byte value. 16-byte aligned rows only (checked by the caller).
+__device__ __forceinline__ u32x4 load8_act(const void *x, int32_t type, int64_t i) {
+    if (type == VQK_F32) {
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(static_cast<const float *>(x) + i);
+        const u32x4 b = *reinterpret_cast<const u32x4 *>(static_cast<const float *>(x) + i + 4);
+        u32x4 r;
+        r.x = uint32_t(f32_to_h(__uint_as_float(a.x))) | (uint32_t(f32_to_h(__uint_as_float(a.y))) << 16);
+        r.y = uint32_t(f32_to_h(__uint_as_float(a.z))) | (uint32_t(f32_to_h(__uint_as_float(a.w))) << 16);
+        r.z = uint32_t(f32_to_h(__uint_as_float(b.x))) | (uint32_t(f32_to_h(__uint_as_float(b.y))) << 16);
+        r.w = uint32_t(f32_to_h(__uint_as_float(b.z))) | (uint32_t(f32_to_h(__uint_as_float(b.w))) << 16);
+        return r;
+    }
+    u32x4 v = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(x) + i);
+    if (type == VQK_BF16) {
+        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            w[k] = uint32_t(f32_to_h(bf16_to_f32(uint16_t(w[k])))) |
+                   (uint32_t(f32_to_h(bf16_to_f32(uint16_t(w[k] >> 16)))) << 16);
+        v = u32x4{w[0], w[1], w[2], w[3]};
+    }
+    return v;
+}
+
+// One activation row -> fp16 in LDS, blocks of XH values at a padded stride
+// XS (halves). Vector path: every thread issues all its 16-byte loads before
+// converting any, so the row costs one memory latency.
 template <int XH, int XS>
 __device__ __forceinline__ void stage_x(const void *x, int32_t type, int64_t base, int IN, int NB,
                                         f16 *xs) {
+    const int esz = type == VQK_F32 ? 4 : 2;
+    const bool vec = ((reinterpret_cast<uintptr_t>(x) + uint64_t(base) * esz) & 15) == 0 &&
+                     (IN & 7) == 0;
+    if (vec) {
+        constexpr int U = 4;
+        const int ng = NB * XH / 8;                      // 8-value groups incl. zero tail
+        for (int g0 = threadIdx.x; g0 < ng; g0 += U * blockDim.x) {
+            u32x4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int g = g0 + u * blockDim.x;
+                v[u] = (g < ng && g * 8 < IN) ? load8_act(x, type, base + g * 8) : u32x4{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int g = g0 + u * blockDim.x;
+                if (g < ng) {
+                    const int i = g * 8;
+                    *reinterpret_cast<u32x4 *>(xs + (i / XH) * XS + (i % XH)) = v[u];
+                }
+            }
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < NB * XH; i += blockDim.x) {
         const float v = i < IN ? load_act(x, type, base + i) : 0.f;
         xs[(i / XH) * XS + (i % XH)] = f16(v);
@@ -189,8 +290,9 @@ __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
     int64_t cr = code_row(0);
     load_block<BITS, GPB>(p, cr, blk, sidx, w, s);   // in flight during staging
 
-    if constexpr (CBL) stage_codebook<D>(p.codebook, p.K, CBN, cb_lds);
+    if constexpr (CBL) stage_codebook_fixed<D, CBN, kThreads>(p.codebook, p.K, cb_lds);
     stage_x<XH, XS>(p.x, p.x_type, int64_t(tok) * p.x_stride, p.IN, p.NB, xs);
+    wait_vmem();
     __syncthreads();
 
     h2 xr[16 * D];
@@ -207,7 +309,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
         if (cr >= 0) v = block_dot<D, BITS, GPB, CBL>(w, xr, s, cb, kmax);
         v = group_sum(v, lpr);
         const int r = row_at(st);
-        if (blk == 0 && r < p.OUT) store_act(p.y, p.y_type, int64_t(pair) * p.y_stride + r, v);
+        if (blk == lpr - 1 && r < p.OUT) store_act(p.y, p.y_type, int64_t(pair) * p.y_stride + r, v);
         cr = crn;
 #pragma unroll
         for (int i = 0; i < BITS; ++i) w[i] = wn[i];

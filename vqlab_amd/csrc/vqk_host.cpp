@@ -113,7 +113,8 @@ int make_geom(const vqk_weights *w, Geom *g) {
     const int gpb_fast = g->D == 4 ? 2 : (g->D == 8 ? 4 : 1);   // group of 64 weights
     g->fast_ok = (g->NSUB % kBlock == 0) && g->row_words > 0 && g->NB <= kWave &&
                  g->BITS >= 2 && (g->gpb == 1 || g->gpb == gpb_fast) &&
-                 g->OUT <= INT32_MAX && g->IN <= INT32_MAX;
+                 g->OUT <= INT32_MAX && g->IN <= INT32_MAX &&
+                 (reinterpret_cast<uintptr_t>(w->codebook) & 15) == 0;   // async LDS copy
     return VQK_OK;
 }
 

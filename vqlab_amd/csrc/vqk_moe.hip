@@ -61,55 +61,101 @@ struct MoeParams {
 };
 
 // ------------------------------------------------------------ routing
-// Wave-level softmax + top-k of one token's logits. Every lane returns the
-// same results: the expert of pair `want` (or -1) in *e_want; lanes r < k
-// hold selection r in (*my_idx, *my_w). Ties go to the lower expert id.
+// Wave-level softmax + top-k of one token's logits (fp32, like the
+// reference's precise softmax), NS logits per lane (NS * 64 >= E). Every lane
+// returns the expert of pair `want` (or -1) in *e_want; lane r < k holds
+// selection r in (*my_idx, *my_w). Argmax is exact: logits become
+// order-preserving integer keys, a DPP max finds the best key and a ballot
+// per slot the lowest index holding it, so ties go to the lower expert id
+// (stable descending order). NaN logits sort below -inf and are never chosen
+// while k <= number of finite logits.
+template <int NS>
 __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int norm, int want,
-                                           int *e_want, int *my_idx, float *my_w) {
+                                           int *e_want, int *my_idx, float *my_w,
+                                           void (*issue)(void *), void *ctx) {
     const int lane = threadIdx.x & (kWave - 1);
-    float v[kMaxSlots];
+    uint32_t key[NS];
+    float raw[NS];
 #pragma unroll
-    for (int s = 0; s < kMaxSlots; ++s) {
+    for (int s = 0; s < NS; ++s) {
         const int i = s * kWave + lane;
-        v[s] = i < E ? lg[i] : -INFINITY;
+        raw[s] = i < E ? lg[i] : 0.f;
     }
-    float m = -INFINITY;
+    issue(ctx);                                          // independent loads go out behind the logits
 #pragma unroll
-    for (int s = 0; s < kMaxSlots; ++s) m = fmaxf(m, v[s]);
-    for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-    float den = 0.f;
+    for (int s = 0; s < NS; ++s) key[s] = (s * kWave + lane) < E ? f32_key(raw[s]) : 0u;
+    uint32_t lmax = 0;
 #pragma unroll
-    for (int s = 0; s < kMaxSlots; ++s) {
-        const int i = s * kWave + lane;
-        if (i < E) den += __expf(v[s] - m);
+    for (int s = 0; s < NS; ++s) lmax = max(lmax, key[s]);
+    const float m = key_f32(wave_max_u32(lmax));
+    float den = 1.f;
+    if (!norm) {                                         // renormalised weights do not need it
+        float lsum = 0.f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+            if (key[s]) lsum += __expf(key_f32(key[s]) - m);
+        den = wave_sum(lsum);
     }
-    for (int off = kWave / 2; off > 0; off >>= 1) den += __shfl_xor(den, off, kWave);
-    float psel = 0.f, mine = -INFINITY;
+    // k sequential selections; lane r keeps selection r, probabilities after
     int e_w = -1, midx = -1;
+    uint32_t mykey = 0;
     for (int r = 0; r < k; ++r) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
+        uint32_t cur = 0;
 #pragma unroll
-        for (int s = 0; s < kMaxSlots; ++s) {
-            const int i = s * kWave + lane;
-            if (i < E && (v[s] > bv || (v[s] == bv && i < bi))) { bv = v[s]; bi = i; }
-        }
-        for (int off = kWave / 2; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, kWave);
-            const int oi = __shfl_xor(bi, off, kWave);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
+        for (int s = 0; s < NS; ++s) cur = max(cur, key[s]);
+        const uint32_t best = wave_max_u32(cur);
+        int bi = -1;
+        if (best) {
 #pragma unroll
-        for (int s = 0; s < kMaxSlots; ++s)
-            if (s * kWave + lane == bi) v[s] = -INFINITY;   // taken
-        const float p = __expf(bv - m) / den;
-        psel += p;
+            for (int s = 0; s < NS; ++s) {
+                const uint64_t hit = __ballot(key[s] == best);
+                if (bi < 0 && hit) bi = s * kWave + (__ffsll((unsigned long long)hit) - 1);
+            }
+#pragma unroll
+            for (int s = 0; s < NS; ++s)
+                if (s * kWave + lane == bi) key[s] = 0u;         // taken
+        }
         if (r == want) e_w = bi;
-        if (lane == r) { midx = bi; mine = p; }
+        if (lane == r) { midx = bi; mykey = bi >= 0 ? best : 0u; }
+    }
+    const float pr = (lane < k && mykey) ? __expf(key_f32(mykey) - m) : 0.f;
+    float w = pr;
+    if (norm) {
+        const float psel = wave_sum(pr);
+        w = psel > 0.f ? pr * (1.f / psel) : 0.f;
+    } else {
+        w = pr * (1.f / den);
     }
     *e_want = e_w;
     *my_idx = midx;
-    *my_w = norm ? mine / psel : mine;
+    *my_w = w;
+}
+
+__device__ __forceinline__ void route(const float *lg, int E, int k, int norm, int want,
+                                      int *e_want, int *my_idx, float *my_w,
+                                      void (*issue)(void *), void *ctx) {
+    const int ns = (E + kWave - 1) / kWave;              // wave-uniform
+    if (ns <= 1) route_wave<1>(lg, E, k, norm, want, e_want, my_idx, my_w, issue, ctx);
+    else if (ns <= 2) route_wave<2>(lg, E, k, norm, want, e_want, my_idx, my_w, issue, ctx);
+    else if (ns <= 4) route_wave<4>(lg, E, k, norm, want, e_want, my_idx, my_w, issue, ctx);
+    else if (ns <= 8) route_wave<8>(lg, E, k, norm, want, e_want, my_idx, my_w, issue, ctx);
+    else route_wave<16>(lg, E, k, norm, want, e_want, my_idx, my_w, issue, ctx);
+}
+
+template <int D, int CBN>
+struct CbPair {            // the two codebook copies K1 queues behind its logits
+    const uint16_t *a, *b;
+    int ka, kb;
+    h2 *da, *db;
+};
+
+template <int D, int CBN>
+__device__ void issue_cb_pair(void *ctx) {
+    if constexpr (CBN > 0) {
+        const CbPair<D, CBN> *c = static_cast<const CbPair<D, CBN> *>(ctx);
+        stage_codebook_fixed<D, CBN, kThreads>(c->a, c->ka, c->da);
+        stage_codebook_fixed<D, CBN, kThreads>(c->b, c->kb, c->db);
+    }
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.f + __expf(-g)); }
@@ -159,10 +205,45 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
     const MoeW &wu = is_shared ? p.sup : p.up;
     const float *lg = p.logits + int64_t(t) * p.E;
 
-    int e_pair, my_idx;
-    float my_w;
-    route_wave(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &e_pair, &my_idx, &my_w);
-    // a NaN logit can leave the argmax at its sentinel: such a pair reads nothing
+    // Wave 0 loads the logits first and routes; every wave meanwhile streams
+    // the two codebooks and x into LDS. One barrier publishes the expert id,
+    // then all waves issue their weight loads (nothing else is outstanding,
+    // so the barrier's wait never drains weight loads).
+    __shared__ int s_route;
+    CbPair<D, CBN> cbp{wg.codebook, wu.codebook, wg.K, wu.K, cbg_lds, cbu_lds};
+    int my_idx = -1;
+    float my_w = 0.f;
+    if (wave == 0) {
+        int e_pair;
+        route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &e_pair, &my_idx, &my_w,
+              &issue_cb_pair<D, CBN>, &cbp);
+        if (lane == 0) s_route = e_pair;
+    } else {
+        issue_cb_pair<D, CBN>(&cbp);
+    }
+    stage_x<XH, XS>(p.x, p.x_type, int64_t(t) * p.H, p.H, p.NB1, xs);
+    // routing / shared-gate outputs, once per token
+    if (blockIdx.x == 0 && j == 0 && wave == 0) {
+        if (lane < p.top_k) {
+            if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
+            p.ids[t * p.top_k + lane] = my_idx;
+            p.wts[t * p.top_k + lane] = my_w;
+            if (p.ids_out) p.ids_out[t * p.top_k + lane] = my_idx;
+            if (p.wts_out) p.wts_out[t * p.top_k + lane] = my_w;
+        }
+        if (p.shared) {
+            float acc = 0.f;
+            for (int i = lane; i < p.H; i += kWave)
+                acc += load_act(p.x, p.x_type, int64_t(t) * p.H + i) * load_act(p.sg_vec, p.sg_type, i);
+            acc = wave_sum(acc);
+            if (lane == 0) p.sg[t] = 1.f / (1.f + __expf(-acc));
+        }
+    }
+    wait_vmem();
+    __syncthreads();
+
+    // a NaN logit can leave a selection empty: such a pair reads nothing
+    const int e_pair = s_route;
     const int64_t e = is_shared ? 0 : ((e_pair >= 0 && e_pair < p.E) ? e_pair : -1);
     const int sidx = GPB == 1 ? blk / p.bpg1 : blk * GPB;
     const int r_wg = int(blockIdx.x) * p.rows_per_wg1;
@@ -179,30 +260,6 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
         moe_load<BITS, GPB>(wg, crg, blk, sidx, p.ngrp1, ag, sg_);
         moe_load<BITS, GPB>(wu, cru, blk, sidx, p.ngrp1, au, su_);
     }
-    if constexpr (CBL) {
-        stage_codebook<D>(wg.codebook, wg.K, CBN, cbg_lds);
-        stage_codebook<D>(wu.codebook, wu.K, CBN, cbu_lds);
-    }
-    stage_x<XH, XS>(p.x, p.x_type, int64_t(t) * p.H, p.H, p.NB1, xs);
-
-    // routing / shared-gate outputs, once per token
-    if (blockIdx.x == 0 && j == 0 && wave == 0) {
-        if (lane < p.top_k) {
-            if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
-            p.ids[t * p.top_k + lane] = my_idx;
-            p.wts[t * p.top_k + lane] = my_w;
-            if (p.ids_out) p.ids_out[t * p.top_k + lane] = my_idx;
-            if (p.wts_out) p.wts_out[t * p.top_k + lane] = my_w;
-        }
-        if (p.shared) {
-            float acc = 0.f;
-            for (int i = lane; i < p.H; i += kWave)
-                acc += load_act(p.x, p.x_type, int64_t(t) * p.H + i) * load_act(p.sg_vec, p.sg_type, i);
-            for (int off = kWave / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
-            if (lane == 0) p.sg[t] = 1.f / (1.f + __expf(-acc));
-        }
-    }
-    __syncthreads();
 
     h2 xr[16 * D];
     load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
@@ -228,7 +285,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
         vg = group_sum(vg, lpr);
         vu = group_sum(vu, lpr);
         const int r = row_at(st);
-        if (blk == 0 && r < p.I) hrow[r] = f32_to_h(silu(vg) * vu);
+        if (blk == lpr - 1 && r < p.I) hrow[r] = f32_to_h(silu(vg) * vu);
         crg = ncg;
         cru = ncu;
 #pragma unroll
@@ -257,6 +314,10 @@ __global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
     const int t = blockIdx.y;
     const bool is_shared = on && j >= p.top_k;
     const MoeW &wd = is_shared ? p.sdown : p.down;
+    if constexpr (CBL) {                       // independent of the routing: first
+        stage_codebook_fixed<D, CBN, kThreads>(p.down.codebook, p.down.K, cbd_lds);
+        if (p.shared) stage_codebook_fixed<D, CBN, kThreads>(p.sdown.codebook, p.sdown.K, cbs_lds);
+    }
     int64_t e = -1;
     float wj = 0.f;
     if (on) {
@@ -279,21 +340,33 @@ __global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
     float s[GPB];
     int64_t cr = code_row(0);
     moe_load<BITS, GPB>(wd, cr, blk, sidx, p.ngrp2, a, s);
-    if constexpr (CBL) {
-        stage_codebook<D>(p.down.codebook, p.down.K, CBN, cbd_lds);
-        if (p.shared) stage_codebook<D>(p.sdown.codebook, p.sdown.K, CBN, cbs_lds);
-    }
-    // the token's P intermediate rows (fp16), blocks at the padded stride
+    // the token's P intermediate rows (fp16), blocks at the padded stride;
+    // 16-byte groups, all loads issued before any LDS store
     {
         const uint16_t *hsrc = p.h + int64_t(t) * p.P * p.I;
-        const int nblk = p.P * p.NB2;
-        for (int i = tid; i < nblk * XH; i += blockDim.x) {
-            const int b = i / XH, o = i % XH;
-            const int jj = b / p.NB2, col = (b % p.NB2) * XH + o;
-            const uint16_t hv = col < p.I ? hsrc[int64_t(jj) * p.I + col] : uint16_t(0);
-            xs[b * XS + o] = __builtin_bit_cast(f16, hv);
+        const int gpr = p.I / 8;                     // 8-value groups per row
+        const int ng = p.P * gpr;
+        constexpr int U = 8;
+        for (int g0 = tid; g0 < ng; g0 += U * blockDim.x) {
+            u32x4 hv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int g = g0 + u * blockDim.x;
+                hv[u] = g < ng ? *reinterpret_cast<const u32x4 *>(hsrc + int64_t(g) * 8)
+                               : u32x4{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int g = g0 + u * blockDim.x;
+                if (g < ng) {
+                    const int jj = g / gpr, col = (g % gpr) * 8;
+                    const int b = jj * p.NB2 + col / XH;
+                    *reinterpret_cast<u32x4 *>(xs + b * XS + col % XH) = hv[u];
+                }
+            }
         }
     }
+    wait_vmem();
     __syncthreads();
 
     h2 xr[16 * D];
@@ -311,7 +384,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
         if (cr >= 0) acc = wj * block_dot<D, BITS, GPB, CBL>(a, xr, s, cb, kmax);
         acc = group_sum(acc, lpr);
         const int r = row_at(st);
-        if (v == 0 && r < p.H) store_act(p.y, p.y_type, int64_t(t) * p.H + r, acc);
+        if (v == lpr - 1 && r < p.H) store_act(p.y, p.y_type, int64_t(t) * p.H + r, acc);
         cr = crn;
 #pragma unroll
         for (int i = 0; i < BITS; ++i) a[i] = n[i];
@@ -389,13 +462,15 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
             return set_error(VQK_EINVAL, "shared expert projections have E=1");
         if (!same_format(sg1, gg) || !same_format(su1, gg) || !same_format(sd1, gd))
             return set_error(VQK_ENOTIMPL, "fused layer: shared expert must share the routed formats");
+        if (!sg1.fast_ok || !su1.fast_ok || !sd1.fast_ok)
+            return set_error(VQK_ENOTIMPL, "fused layer: shared expert outside the fast kernels");
         if (!act_size(m->sh_gate_vec_type)) return set_error(VQK_EINVAL, "bad shared gate vector type");
     }
     const int64_t E = gg.E;
     const int k = m->top_k;
     if (E > kMaxExperts) return set_error(VQK_ENOTIMPL, "fused layer: E=%lld > %d", (long long)E, kMaxExperts);
     if (k < 1 || k > E || k > kMaxTopK) return set_error(VQK_EINVAL, "top_k=%d outside [1, min(E, %d)]", k, kMaxTopK);
-    if (!gg.fast_ok || !gd.fast_ok)
+    if (!gg.fast_ok || !gu.fast_ok || !gd.fast_ok)
         return set_error(VQK_ENOTIMPL, "fused layer: shape outside the fast kernels (ragged / NB > 64)");
     const int P = k + (shared ? 1 : 0);
     if (P * gd.NB > kWave)
