@@ -89,6 +89,13 @@ def test_predicates(L):
     assert not VS.dense_fits(256, 4096, 48, 8)      # 48 does not divide IN
     assert not VS.dense_fits(256, 4096, 4, 8)       # a group smaller than one subvector
     assert VS.wdec_fits(4, 512, 64, 12) and not VS.wdec_fits(3, 512, 64, 12)
+    # the grouped GEMM: d 2/4/8, up to 16-bit codes (0 = unpacked), any K
+    # that 16 bits index, IN a whole number of scale groups
+    assert VS.gemmseg_fits(8, 16384, 64, 14, 4096) and VS.gemmseg_fits(2, 256, 64, 0, 2048)
+    assert VS.gemmseg_fits(8, 65536, 64, 16, 640)
+    assert not VS.gemmseg_fits(3, 4096, 64, 12, 2048)
+    assert not VS.gemmseg_fits(4, 4096, 64, 17, 2048)
+    assert not VS.gemmseg_fits(4, 4096, 48, 12, 2048)  # 48 does not divide IN
 
 
 def _w(L, **kw):

@@ -1,0 +1,249 @@
+"""Matrix-core paths against the oracle, through the C ABI.
+
+vqk_dense_gemm (_decode_matmul, vq_dense.py:262-312) and vqk_grouped_gemm
+(_gemmseg_prefill, vq_switch.py:4569-4722): outputs within rtol 2e-2 /
+atol 1e-3 of the float64 decode-then-matmul oracle with x rounded to fp16
+(the operand the matrix cores take). The device-side sort must build the
+oracle's tile metadata (tile_meta, vq_switch.py:4590-4610) exactly.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import vq_oracle as vo
+from vq_cases import assert_close, make_module, skipzero, to_device
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _x(rng, N, IN, dt=torch.bfloat16):
+    return torch.from_numpy(rng.standard_normal((N, IN)).astype(np.float32)).to("cuda", dt)
+
+
+def _x16(x):
+    """The fp16 operand the matrix cores see, as float32 on the host."""
+    return x.to(torch.float16).float().cpu().numpy()
+
+
+# -------------------------------------------------------------- dense GEMM
+@pytest.mark.parametrize("case", [
+    # (N, OUT, IN, D, K, G, packed)
+    (33, 512, 1024, 2, 256, 64, False),        # just above the GEMV cutoff; c1 format
+    (256, 640, 2048, 4, 4096, 64, True),       # c2 format, OUT not a multiple of 128
+    (300, 384, 1024, 8, 16384, 64, True),      # d8 K16384: codebook gathered from L2
+    (130, 256, 640, 8, 65536, 64, False),      # c5 format (uint16 codes), NSUB 80
+    (64, 200, 96, 4, 1000, 32, False),         # IN not a multiple of 64, K not a power of 2
+    (129, 128, 512, 2, 512, 128, True),        # a scale group spans two 64-column steps
+])
+def test_dense_gemm(case):
+    from vqlab_amd import vq_dense as VD
+    N, OUT, IN, D, K, G, packed = case
+    print(f"dense gemm {case}", flush=True)
+    rng = np.random.default_rng(N + OUT + IN)
+    m = make_module(rng, 1, OUT, IN, D, K, G=G, packed=packed)
+    codes, cb, sc = to_device(m)
+    x = _x(rng, N, IN)
+    y = VD._decode_matmul(x, codes[0], cb, sc[0], G, OUT, IN, m["pack_bits"])
+    assert y.shape == (N, OUT) and y.dtype == x.dtype
+    w = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], G)
+    assert_close(_np(y), vo.decode_matmul(_x16(x), w), what=f"dense gemm {case}")
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
+def test_dense_gemm_dtypes_and_linear(xdt):
+    """VQLinear routes N > the GEMV cutoff to the GEMM; both agree with the
+    oracle on the same module, in fp16 and fp32 activations."""
+    from vqlab_amd import vq_dense as VD
+    rng = np.random.default_rng(21)
+    m = make_module(rng, 1, 512, 2048, 4, 4096)
+    codes, cb, sc = to_device(m)
+    lin = VD.VQLinear(codes[0], cb, sc[0], group_size=64, pack_bits=12, in_features=2048)
+    x = _x(rng, 200, 2048, xdt)
+    y = lin(x[None])
+    assert y.shape == (1, 200, 512) and y.dtype == xdt
+    w = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], 64)
+    ref = vo.decode_matmul(_x16(x), w)
+    assert_close(_np(y[0]), ref, what=f"VQLinear {xdt}")
+    y8 = lin(x[:8])                                   # the GEMV side of the cutoff
+    assert_close(_np(y8), ref[:8], what="VQLinear gemv side")
+
+
+def test_dense_gemm_empty_and_refusals():
+    from vqlab_amd import _lib as L, _torch as Tt
+    rng = np.random.default_rng(22)
+    m = make_module(rng, 2, 128, 256, 4, 256)
+    codes, cb, sc = to_device(m)
+    keep = []
+    w = Tt.weights(codes, cb, sc, 64, 8, 256, keep=keep)
+    y = torch.empty((1, 128), dtype=torch.bfloat16, device="cuda")
+    x = torch.zeros((1, 256), dtype=torch.bfloat16, device="cuda")
+    # two experts: the dense GEMM takes exactly one linear
+    assert L.lib().vqk_dense_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, 1, Tt.ptr(y),
+                                  L.VQK_BF16, Tt.stream()) == L.VQK_EINVAL
+    w1 = Tt.weights(codes[0], cb, sc[0], 64, 8, 256, keep=keep)
+    assert L.lib().vqk_dense_gemm(ctypes.byref(w1), Tt.ptr(x), L.VQK_BF16, 0, Tt.ptr(y),
+                                  L.VQK_BF16, Tt.stream()) == L.VQK_OK
+
+
+# ------------------------------------------------------------ grouped GEMM
+def _routes(rng, T, k, E, lo=1, hi=8):
+    """Top-k ids per token (distinct within a token) drawn so that each
+    touched expert receives between lo and hi tokens where the draw allows."""
+    ids = np.zeros((T, k), np.int64)
+    load = np.zeros(E, np.int64)
+    for t in range(T):
+        w = np.where(load < hi, 1.0, 1e-6) * (1.0 + 4.0 * (load > 0) * (load < lo + 1))
+        ids[t] = rng.choice(E, k, replace=False, p=w / w.sum())
+        load[ids[t]] += 1
+    return ids
+
+
+@pytest.mark.parametrize("shape", [
+    # (T, k, E, OUT, IN, D, K): c4 rows (c3 layer, fewer experts), c2 rows
+    (64, 10, 40, 1024, 4096, 8, 16384),
+    (16, 10, 48, 4096, 1024, 8, 16384),
+    (64, 8, 32, 512, 2048, 4, 4096),
+    (40, 4, 16, 2048, 512, 4, 4096),
+])
+def test_grouped_gemm_shapes(shape):
+    from vqlab_amd import vq_switch as VS
+    T, k, E, OUT, IN, D, K = shape
+    print(f"grouped gemm {shape}", flush=True)
+    rng = np.random.default_rng(sum(shape))
+    m = make_module(rng, E, OUT, IN, D, K)
+    codes, cb, sc = to_device(m)
+    ids = _routes(rng, T, k, E).reshape(-1)
+    x = _x(rng, T, IN)
+    e = torch.from_numpy(ids.astype(np.int32)).cuda()
+    y = VS._gemmseg(x, e, codes, cb, sc, m["pack_bits"], IN, k)
+    assert y.shape == (T * k, OUT)
+    ref = vo.expert_gemv(_x16(x), ids, m["codes"], m["codebook"], m["scales"], 64, xkrep=k)
+    assert_close(_np(y), ref, what=f"grouped {shape}")
+    # the GEMV on the same pairs agrees to the same bar
+    yg = VS._fused(x, e, codes, cb, sc, pack_bits=m["pack_bits"], xkrep=k)
+    assert_close(_np(y), _np(yg), rtol=2e-2, atol=2e-3, what="grouped vs gemv")
+
+
+def test_grouped_gemm_skipzero_mtp_verify():
+    """The c4 case: MTP verify on the c3 layer format, 20 % of rows dead,
+    stored compact with a row table; dead rows give exact zeros."""
+    from vqlab_amd import vq_switch as VS
+    print("grouped gemm skipzero", flush=True)
+    rng = np.random.default_rng(23)
+    E, OUT, IN, T, k = 32, 1024, 4096, 16, 10
+    m = make_module(rng, E, OUT, IN, 8, 16384, dead_frac=0.2)
+    codes, cb, sc = to_device(m)
+    sz, rt = skipzero(m)
+    zc = torch.from_numpy(sz["sz_codes"].view(np.int32)).cuda()
+    zs = torch.from_numpy(sz["sz_scales"]).cuda()
+    rtd = torch.from_numpy(rt).cuda()
+    ids = _routes(rng, T, k, E).reshape(-1)
+    x = _x(rng, T, IN)
+    e = torch.from_numpy(ids.astype(np.int32)).cuda()
+    yc = VS._gemmseg(x, e, zc, cb, zs, 14, IN, k, rtd)
+    ye = VS._gemmseg(x, e, codes, cb, sc, 14, IN, k)
+    dead = rt[ids] < 0
+    assert dead.any() and (_np(yc)[dead] == 0).all()
+    assert torch.equal(yc[torch.from_numpy(~dead).cuda()], ye[torch.from_numpy(~dead).cuda()])
+    ref = vo.expert_gemv(_x16(x), ids, m["codes"], m["codebook"], m["scales"], 64, xkrep=k)
+    assert_close(_np(yc), ref, what="skipzero grouped")
+
+
+def test_grouped_gemm_sort_builds_oracle_tiles():
+    """Workspace after a call: order[] groups the pairs by expert exactly as
+    the oracle's stable argsort does (as sets within each segment) and the
+    tile records equal tile_meta(), including an id outside [0, E), whose
+    rows come out as zeros."""
+    from vqlab_amd import _lib as L, _torch as Tt
+    print("grouped gemm sort", flush=True)
+    rng = np.random.default_rng(24)
+    E, OUT, IN, N = 40, 256, 512, 700
+    m = make_module(rng, E, OUT, IN, 4, 256, packed=False)
+    codes, cb, sc = to_device(m)
+    ids = rng.integers(0, E, N).astype(np.int64)
+    ids[rng.integers(0, E, N) < 4] = 7                 # one expert with > 32 rows
+    ids[5] = E + 3                                      # outside [0, E)
+    x = _x(rng, N, IN, torch.float16)
+    e = torch.from_numpy(ids.astype(np.int32)).cuda()
+    keep = []
+    w = Tt.weights(codes, cb, sc, 64, 0, IN, keep=keep)
+    ws = ctypes.c_size_t()
+    L.check(L.lib().vqk_grouped_gemm_workspace(ctypes.byref(w), N, ctypes.byref(ws)))
+    work = torch.zeros(ws.value, dtype=torch.uint8, device="cuda")
+    y = torch.empty((N, OUT), dtype=torch.float32, device="cuda")
+    L.check(L.lib().vqk_grouped_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_F16, N, Tt.ptr(e), N, 1,
+                                     Tt.ptr(y), L.VQK_F32, Tt.ptr(work), ws.value, Tt.stream()))
+    torch.cuda.synchronize()
+    wb = work.cpu().numpy()
+    al = lambda v: (v + 255) & ~255
+    mt = (N + 31) // 32 + min(N, E + 1)
+    order = wb[:4 * N].view(np.int32)
+    tm = wb[al(4 * N):al(4 * N) + 12 * mt].view(np.int32).reshape(mt, 3)
+    nt = int(wb[al(4 * N) + al(12 * mt):][:4].view(np.int32)[0])
+    valid = ids < E
+    ro, _, _, rs = vo.sort_routing(np.where(valid, ids, E), 1)
+    ref_tm = vo.tile_meta(rs[rs < E], E, 32)
+    assert nt == len(ref_tm) + 1                        # + one tile for the bad id
+    assert np.array_equal(tm[:len(ref_tm)], ref_tm)
+    assert tuple(tm[len(ref_tm)]) == (-1, N - 1, 1)
+    starts = np.concatenate([[0], np.cumsum(np.bincount(rs, minlength=E + 1))])
+    for ex in range(E + 1):                          # one segment per expert (+ bad ids)
+        a, b = starts[ex], starts[ex + 1]
+        assert sorted(order[a:b]) == sorted(ro[a:b])
+    yn = _np(y)
+    assert (yn[5] == 0).all()
+    ref = vo.expert_gemv(x.float().cpu().numpy()[valid], ids[valid], m["codes"], m["codebook"],
+                         m["scales"], 64)
+    assert_close(yn[valid], ref, what="sort case")
+
+
+def test_grouped_gemm_errors():
+    from vqlab_amd import _lib as L, _torch as Tt
+    rng = np.random.default_rng(25)
+    m = make_module(rng, 4, 128, 256, 4, 256)
+    codes, cb, sc = to_device(m)
+    keep = []
+    w = Tt.weights(codes, cb, sc, 64, 8, 256, keep=keep)
+    x = torch.zeros((4, 256), dtype=torch.bfloat16, device="cuda")
+    e = torch.zeros(8, dtype=torch.int32, device="cuda")
+    y = torch.empty((8, 128), dtype=torch.bfloat16, device="cuda")
+    ws = ctypes.c_size_t()
+    L.check(L.lib().vqk_grouped_gemm_workspace(ctypes.byref(w), 8, ctypes.byref(ws)))
+    work = torch.empty(ws.value, dtype=torch.uint8, device="cuda")
+    lib = L.lib()
+    assert lib.vqk_grouped_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, 4, Tt.ptr(e), 8, 2,
+                                Tt.ptr(y), L.VQK_BF16, Tt.ptr(work), ws.value - 1,
+                                Tt.stream()) == L.VQK_ENOSPACE
+    assert lib.vqk_grouped_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, 4, Tt.ptr(e), 8, 3,
+                                Tt.ptr(y), L.VQK_BF16, Tt.ptr(work), ws.value,
+                                Tt.stream()) == L.VQK_EINVAL
+    assert lib.vqk_grouped_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, 4, Tt.ptr(e), 8, 2,
+                                Tt.ptr(y), L.VQK_BF16, Tt.ptr(work), ws.value,
+                                Tt.stream()) == L.VQK_OK
+
+
+def test_switch_linear_prefill_takes_grouped_gemm():
+    """N > VQ_FUSED_MAX_N pairs: VQSwitchLinear runs the grouped GEMM."""
+    from vqlab_amd import vq_switch as VS
+    print("switch linear prefill", flush=True)
+    rng = np.random.default_rng(26)
+    E, OUT, IN, T, k = 16, 256, 1024, 80, 8
+    m = make_module(rng, E, OUT, IN, 4, 4096)
+    codes, cb, sc = to_device(m)
+    mod = VS.VQSwitchLinear(codes, cb, sc, pack_bits=12, in_features=IN)
+    assert VS.gemmseg_fits(4, 4096, 64, 12, IN)
+    ids = _routes(rng, T, k, E)
+    x = _x(rng, T, IN)
+    idx = torch.from_numpy(ids.astype(np.int32)).cuda()
+    y = mod(x[:, None, None, :], idx)
+    assert y.shape == (T, k, 1, OUT)
+    ref = vo.expert_gemv(_x16(x), ids.reshape(-1), m["codes"], m["codebook"], m["scales"], 64,
+                         xkrep=k)
+    assert_close(_np(y).reshape(T * k, OUT), ref, what="prefill module")

@@ -1,0 +1,461 @@
+// Matrix-core VQ GEMMs: the large-N paths.
+//
+//   vqk_dense_gemm     _decode_matmul (vq_dense.py:262-312): y = x . W^T, E = 1
+//   vqk_grouped_gemm   _gemmseg_prefill (vq_switch.py:4569-4722): routed pairs
+//                      count-sorted by expert on device, one tile per <= BM
+//                      rows of an expert segment (the reference's tmeta,
+//                      vq_switch.py:4590-4610), results in caller order
+//
+// Each workgroup owns a BM x BN output tile. Per K-step of 64 input columns it
+// stages the x rows (fp16) and DECODES the matching 64-column slice of BN
+// weight rows into LDS -- W[o, k] = fp16(f32(cb[c]) * f32(s)), the bit-exact
+// dequant -- then runs v_mfma_f32_32x32x16_f16 over the two tiles with fp32
+// accumulation. No fp16 weight is ever materialised in HBM. Operand layout
+// (checked on gfx950): lane l feeds A[l%32][8*(l/32) .. +8] and
+// B[8*(l/32) .. +8][l%32]; accumulator register i holds row
+// 8*(i/4) + 4*(l/32) + i%4, column l%32.
+#include "vqk_gemv.h"
+#include "vqk_internal.h"
+
+namespace vqk {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBK = 64;             // input columns per K-step (one 64-weight scale group)
+constexpr int kLdsStride = kBK + 8; // halves per staged row (16 B skew)
+
+struct GemmParams {
+    const void *codes;
+    int64_t code_cols;      // row stride in code units (u32 words when packed)
+    int32_t bits;           // packed width, 0 = unpacked
+    int32_t code_bytes;     // 1 / 2 when unpacked
+    const uint16_t *codebook;
+    int32_t K;
+    const uint16_t *scales;
+    int32_t ngrp, G;
+    const int32_t *row_table;
+    int64_t stored_rows;
+    int32_t E, OUT, IN, NSUB;
+    const void *x;
+    int32_t x_type, xkrep;
+    void *y;
+    int32_t y_type;
+    int32_t N;              // dense: rows of x; grouped: pairs
+    const int32_t *tmeta;   // grouped: [max_tiles, 3] (expert or -1, row_start, nrows)
+    const int32_t *ntiles;  // grouped: tiles actually built
+    const int32_t *order;   // grouped: sorted position -> pair index
+    const uint32_t *eidx;   // grouped: expert of each pair
+};
+
+__device__ __forceinline__ uint32_t gemm_code(const GemmParams &p, int64_t cr, int j) {
+    if (p.bits) {
+        const uint32_t *row = static_cast<const uint32_t *>(p.codes) + cr * p.code_cols;
+        const int64_t bit = int64_t(j >> 5) * (int64_t(kBlock) * p.bits) + (j & 31) * p.bits;
+        const int sh = int(bit & 31);
+        uint32_t v = row[bit >> 5] >> sh;
+        if (sh + p.bits > 32) v |= row[(bit >> 5) + 1] << (32 - sh);
+        return v & ((1u << p.bits) - 1u);
+    }
+    if (p.code_bytes == 1) return static_cast<const uint8_t *>(p.codes)[cr * p.code_cols + j];
+    return static_cast<const uint16_t *>(p.codes)[cr * p.code_cols + j];
+}
+
+// BM x BN output tile, WM x WN waves, each wave (BM/WM) x (BN/WN) = TM x TN
+// MFMA 32x32 tiles. CBL: codebook staged in LDS (K*D*2 bytes, dynamic).
+template <int D, bool CBL, int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN) k_vq_gemm(const GemmParams p) {
+    constexpr int NT = 64 * WM * WN;
+    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+    constexpr int CPR = kBK / D;                      // codes per weight row per K-step
+    static_assert(TM >= 1 && TN >= 1, "tile too small for the wave grid");
+    extern __shared__ __align__(16) uint8_t smem[];
+    f16 *As = reinterpret_cast<f16 *>(smem);                         // [BM][kLdsStride]
+    f16 *Bs = As + BM * kLdsStride;                                  // [BN][kLdsStride]
+    uint16_t *cbs = reinterpret_cast<uint16_t *>(Bs + BN * kLdsStride);  // [K][D] if CBL
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int o0 = int(blockIdx.x) * BN;
+
+    // ---- the row block of this tile
+    int expert, row0, nrows;
+    const bool grouped = p.tmeta != nullptr;
+    if (grouped) {
+        if (int(blockIdx.y) >= *p.ntiles) return;                   // uniform: no barrier passed yet
+        const int32_t *tm = p.tmeta + 3 * blockIdx.y;
+        expert = tm[0];
+        row0 = tm[1];
+        nrows = tm[2];
+    } else {
+        expert = 0;
+        row0 = int(blockIdx.y) * BM;
+        nrows = min(BM, p.N - row0);
+    }
+    if constexpr (CBL) {
+        lds_copy_async(p.codebook, cbs, p.K * D * 2, p.K * D * 2);
+        wait_vmem();
+        __syncthreads();
+    }
+    const uint16_t *cb = CBL ? cbs : p.codebook;
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) acc[a][b] = f32x16{};
+
+    // x row (element offset) of tile row m, or -1
+    auto xrow = [&](int m) -> int64_t {
+        if (m >= nrows) return -1;
+        if (!grouped) return int64_t(row0 + m) * p.IN;
+        const int pair = p.order[row0 + m];
+        return int64_t(pair / p.xkrep) * p.IN;
+    };
+    // code row of weight row o of this tile's expert, or -1 (dead / outside)
+    auto wrow = [&](int o) -> int64_t {
+        if (expert < 0 || o >= p.OUT) return -1;
+        int64_t f = int64_t(expert) * p.OUT + o;
+        if (p.row_table) f = p.row_table[f];
+        return f < p.stored_rows ? f : -1;
+    };
+
+    for (int k0 = 0; k0 < p.IN; k0 += kBK) {
+        // ---- stage x: BM rows x 64 columns, 8 values per thread per round
+        for (int c = tid; c < BM * (kBK / 8); c += NT) {
+            const int m = c / (kBK / 8), kc = (c % (kBK / 8)) * 8;
+            const int64_t base = xrow(m);
+            u32x4 v = {0, 0, 0, 0};
+            if (base >= 0) {
+                if (k0 + kc + 8 <= p.IN && ((reinterpret_cast<uintptr_t>(p.x) +
+                                             uint64_t(base + k0 + kc) * (p.x_type == VQK_F32 ? 4 : 2)) & 15) == 0) {
+                    v = load8_act(p.x, p.x_type, base + k0 + kc);
+                } else {
+                    uint16_t h[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        h[u] = k0 + kc + u < p.IN ? f32_to_h(load_act(p.x, p.x_type, base + k0 + kc + u)) : 0;
+                    v = u32x4{uint32_t(h[0]) | (uint32_t(h[1]) << 16), uint32_t(h[2]) | (uint32_t(h[3]) << 16),
+                              uint32_t(h[4]) | (uint32_t(h[5]) << 16), uint32_t(h[6]) | (uint32_t(h[7]) << 16)};
+                }
+            }
+            *reinterpret_cast<u32x4 *>(As + m * kLdsStride + kc) = v;
+        }
+        // ---- decode W: BN rows x CPR codes, D halves each, bit-exact dequant
+        for (int c = tid; c < BN * CPR; c += NT) {
+            const int r = c / CPR, jj = c % CPR;
+            const int j = k0 / D + jj;
+            const int64_t cr = wrow(o0 + r);
+            uint16_t h[D];
+            if (cr >= 0 && j < p.NSUB) {
+                const uint32_t code = min(gemm_code(p, cr, j), uint32_t(p.K - 1));
+                const float s = h_to_f32(p.scales[cr * p.ngrp + (j * D) / p.G]);
+                const uint16_t *e = cb + int64_t(code) * D;
+#pragma unroll
+                for (int u = 0; u < D; ++u) h[u] = f32_to_h(s * h_to_f32(e[u]));
+            } else {
+#pragma unroll
+                for (int u = 0; u < D; ++u) h[u] = 0;
+            }
+            f16 *dst = Bs + r * kLdsStride + jj * D;
+            if constexpr (D == 2) {
+                *reinterpret_cast<uint32_t *>(dst) = uint32_t(h[0]) | (uint32_t(h[1]) << 16);
+            } else if constexpr (D == 4) {
+                *reinterpret_cast<u32x2 *>(dst) = u32x2{uint32_t(h[0]) | (uint32_t(h[1]) << 16),
+                                                         uint32_t(h[2]) | (uint32_t(h[3]) << 16)};
+            } else {
+                *reinterpret_cast<u32x4 *>(dst) = u32x4{uint32_t(h[0]) | (uint32_t(h[1]) << 16),
+                                                         uint32_t(h[2]) | (uint32_t(h[3]) << 16),
+                                                         uint32_t(h[4]) | (uint32_t(h[5]) << 16),
+                                                         uint32_t(h[6]) | (uint32_t(h[7]) << 16)};
+            }
+        }
+        __syncthreads();
+        // ---- matrix cores: 4 sub-steps of 16 columns
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 16) {
+            h8 af[TM], bf[TN];
+            const int kof = kk + (lane >> 5) * 8;
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                const int m = (wm * TM + a) * 32 + (lane & 31);
+                af[a] = *reinterpret_cast<const h8 *>(As + m * kLdsStride + kof);
+            }
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                const int n = (wn * TN + b) * 32 + (lane & 31);
+                bf[b] = *reinterpret_cast<const h8 *>(Bs + n * kLdsStride + kof);
+            }
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int b = 0; b < TN; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: rows back to caller order
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int m = (wm * TM + a) * 32 + (i / 4) * 8 + (lane >> 5) * 4 + (i % 4);
+            if (m >= nrows) continue;
+            const int64_t yr = grouped ? int64_t(p.order[row0 + m]) : int64_t(row0 + m);
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                const int o = o0 + (wn * TN + b) * 32 + (lane & 31);
+                if (o < p.OUT) store_act(p.y, p.y_type, yr * p.OUT + o, acc[a][b][i]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- sorting
+// One workgroup: histogram of the pairs' experts (bucket E = ids outside
+// [0, E): their rows decode to zero), exclusive scans of the counts and of
+// the tile counts, scatter of pair indices into expert order, and one
+// (expert, row_start, nrows) record per tile of <= BM rows, experts ascending
+// (the reference's tile metadata, vq_switch.py:4590-4610). Within an expert
+// the order of pairs follows the atomics; every output row is computed
+// independently, so the results do not depend on it.
+constexpr int kSortThreads = 1024;
+
+__device__ __forceinline__ void block_exclusive_scan(int *a, int n, int *tmp) {
+    // a[0..n) in LDS, n <= 4 * kSortThreads; tmp has kSortThreads ints
+    const int tid = threadIdx.x;
+    const int per = (n + kSortThreads - 1) / kSortThreads;
+    int local = 0;
+    for (int i = 0; i < per; ++i) {
+        const int k = tid * per + i;
+        if (k < n) local += a[k];
+    }
+    tmp[tid] = local;
+    __syncthreads();
+    for (int off = 1; off < kSortThreads; off <<= 1) {
+        const int v = tid >= off ? tmp[tid - off] : 0;
+        __syncthreads();
+        tmp[tid] += v;
+        __syncthreads();
+    }
+    int run = tmp[tid] - local;                 // exclusive prefix of this thread's chunk
+    for (int i = 0; i < per; ++i) {
+        const int k = tid * per + i;
+        if (k < n) {
+            const int v = a[k];
+            a[k] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(kSortThreads) k_group_sort(const uint32_t *eidx, int N, int E,
+                                                             int BM, int max_tiles, int32_t *order,
+                                                             int32_t *tmeta, int32_t *ntiles) {
+    extern __shared__ int sh[];
+    const int NBK = E + 1;
+    int *cnt = sh;                 // [NBK] counts, then starts
+    int *tls = cnt + NBK;          // [NBK] tiles per bucket, then tile starts
+    int *cur = tls + NBK;          // [NBK] scatter cursors
+    int *tmp = cur + NBK;          // [kSortThreads]
+    const int tid = threadIdx.x;
+    for (int b = tid; b < NBK; b += kSortThreads) cnt[b] = 0;
+    __syncthreads();
+    for (int n = tid; n < N; n += kSortThreads) {
+        const uint32_t e = eidx[n];
+        atomicAdd(&cnt[e < uint32_t(E) ? int(e) : E], 1);
+    }
+    __syncthreads();
+    for (int b = tid; b < NBK; b += kSortThreads) tls[b] = (cnt[b] + BM - 1) / BM;
+    __syncthreads();
+    // keep the counts: cur = counts for now
+    for (int b = tid; b < NBK; b += kSortThreads) cur[b] = cnt[b];
+    __syncthreads();
+    block_exclusive_scan(cnt, NBK, tmp);       // cnt -> bucket starts
+    block_exclusive_scan(tls, NBK, tmp);       // tls -> tile starts
+    for (int b = tid; b < NBK; b += kSortThreads) {
+        const int c = cur[b];
+        const int nt = (c + BM - 1) / BM;
+        for (int t = 0; t < nt; ++t) {
+            const int ti = tls[b] + t;
+            if (ti < max_tiles) {
+                tmeta[3 * ti + 0] = b < E ? b : -1;
+                tmeta[3 * ti + 1] = cnt[b] + t * BM;
+                tmeta[3 * ti + 2] = min(BM, c - t * BM);
+            }
+        }
+        if (b == NBK - 1) *ntiles = min(max_tiles, tls[b] + nt);
+    }
+    __syncthreads();
+    for (int b = tid; b < NBK; b += kSortThreads) cur[b] = cnt[b];
+    __syncthreads();
+    for (int n = tid; n < N; n += kSortThreads) {
+        const uint32_t e = eidx[n];
+        const int pos = atomicAdd(&cur[e < uint32_t(E) ? int(e) : E], 1);
+        order[pos] = n;
+    }
+}
+
+// ---------------------------------------------------------------- host
+constexpr int kGroupBM = 32, kGroupBN = 128;
+constexpr int kDenseBM = 128, kDenseBN = 128;
+constexpr int kMaxSortExperts = 4096;
+
+static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
+
+static int64_t group_max_tiles(int64_t N, int64_t E) {
+    return (N + kGroupBM - 1) / kGroupBM + (N < E + 1 ? N : E + 1);
+}
+
+static int fill_gemm(const vqk_weights *w, const Geom &g, GemmParams *p) {
+    memset(p, 0, sizeof *p);
+    p->codes = w->codes;
+    p->code_cols = w->code_cols;
+    p->bits = g.packed ? g.BITS : 0;
+    p->code_bytes = g.packed ? 4 : g.BITS / 8;
+    p->codebook = w->codebook;
+    p->K = int32_t(g.K);
+    p->scales = w->scales;
+    p->ngrp = int32_t(g.NGRP);
+    p->G = g.G;
+    p->row_table = w->row_table;
+    p->stored_rows = g.rows;
+    p->E = int32_t(g.E);
+    p->OUT = int32_t(g.OUT);
+    p->IN = int32_t(g.IN);
+    p->NSUB = int32_t(g.NSUB);
+    if (g.OUT > INT32_MAX || g.IN > INT32_MAX) return set_error(VQK_ENOTIMPL, "shape too large");
+    return VQK_OK;
+}
+
+template <int D, bool CBL, int BM, int BN, int WM, int WN>
+static int go_gemm(const GemmParams &p, dim3 grid, size_t smem, hipStream_t st) {
+    return launch_with_lds<k_vq_gemm<D, CBL, BM, BN, WM, WN>>(grid, dim3(64 * WM * WN), smem, st, p);
+}
+
+template <int BM, int BN, int WM, int WN>
+static int launch_gemm(const GemmParams &p, const Geom &g, dim3 grid, hipStream_t st) {
+    const bool cbl = g.K * g.D * 2 <= kCbLdsMax &&
+                     (reinterpret_cast<uintptr_t>(p.codebook) & 15) == 0 && (g.K * g.D * 2) % 4 == 0;
+    const size_t smem = size_t(BM + BN) * kLdsStride * 2 + (cbl ? size_t(g.K) * g.D * 2 : 0);
+    switch (g.D) {
+        case 2: return cbl ? go_gemm<2, true, BM, BN, WM, WN>(p, grid, smem, st)
+                           : go_gemm<2, false, BM, BN, WM, WN>(p, grid, smem, st);
+        case 4: return cbl ? go_gemm<4, true, BM, BN, WM, WN>(p, grid, smem, st)
+                           : go_gemm<4, false, BM, BN, WM, WN>(p, grid, smem, st);
+        default: return cbl ? go_gemm<8, true, BM, BN, WM, WN>(p, grid, smem, st)
+                            : go_gemm<8, false, BM, BN, WM, WN>(p, grid, smem, st);
+    }
+}
+
+static int check_acts(const void *x, int32_t x_type, const void *y, int32_t y_type) {
+    if (!act_size(x_type) || !act_size(y_type))
+        return set_error(VQK_EINVAL, "x/y type must be VQK_F16, VQK_BF16 or VQK_F32");
+    if (!x || !y) return set_error(VQK_EINVAL, "x and y are required");
+    return VQK_OK;
+}
+
+}  // namespace vqk
+
+using namespace vqk;
+
+extern "C" {
+
+int vqk_gemmseg_fits(int32_t D, int64_t K, int32_t G, int32_t pack_bits, int64_t IN) {
+    return (D == 2 || D == 4 || D == 8) && K >= 1 && K <= 65536 && G > 0 && G % D == 0 &&
+           IN > 0 && IN % G == 0 && IN % D == 0 && pack_bits >= 0 && pack_bits <= 16;
+}
+
+int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_t N, void *y,
+                   int32_t y_type, void *stream) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if (g.E != 1) return set_error(VQK_EINVAL, "dense GEMM takes one linear (E=1), got E=%lld",
+                                   (long long)g.E);
+    if ((rc = check_acts(x, x_type, y, y_type))) return rc;
+    if (N < 0 || N > INT32_MAX) return set_error(VQK_EINVAL, "N=%lld", (long long)N);
+    if (N == 0) return VQK_OK;
+    GemmParams p;
+    if ((rc = fill_gemm(w, g, &p))) return rc;
+    p.x = x;
+    p.x_type = x_type;
+    p.xkrep = 1;
+    p.y = y;
+    p.y_type = y_type;
+    p.N = int32_t(N);
+    const int64_t gy = (N + kDenseBM - 1) / kDenseBM;
+    const dim3 grid(unsigned((g.OUT + kDenseBN - 1) / kDenseBN), 1, 1);
+    for (int64_t y0 = 0; y0 < gy; y0 += 65535) {
+        // rows are addressed through blockIdx.y; split huge N into launches
+        GemmParams q = p;
+        const int64_t rows0 = y0 * kDenseBM;
+        q.x = static_cast<const uint8_t *>(x) + rows0 * g.IN * act_size(x_type);
+        q.y = static_cast<uint8_t *>(y) + rows0 * g.OUT * act_size(y_type);
+        q.N = int32_t((N - rows0) < int64_t(65535) * kDenseBM ? (N - rows0) : int64_t(65535) * kDenseBM);
+        const dim3 gr(grid.x, unsigned((q.N + kDenseBM - 1) / kDenseBM), 1);
+        rc = launch_gemm<kDenseBM, kDenseBN, 2, 2>(q, g, gr, hipStream_t(stream));
+        if (rc) return rc;
+    }
+    return VQK_OK;
+}
+
+int vqk_grouped_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if (!bytes || N < 0) return set_error(VQK_EINVAL, "bad arguments");
+    const int64_t mt = group_max_tiles(N, g.E);
+    *bytes = al256(sizeof(int32_t) * size_t(N)) + al256(sizeof(int32_t) * 3 * size_t(mt)) + 256;
+    return VQK_OK;
+}
+
+int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
+                     const uint32_t *eidx, int64_t N, int64_t xkrep, void *y, int32_t y_type,
+                     void *workspace, size_t ws_bytes, void *stream) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if ((rc = check_acts(x, x_type, y, y_type))) return rc;
+    if (!eidx && N > 0) return set_error(VQK_EINVAL, "eidx is required");
+    if (N < 0 || T < 0 || xkrep < 1 || N != T * xkrep)
+        return set_error(VQK_EINVAL, "pairs N=%lld must equal tokens T=%lld x xkrep=%lld",
+                         (long long)N, (long long)T, (long long)xkrep);
+    if (N > INT32_MAX / 2) return set_error(VQK_ENOTIMPL, "N=%lld pairs is too many", (long long)N);
+    if (g.E > kMaxSortExperts)
+        return set_error(VQK_ENOTIMPL, "grouped GEMM sorts at most %d experts", kMaxSortExperts);
+    size_t need = 0;
+    vqk_grouped_gemm_workspace(w, N, &need);
+    if (!workspace || ws_bytes < need)
+        return set_error(VQK_ENOSPACE, "workspace %zu B < %zu B", ws_bytes, need);
+    if (N == 0) return VQK_OK;
+    const int64_t mt = group_max_tiles(N, g.E);
+    if (mt > 65535) return set_error(VQK_ENOTIMPL, "%lld tiles exceed one launch", (long long)mt);
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    int32_t *order = reinterpret_cast<int32_t *>(ws);
+    int32_t *tmeta = reinterpret_cast<int32_t *>(ws + al256(sizeof(int32_t) * size_t(N)));
+    int32_t *ntiles = reinterpret_cast<int32_t *>(ws + al256(sizeof(int32_t) * size_t(N)) +
+                                                  al256(sizeof(int32_t) * 3 * size_t(mt)));
+    hipStream_t st = hipStream_t(stream);
+    const size_t sort_lds = sizeof(int) * (3 * size_t(g.E + 1) + kSortThreads);
+    hipLaunchKernelGGL(k_group_sort, dim3(1), dim3(kSortThreads), sort_lds, st, eidx, int(N),
+                       int(g.E), kGroupBM, int(mt), order, tmeta, ntiles);
+    if ((rc = hip_status(hipGetLastError(), "group sort launch"))) return rc;
+    GemmParams p;
+    if ((rc = fill_gemm(w, g, &p))) return rc;
+    p.x = x;
+    p.x_type = x_type;
+    p.xkrep = int32_t(xkrep);
+    p.y = y;
+    p.y_type = y_type;
+    p.N = int32_t(N);
+    p.tmeta = tmeta;
+    p.ntiles = ntiles;
+    p.order = order;
+    p.eidx = eidx;
+    const dim3 grid(unsigned((g.OUT + kGroupBN - 1) / kGroupBN), unsigned(mt), 1);
+    return launch_gemm<kGroupBM, kGroupBN, 1, 4>(p, g, grid, st);
+}
+
+}  // extern "C"
