@@ -183,13 +183,13 @@ def test_grouped_gemm_sort_builds_oracle_tiles():
     torch.cuda.synchronize()
     wb = work.cpu().numpy()
     al = lambda v: (v + 255) & ~255
-    mt = (N + 31) // 32 + min(N, E + 1)
+    mt = (N + 15) // 16 + min(N, E + 1)                 # tiles of <= 16 rows
     order = wb[:4 * N].view(np.int32)
     tm = wb[al(4 * N):al(4 * N) + 12 * mt].view(np.int32).reshape(mt, 3)
     nt = int(wb[al(4 * N) + al(12 * mt):][:4].view(np.int32)[0])
     valid = ids < E
     ro, _, _, rs = vo.sort_routing(np.where(valid, ids, E), 1)
-    ref_tm = vo.tile_meta(rs[rs < E], E, 32)
+    ref_tm = vo.tile_meta(rs[rs < E], E, 16)
     assert nt == len(ref_tm) + 1                        # + one tile for the bad id
     assert np.array_equal(tm[:len(ref_tm)], ref_tm)
     assert tuple(tm[len(ref_tm)]) == (-1, N - 1, 1)

@@ -15,6 +15,7 @@
 // B[8*(l/32) .. +8][l%32]; accumulator register i holds row
 // 8*(i/4) + 4*(l/32) + i%4, column l%32.
 #include "vqk_gemv.h"
+#include "vqk_gseg.h"
 #include "vqk_internal.h"
 
 namespace vqk {
@@ -298,14 +299,54 @@ __global__ void __launch_bounds__(kSortThreads) k_group_sort(const uint32_t *eid
 }
 
 // ---------------------------------------------------------------- host
-constexpr int kGroupBM = 32, kGroupBN = 128;
+constexpr int kGroupBM = 32, kGroupBN = 128;   // fallback tile kernel (tiles hold <= kSegTok rows)
 constexpr int kDenseBM = 128, kDenseBN = 128;
 constexpr int kMaxSortExperts = 4096;
+constexpr int kSegDenseMaxN = 64;               // dense rows up to which the segment kernel runs
 
 static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// Tiles of <= kSegTok sorted rows: sum over experts of ceil(count / kSegTok)
+// is at most ceil(N / kSegTok) + (non-empty buckets).
 static int64_t group_max_tiles(int64_t N, int64_t E) {
-    return (N + kGroupBM - 1) / kGroupBM + (N < E + 1 ? N : E + 1);
+    return (N + kSegTok - 1) / kSegTok + (N < E + 1 ? N : E + 1);
+}
+
+// The register-decode segment kernel covers whole 32-code blocks per row
+// (rows of NB * BITS words), BITS 2..16, the GEMV's scale-group layouts and
+// 16-byte aligned codebook and activations.
+static bool seg_fits(const Geom &g, const vqk_weights *w, const void *x) {
+    const int gpb_fast = g.D == 4 ? 2 : (g.D == 8 ? 4 : 1);
+    return (g.D == 2 || g.D == 4 || g.D == 8) && g.NSUB % kBlock == 0 && g.row_words > 0 &&
+           g.row_words == g.NB * g.BITS && g.BITS >= 2 && g.BITS <= 16 &&
+           (g.gpb == 1 || g.gpb == gpb_fast) && g.IN <= INT32_MAX && g.OUT <= INT32_MAX &&
+           (reinterpret_cast<uintptr_t>(w->codebook) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+}
+
+static void fill_seg(const vqk_weights *w, const Geom &g, SegParams *p) {
+    memset(p, 0, sizeof *p);
+    p->codes = static_cast<const uint32_t *>(w->codes);
+    p->row_words = g.row_words;
+    p->codebook = w->codebook;
+    p->K = int32_t(g.K);
+    p->scales = w->scales;
+    p->ngrp = int32_t(g.NGRP);
+    p->bpg = g.bpg;
+    p->row_table = w->row_table;
+    p->stored_rows = g.rows;
+    p->E = int32_t(g.E);
+    p->OUT = int32_t(g.OUT);
+    p->IN = int32_t(g.IN);
+    p->NB = int32_t(g.NB);
+}
+
+static int launch_seg(const SegParams &p, const Geom &g, dim3 grid, hipStream_t st) {
+    switch (g.D) {
+        case 2: return launch_seg_d2(p, g.BITS, g.gpb, grid, st);
+        case 4: return launch_seg_d4(p, g.BITS, g.gpb, grid, st);
+        default: return launch_seg_d8(p, g.BITS, g.gpb, grid, st);
+    }
 }
 
 static int fill_gemm(const vqk_weights *w, const Geom &g, GemmParams *p) {
@@ -377,6 +418,19 @@ int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_t 
     if ((rc = check_acts(x, x_type, y, y_type))) return rc;
     if (N < 0 || N > INT32_MAX) return set_error(VQK_EINVAL, "N=%lld", (long long)N);
     if (N == 0) return VQK_OK;
+    if (N <= kSegDenseMaxN && seg_fits(g, w, x)) {
+        SegParams sp;
+        fill_seg(w, g, &sp);
+        sp.x = x;
+        sp.x_type = x_type;
+        sp.xkrep = 1;
+        sp.y = y;
+        sp.y_type = y_type;
+        sp.N = int32_t(N);
+        const dim3 grid(unsigned((g.OUT + kSegRows - 1) / kSegRows),
+                        unsigned((N + kSegTok - 1) / kSegTok), 1);
+        return launch_seg(sp, g, grid, hipStream_t(stream));
+    }
     GemmParams p;
     if ((rc = fill_gemm(w, g, &p))) return rc;
     p.x = x;
@@ -440,8 +494,23 @@ int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_
     hipStream_t st = hipStream_t(stream);
     const size_t sort_lds = sizeof(int) * (3 * size_t(g.E + 1) + kSortThreads);
     hipLaunchKernelGGL(k_group_sort, dim3(1), dim3(kSortThreads), sort_lds, st, eidx, int(N),
-                       int(g.E), kGroupBM, int(mt), order, tmeta, ntiles);
+                       int(g.E), kSegTok, int(mt), order, tmeta, ntiles);
     if ((rc = hip_status(hipGetLastError(), "group sort launch"))) return rc;
+    if (seg_fits(g, w, x)) {
+        SegParams sp;
+        fill_seg(w, g, &sp);
+        sp.x = x;
+        sp.x_type = x_type;
+        sp.xkrep = int32_t(xkrep);
+        sp.y = y;
+        sp.y_type = y_type;
+        sp.N = int32_t(N);
+        sp.tmeta = tmeta;
+        sp.ntiles = ntiles;
+        sp.order = order;
+        const dim3 grid(unsigned((g.OUT + kSegRows - 1) / kSegRows), unsigned(mt), 1);
+        return launch_seg(sp, g, grid, st);
+    }
     GemmParams p;
     if ((rc = fill_gemm(w, g, &p))) return rc;
     p.x = x;

@@ -1,0 +1,288 @@
+// Register-decode matrix-core kernel for expert segments (and small dense
+// batches): y[t, o] = sum_i x[t, i] * W[o, i] for up to 16 tokens t that share
+// one expert's weight rows o.
+//
+// No weight tile passes through LDS. v_mfma_f32_16x16x32_f16 takes its A
+// operand as 8 consecutive k values of one row per lane (lane l: row l % 16,
+// k group l / 16), which for d = 8 is exactly one codebook entry. So each
+// lane owns one 32-code packing block of a weight row (its BITS words and
+// scales in registers, as in the GEMV), and per MFMA step decodes the next
+// 8 weights straight into its A operand:
+//     W[8] = cb[code] * s          (v_pk_mul_f16: the exact product of two fp16
+//                                   values rounded once to fp16, i.e. the
+//                                   bit-exact dequant fp16(f32(cb) * f32(s)))
+// The lane groups g = 0..3 hold blocks 4*sb + g of the same row, and the
+// B operand (x) of lane (token t, group g) is read from the matching columns
+// of an LDS copy of the tokens' activations, so A and B use the same k
+// permutation and the product is the plain dot product.
+//
+// Workgroup = 4 waves x 2 row tiles of 16 = 128 weight rows; one token tile
+// of <= 16 rows (grouped: one tile of an expert segment from the device
+// sort, vq_switch.py:4590-4610; dense: 16 consecutive rows of x). The K loop
+// walks supersteps of 4 blocks per row (128 * D columns); the x columns of
+// the next superstep and the next blocks' words are loaded while the
+// current superstep runs, and one barrier per superstep publishes the
+// double-buffered x chunk.
+#pragma once
+
+#include "vqk_gemv.h"
+
+namespace vqk {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct SegParams {
+    const uint32_t *codes;     // code rows as 32-code blocks of BITS words
+    int64_t row_words;         // words per code row (NB * BITS)
+    const uint16_t *codebook;  // fp16 [K, D]
+    int32_t K;
+    const uint16_t *scales;    // fp16, ngrp per code row
+    int32_t ngrp, bpg;         // bpg: blocks per scale group when GPB == 1
+    const int32_t *row_table;  // [E, OUT] or NULL
+    int64_t stored_rows;
+    int32_t E, OUT, IN, NB;
+    const void *x;
+    int32_t x_type, xkrep;
+    void *y;
+    int32_t y_type;
+    int32_t N;                 // dense: rows of x; grouped: pairs
+    const int32_t *tmeta;      // grouped: (expert or -1, row_start, nrows) per tile
+    const int32_t *ntiles;     // grouped: tiles built by the sort
+    const int32_t *order;      // grouped: sorted position -> pair
+};
+
+constexpr int kSegRows = 128;      // weight rows per workgroup
+constexpr int kSegTok = 16;        // tokens per tile
+
+// Entry D halves of a table (LDS or global) as 8 halves: d8 one entry,
+// d4 two, d2 four (the codes of one MFMA step).
+template <int D, int BITS>
+__device__ __forceinline__ h8 step_entries(const uint32_t (&w)[BITS], int s, const f16 *tab,
+                                           uint32_t kmax, bool clamp) {
+    if constexpr (D == 8) {
+        uint32_t c = block_field<BITS>(w, s);
+        if (clamp) c = min(c, kmax);
+        return *reinterpret_cast<const h8 *>(tab + c * 8);
+    } else if constexpr (D == 4) {
+        uint32_t c0 = block_field<BITS>(w, 2 * s), c1 = block_field<BITS>(w, 2 * s + 1);
+        if (clamp) { c0 = min(c0, kmax); c1 = min(c1, kmax); }
+        const h4 a = *reinterpret_cast<const h4 *>(tab + c0 * 4);
+        const h4 b = *reinterpret_cast<const h4 *>(tab + c1 * 4);
+        return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    } else {
+        uint32_t c[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            c[u] = block_field<BITS>(w, 4 * s + u);
+            if (clamp) c[u] = min(c[u], kmax);
+        }
+        const h2 a = *reinterpret_cast<const h2 *>(tab + c[0] * 2);
+        const h2 b = *reinterpret_cast<const h2 *>(tab + c[1] * 2);
+        const h2 e = *reinterpret_cast<const h2 *>(tab + c[2] * 2);
+        const h2 f = *reinterpret_cast<const h2 *>(tab + c[3] * 2);
+        return h8{a[0], a[1], b[0], b[1], e[0], e[1], f[0], f[1]};
+    }
+}
+
+// A zero entry for lanes without a block (dead row, past the row's end):
+// their codes read 0 from here and their scale is 0, so their weights are +0.
+static __device__ __align__(16) const uint16_t kSegZeroEntry[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+
+template <int D, int BITS, int GPB, bool CBL>
+__global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
+    constexpr int TN = 2;                       // 16-row tiles per wave
+    constexpr int SPB = 4 * D;                  // MFMA steps per block (8 weights each)
+    constexpr int CC = 128 * D;                 // x columns per superstep
+    constexpr int XS = CC + 8;                  // LDS row stride of an x chunk (halves)
+    constexpr int PIECES = kSegTok * CC / 8;    // 16-byte pieces per chunk
+    constexpr int PPT = PIECES / 256;
+    static_assert(PIECES % 256 == 0, "chunk must split evenly over 256 threads");
+    constexpr int CBN = 1 << BITS;              // LDS table entries (CBL)
+
+    extern __shared__ __align__(16) uint8_t smem[];
+    f16 *xs = reinterpret_cast<f16 *>(smem);    // [2][kSegTok][XS]
+    f16 *cbl = xs + 2 * kSegTok * XS;           // [CBN + 1][D] (CBL); entry CBN is zero
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ln = lane & 15, lg = lane >> 4;
+
+    int expert, row0, nrows;
+    const bool grouped = p.tmeta != nullptr;
+    if (grouped) {
+        if (int(blockIdx.y) >= *p.ntiles) return;   // uniform, before any barrier
+        const int32_t *tm = p.tmeta + 3 * blockIdx.y;
+        expert = tm[0];
+        row0 = tm[1];
+        nrows = tm[2];
+    } else {
+        expert = 0;
+        row0 = int(blockIdx.y) * kSegTok;
+        nrows = min(kSegTok, p.N - row0);
+    }
+    const int o0 = int(blockIdx.x) * kSegRows + wave * 32;
+
+    if constexpr (CBL) {
+        const int ent = min(p.K, CBN);
+        lds_copy_async(p.codebook, cbl, ent * D * 2, (CBN + 1) * D * 2);
+    }
+
+    // ---- this lane's weight rows (one per row tile) and token rows of its x pieces
+    int64_t cr[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+        const int o = o0 + 16 * tn + ln;
+        int64_t f = -1;
+        if (expert >= 0 && expert < p.E && o < p.OUT) {
+            f = int64_t(expert) * p.OUT + o;
+            if (p.row_table) f = p.row_table[f];
+            if (f < 0 || f >= p.stored_rows) f = -1;
+        }
+        cr[tn] = f;
+    }
+    int64_t xoff[PPT];
+#pragma unroll
+    for (int r = 0; r < PPT; ++r) {
+        const int t = (tid + 256 * r) / (CC / 8);
+        int64_t off = -1;
+        if (t < nrows) {
+            const int64_t row = grouped ? int64_t(p.order[row0 + t] / p.xkrep) : int64_t(row0 + t);
+            off = row * p.IN;
+        }
+        xoff[r] = off;
+    }
+
+    const int NSS = (p.NB + 3) >> 2;
+    const uint32_t kmax = uint32_t(p.K - 1);
+
+    auto load_x = [&](int sb, u32x4 (&v)[PPT]) {
+#pragma unroll
+        for (int r = 0; r < PPT; ++r) {
+            const int col = sb * CC + ((tid + 256 * r) % (CC / 8)) * 8;
+            v[r] = (xoff[r] >= 0 && col < p.IN) ? load8_act(p.x, p.x_type, xoff[r] + col)
+                                                : u32x4{0, 0, 0, 0};
+        }
+    };
+    auto store_x = [&](int buf, const u32x4 (&v)[PPT]) {
+#pragma unroll
+        for (int r = 0; r < PPT; ++r) {
+            const int pc = tid + 256 * r;
+            *reinterpret_cast<u32x4 *>(xs + (buf * kSegTok + pc / (CC / 8)) * XS + (pc % (CC / 8)) * 8) = v[r];
+        }
+    };
+    // words and scales of block 4*sb + lg of each row; lanes without one get
+    // zero words, zero scales and the zero entry
+    auto load_w = [&](int sb, uint32_t (&w)[TN][BITS], h2 (&s)[TN][GPB], bool (&live)[TN]) {
+        const int b = 4 * sb + lg;
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+            live[tn] = cr[tn] >= 0 && b < p.NB;
+            if (live[tn]) {
+                const uint32_t *src = p.codes + cr[tn] * p.row_words + int64_t(b) * BITS;
+#pragma unroll
+                for (int i = 0; i < BITS; ++i) w[tn][i] = __builtin_nontemporal_load(src + i);
+                const uint16_t *sr = p.scales + cr[tn] * p.ngrp + (GPB == 1 ? b / p.bpg : b * GPB);
+#pragma unroll
+                for (int g = 0; g < GPB; ++g) {
+                    const f16 v = __builtin_bit_cast(f16, __builtin_nontemporal_load(sr + g));
+                    s[tn][g] = h2{v, v};
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < BITS; ++i) w[tn][i] = 0u;
+#pragma unroll
+                for (int g = 0; g < GPB; ++g) s[tn][g] = h2{0, 0};
+            }
+        }
+    };
+
+    f32x4 acc[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) acc[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int buf, const uint32_t (&w)[TN][BITS], const h2 (&s)[TN][GPB],
+                       const bool (&live)[TN]) {
+        const f16 *xb = xs + (buf * kSegTok + ln) * XS + lg * (32 * D);
+        const f16 *tab[TN];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+            if constexpr (CBL) tab[tn] = live[tn] ? cbl : cbl + CBN * D;
+            else tab[tn] = live[tn] ? reinterpret_cast<const f16 *>(p.codebook)
+                                    : reinterpret_cast<const f16 *>(kSegZeroEntry);
+        }
+#pragma unroll
+        for (int st = 0; st < SPB; ++st) {
+            const h8 xf = *reinterpret_cast<const h8 *>(xb + 8 * st);
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const int q = (st * GPB) / (4 * D);
+                const h8 e = step_entries<D, BITS>(w[tn], st, tab[tn], kmax, !CBL);
+                const h2 sc = s[tn][q];
+                const h8 wv = e * h8{sc[0], sc[0], sc[0], sc[0], sc[0], sc[0], sc[0], sc[0]};
+                acc[tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv, xf, acc[tn], 0, 0, 0);
+            }
+        }
+    };
+
+    uint32_t w0[TN][BITS], w1[TN][BITS];
+    h2 s0[TN][GPB], s1[TN][GPB];
+    bool l0[TN], l1[TN];
+    u32x4 xr[PPT];
+
+    load_x(0, xr);
+    load_w(0, w0, s0, l0);
+    store_x(0, xr);
+    wait_vmem();
+    __syncthreads();
+    for (int sb = 0; sb < NSS; sb += 2) {
+        const bool more1 = sb + 1 < NSS;
+        if (more1) {
+            load_x(sb + 1, xr);
+            load_w(sb + 1, w1, s1, l1);
+        }
+        compute(0, w0, s0, l0);
+        if (more1) store_x(1, xr);
+        __syncthreads();
+        if (!more1) break;
+        const bool more2 = sb + 2 < NSS;
+        if (more2) {
+            load_x(sb + 2, xr);
+            load_w(sb + 2, w0, s0, l0);
+        }
+        compute(1, w1, s1, l1);
+        if (more2) store_x(0, xr);
+        __syncthreads();
+    }
+
+    // ---- epilogue: lane holds rows 16*tn + 4*lg + i of token ln
+    uint64_t alive[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) alive[tn] = __ballot(cr[tn] >= 0);
+    if (ln < nrows) {
+        const int64_t yr = grouped ? int64_t(p.order[row0 + ln]) : int64_t(row0 + ln);
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * tn + 4 * lg + i;
+                const int o = o0 + r;
+                if (o < p.OUT) {
+                    const float v = ((alive[tn] >> (r - 16 * tn)) & 1) ? acc[tn][i] : 0.f;
+                    store_act(p.y, p.y_type, yr * p.OUT + o, v);
+                }
+            }
+        }
+    }
+}
+
+// LDS bytes of k_seg_mfma<D, BITS, ...>.
+__host__ __device__ constexpr size_t seg_lds(int D, int BITS, bool cbl) {
+    return size_t(2) * kSegTok * (128 * D + 8) * 2 + (cbl ? (size_t(1) << BITS) * D * 2 + D * 2 : 0);
+}
+
+// Launches k_seg_mfma for geometry-dependent template arguments; returns a
+// VQK status (VQK_ENOTIMPL when no instance matches).
+int launch_seg_d2(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st);
+int launch_seg_d4(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st);
+int launch_seg_d8(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st);
+
+}  // namespace vqk
