@@ -1,6 +1,6 @@
 """Benchmark of the VQ MoE decode layer on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c3b4|c1]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c3b4|c4|c4t16|c5]
 
 Default workload: a Qwen3.6-35B-A3B-shaped MoE
 decode layer -- hidden 2048, 256 experts of intermediate 512, top-8 softmax
@@ -21,6 +21,17 @@ the timed wall time. roofline uses the layer call's total algorithmic bytes
 (codes + scales + codebooks + activations) over its event-timed duration.
 cpu_baseline: the repository's numpy oracle of the same layer (unpack ->
 fp16 dequant -> float64 matmuls), single-threaded, on a bounded sample.
+
+--workload c4 / c4t16: an MTP verify batch of T tokens
+through the config-3 layer with 20% of the routed experts' rows dead and
+stored compact (skipzero row table); the block runs its composed path
+(device softmax/top-k, then each projection as ONE grouped call over the
+T*k pairs: vqk_grouped_gemm above 512 pairs, the fused GEMV below).
+value = packed GB/s of the live rows of the touched experts.
+
+--workload c5: dense VQ prefill, x [2048, 5120]
+through VQLinear 5120->17408 then 17408->5120 (d8, K=65536 uint16 codes);
+value = TFLOP/s of the two GEMMs, roofline against the fp16 MFMA peak.
 """
 from __future__ import annotations
 
@@ -43,7 +54,20 @@ WORKLOADS = {
                desc="Qwen3.5-397B-A17B-shaped MoE decode layer, B=1 (BASELINE configs[2])"),
     "c3b4": dict(H=4096, E=512, I=1024, k=10, shared=True, d=8, K=16384, bits=14, T=4, layers=4,
                  desc="Qwen3.5-397B-A17B-shaped MoE decode layer, B=4 (BASELINE configs[2])"),
+    # batched paths: grouped expert GEMM (c4) and dense prefill GEMM (c5)
+    "c4": dict(H=4096, E=512, I=1024, k=10, shared=True, d=8, K=16384, bits=14, T=64, layers=2,
+               dead=0.2, kind="mtp",
+               desc="MTP verify batch on the config-3 layer, T=64, 20% skipzero rows "
+                    "(BASELINE configs[3])"),
+    "c4t16": dict(H=4096, E=512, I=1024, k=10, shared=True, d=8, K=16384, bits=14, T=16,
+                  layers=2, dead=0.2, kind="mtp",
+                  desc="MTP verify batch on the config-3 layer, T=16, 20% skipzero rows "
+                       "(BASELINE configs[3])"),
+    "c5": dict(N=2048, H=5120, F=17408, d=8, K=65536, kind="prefill",
+               desc="Dense Qwen3.8-27B-shaped VQ prefill: 5120x17408 then 17408x5120, "
+                    "x [2048, 5120] (BASELINE configs[4])"),
 }
+MFMA_F16_PEAK_TFS = 2500.0
 
 
 def log(*a):
@@ -134,6 +158,192 @@ def cpu_baseline(w, budget_s=12.0):
                       f"{pool} since per-token work does not depend on E)"}
 
 
+def _graph_time(torch, step, warmup, steps, dev):
+    """Warm up eagerly, capture `steps` calls of step(s) in one HIP graph,
+    replay it between HIP events on the capture stream. -> (wall s, event ms)."""
+    for s in range(warmup):
+        step(s)
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream(device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            for s in range(warmup, warmup + steps):
+                step(s)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(cap):
+        ev0.record(cap)
+        graph.replay()
+        ev1.record(cap)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, ev0.elapsed_time(ev1)
+
+
+def _skipzero_proj(torch, dev, g, e, out, inn, d, K, bits, dead):
+    """Routed projection with `dead` of its rows all-zero, stored compact:
+    codes [n_live, WPR] + scales [n_live, NGRP] + row table [e, out]."""
+    from vqlab_amd.vq_switch import VQSwitchLinear
+    wpr = ((inn // d) + 31) // 32 * bits
+    live = torch.rand((e, out), device=dev, generator=g) >= dead
+    n_live = int(live.sum().item())
+    rt = torch.full((e, out), -1, dtype=torch.int32, device=dev)
+    rt[live] = torch.arange(n_live, dtype=torch.int32, device=dev)
+    codes = torch.randint(-2**31, 2**31 - 1, (n_live, wpr), dtype=torch.int32, device=dev,
+                          generator=g)
+    cb = (torch.randn((K, d), device=dev, generator=g) * 0.02).to(torch.float16)
+    sc = (torch.rand((n_live, inn // 64), device=dev, generator=g) + 0.5).to(torch.float16)
+    return VQSwitchLinear(codes, cb, sc, pack_bits=bits, in_features=inn, row_table=rt)
+
+
+def run_mtp(torch, dev, a, w):
+    """c4: MTP verify batch through the skipzero config-3 layer (composed path)."""
+    from vqlab_amd.moe import VQSparseMoeBlock, VQSwitchGLU
+    from vqlab_amd.vq_switch import VQSwitchLinear
+    from oracle import vq_oracle as vo
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    H, E, I, k, d, K, bits, T, L = (w[n] for n in ("H", "E", "I", "k", "d", "K", "bits", "T",
+                                                    "layers"))
+    log(f"building {L} layers of {w['desc']}")
+    layers, live_rows = [], []
+    for _ in range(L):
+        gp, up, dn = (_skipzero_proj(torch, dev, g, E, o, i, d, K, bits, w["dead"])
+                      for o, i in ((I, H), (I, H), (H, I)))
+        live_rows.append([(p.row_table >= 0).sum(1).cpu().numpy() for p in (gp, up, dn)])
+
+        def dense(o, i):
+            wpr = ((i // d) + 31) // 32 * bits
+            return VQSwitchLinear(
+                torch.randint(-2**31, 2**31 - 1, (1, o, wpr), dtype=torch.int32, device=dev,
+                              generator=g),
+                (torch.randn((K, d), device=dev, generator=g) * 0.02).to(torch.float16),
+                (torch.rand((1, o, i // 64), device=dev, generator=g) + 0.5).to(torch.float16),
+                pack_bits=bits, in_features=i)
+        sh = VQSwitchGLU(dense(I, H), dense(I, H), dense(H, I))
+        sg = (torch.randn((H,), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        layers.append(VQSparseMoeBlock(VQSwitchGLU(gp, up, dn), k, True, sh, sg))
+    total = a.warmup + a.steps
+    xs = [torch.randn((T, H), device=dev, generator=g).to(torch.bfloat16) for _ in range(L)]
+    logits = torch.randn((total, L, T, E), device=dev, generator=g)
+    ys = [None] * L
+
+    def step(s):
+        for l in range(L):
+            ys[l] = layers[l].composed(xs[l], logits[s, l])
+
+    wall, ev_ms = _graph_time(torch, step, a.warmup, a.steps, dev)
+    # bytes of the live rows of the experts each call touched (+ the shared expert)
+    wpr_h, wpr_i = ((H // d) + 31) // 32 * bits, ((I // d) + 31) // 32 * bits
+    row_gu, row_dn = wpr_h * 4 + (H // 64) * 2, wpr_i * 4 + (I // 64) * 2
+    lg = logits[a.warmup:].cpu().numpy()
+    packed = 0
+    for s in range(a.steps):
+        for l in range(L):
+            ids, _ = vo.route(lg[s, l], k)
+            u = np.unique(ids)
+            lr = live_rows[l]
+            packed += int(lr[0][u].sum() + lr[1][u].sum()) * row_gu + int(lr[2][u].sum()) * row_dn
+    packed += a.steps * L * (2 * I * row_gu + H * row_dn)          # shared expert
+    calls = a.steps * L
+    alg_per_call = packed / calls + 6 * K * d * 2 + T * (2 * H * 2 + E * 4)
+    us_call = ev_ms * 1e3 / calls
+    achieved = alg_per_call / (us_call * 1e-6) / 1e9
+    value = packed / wall / 1e9
+    cpu = None if a.no_cpu else cpu_baseline(dict(w, shared=False))
+    return {
+        "metric": "packed-weight GB/s (% of HBM peak) and µs/call for the MTP-verify MoE layer",
+        "value": round(value, 2), "unit": "GB/s", "dtype": "fp16",
+        "config": {"workload": w["desc"], "hidden": H, "experts": E, "intermediate": I,
+                   "top_k": k, "shared_expert": True, "d": d, "K": K, "index_bits": bits,
+                   "group": 64, "tokens": T, "dead_row_frac": w["dead"], "io_dtype": "bf16",
+                   "layers_rotated": L},
+        "us_per_call": round(wall * 1e6 / calls, 3),
+        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_seg_mfma (grouped gate/up/down) + routing/SwiGLU glue",
+                     "alg_bytes_per_call": int(alg_per_call),
+                     "us_per_call_events": round(us_call, 3)},
+        "cpu_baseline": cpu,
+    }, wall, calls
+
+
+def cpu_prefill_baseline(w, budget_s=10.0):
+    """Numpy oracle of the dense prefill GEMM on a bounded sample of rows."""
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:
+        threadpool_limits = None
+    from oracle import vq_oracle as vo
+    rng = np.random.default_rng(7)
+    H, d, K = w["H"], w["d"], w["K"]
+    rows, ntok = 64, 256
+    codes = rng.integers(0, K, (rows, H // d)).astype(np.uint16)
+    cb = (rng.standard_normal((K, d)) * 0.02).astype(np.float16)
+    sc = rng.uniform(0.5, 1.5, (rows, H // 64)).astype(np.float16)
+    x = rng.standard_normal((ntok, H)).astype(np.float32)
+    ctx = threadpool_limits(1) if threadpool_limits else None
+    n, t0 = 0, time.perf_counter()
+    try:
+        if ctx:
+            ctx.__enter__()
+        while n < 2 or (time.perf_counter() - t0 < budget_s and n < 2000):
+            wd = vo.dequant(codes, cb, sc, 64)
+            vo.decode_matmul(x, wd)
+            n += 1
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    dt = (time.perf_counter() - t0) / n
+    tfs = 2.0 * rows * H * ntok / dt / 1e12
+    return {"value": round(tfs, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"{n} x (dequant {rows}x{H} rows + float64 matmul with {ntok} tokens), "
+                      f"numpy oracle, 1 thread"}
+
+
+def run_prefill(torch, dev, a, w):
+    """c5: dense VQ prefill, two linears through VQLinear (vqk_dense_gemm)."""
+    from vqlab_amd.vq_dense import VQLinear
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    N, H, F, d, K = (w[n] for n in ("N", "H", "F", "d", "K"))
+    log(f"building {w['desc']}")
+
+    def lin(o, i):
+        codes = torch.randint(0, K, (o, i // d), dtype=torch.int32, device=dev,
+                              generator=g).to(torch.int16)
+        cb = (torch.randn((K, d), device=dev, generator=g) * 0.02).to(torch.float16)
+        sc = (torch.rand((o, i // 64), device=dev, generator=g) + 0.5).to(torch.float16)
+        return VQLinear(codes, cb, sc, group_size=64, pack_bits=0)
+    l1, l2 = lin(F, H), lin(H, F)
+    x = torch.randn((N, H), device=dev, generator=g).to(torch.bfloat16)
+    out = [None, None]
+
+    def step(s):
+        out[0] = l1(x)
+        out[1] = l2(out[0])
+
+    wall, ev_ms = _graph_time(torch, step, a.warmup, a.steps, dev)
+    flop = 2.0 * 2 * N * H * F
+    tfs = flop * a.steps / wall / 1e12
+    ev_tfs = flop * a.steps / (ev_ms * 1e-3) / 1e12
+    cpu = None if a.no_cpu else cpu_prefill_baseline(w)
+    return {
+        "metric": "TFLOP/s (% of fp16 MFMA peak) of the dense VQ prefill GEMMs",
+        "value": round(tfs, 2), "unit": "TFLOP/s", "dtype": "fp16",
+        "config": {"workload": w["desc"], "tokens": N, "hidden": H, "ffn": F, "d": d, "K": K,
+                   "index_bits": 16, "group": 64, "io_dtype": "bf16"},
+        "us_per_step_events": round(ev_ms * 1e3 / a.steps, 2),
+        "roofline": {"bound": "mfma", "achieved": round(ev_tfs, 2), "peak": MFMA_F16_PEAK_TFS,
+                     "unit": "TFLOP/s", "frac": round(ev_tfs / MFMA_F16_PEAK_TFS, 4),
+                     "traffic": None, "kernel": "vqk_dense_gemm (both linears)",
+                     "flop_per_step": flop},
+        "cpu_baseline": cpu,
+    }, wall, a.steps
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -153,6 +363,18 @@ def main():
     w = WORKLOADS[a.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if w.get("kind") in ("mtp", "prefill"):
+        fn = run_mtp if w["kind"] == "mtp" else run_prefill
+        body, wall, _ = fn(torch, dev, a, w)
+        out = {"metric": body.pop("metric"), "value": body.pop("value"), "unit": body.pop("unit"),
+               "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+               "ms_per_step": round(wall * 1e3 / a.steps, 5), "higher_is_better": True,
+               "scaling": "weak", "vs_baseline": None, "dtype": body.pop("dtype"),
+               "data": "synthetic (random VQ weights, N(0,1) activations and router logits; "
+                       "no checkpoints offline)"}
+        out.update(body)
+        print(json.dumps(out), flush=True)
+        return
     g = torch.Generator(device=dev)
     g.manual_seed(1234)
     L, T, E, H, k = w["layers"], w["T"], w["E"], w["H"], w["k"]
