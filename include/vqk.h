@@ -146,10 +146,19 @@ int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type,
                      void *stream);
 
 /* ---- a11: dense large-N path, _decode_matmul (vq_dense.py:262-312) ---------
- * y[N, OUT] = x[N, IN] . W^T for E == 1 with W dequantised tile by tile into
- * LDS and fed to the matrix cores (no materialised fp16 weight). */
+ * y[N, OUT] = x[N, IN] . W^T for E == 1. Up to 64 rows: W is decoded straight
+ * into matrix-core operands (no workspace). Above: the reference's
+ * decode-then-matmul -- W is dequantised bit-exactly into the workspace panel
+ * by panel and multiplied by an LDS-tiled fp16 matrix-core GEMM (x narrowed
+ * to fp16 in the workspace first). vqk_dense_gemm_workspace gives the size of
+ * a single whole-weight panel; any workspace holding fp16 x plus 128 weight
+ * rows works (smaller panels, more passes), less is VQK_ENOSPACE. With no
+ * workspace (NULL, 0), and for IN % 64 != 0, a tile kernel that decodes W
+ * into LDS per output tile runs instead. */
+int vqk_dense_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes);
 int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type,
-                   int64_t N, void *y, int32_t y_type, void *stream);
+                   int64_t N, void *y, int32_t y_type, void *workspace,
+                   size_t ws_bytes, void *stream);
 
 /* ---- a15: fused MoE decode layer (SwitchGLU + SparseMoeBlock routing) -------
  * mlx-lm's SparseMoeBlock around VQSwitchLinear (restated in

@@ -86,10 +86,45 @@ def test_dense_gemm_empty_and_refusals():
     x = torch.zeros((1, 256), dtype=torch.bfloat16, device="cuda")
     # two experts: the dense GEMM takes exactly one linear
     assert L.lib().vqk_dense_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, 1, Tt.ptr(y),
-                                  L.VQK_BF16, Tt.stream()) == L.VQK_EINVAL
+                                  L.VQK_BF16, None, 0, Tt.stream()) == L.VQK_EINVAL
     w1 = Tt.weights(codes[0], cb, sc[0], 64, 8, 256, keep=keep)
     assert L.lib().vqk_dense_gemm(ctypes.byref(w1), Tt.ptr(x), L.VQK_BF16, 0, Tt.ptr(y),
-                                  L.VQK_BF16, Tt.stream()) == L.VQK_OK
+                                  L.VQK_BF16, None, 0, Tt.stream()) == L.VQK_OK
+    # above 64 rows the decode-then-GEMM path wants fp16 x + >= 128 weight rows
+    xb = torch.zeros((100, 256), dtype=torch.bfloat16, device="cuda")
+    yb = torch.empty((100, 128), dtype=torch.bfloat16, device="cuda")
+    ws = ctypes.c_size_t()
+    L.check(L.lib().vqk_dense_gemm_workspace(ctypes.byref(w1), 100, ctypes.byref(ws)))
+    assert ws.value >= 100 * 256 * 2 + 128 * 256 * 2
+    small = torch.empty(1024, dtype=torch.uint8, device="cuda")
+    assert L.lib().vqk_dense_gemm(ctypes.byref(w1), Tt.ptr(xb), L.VQK_BF16, 100, Tt.ptr(yb),
+                                  L.VQK_BF16, Tt.ptr(small), 1024, Tt.stream()) == L.VQK_ENOSPACE
+
+
+@pytest.mark.parametrize("panel_rows", [128, 256, None])
+def test_dense_gemm_panels_and_tile_fallback(panel_rows):
+    """Workspaces smaller than the whole weight decode it in panels; with no
+    workspace the LDS tile kernel runs. All agree with the oracle."""
+    from vqlab_amd import _lib as L, _torch as Tt
+    print(f"dense gemm panels {panel_rows}", flush=True)
+    rng = np.random.default_rng(27)
+    N, OUT, IN = 300, 700, 1024
+    m = make_module(rng, 1, OUT, IN, 4, 4096)
+    codes, cb, sc = to_device(m)
+    keep = []
+    w = Tt.weights(codes[0], cb, sc[0], 64, 12, IN, keep=keep)
+    x = _x(rng, N, IN)
+    y = torch.empty((N, OUT), dtype=torch.float32, device="cuda")
+    if panel_rows is None:
+        work, nb = None, 0
+    else:
+        nb = N * IN * 2 + 512 + panel_rows * IN * 2
+        work = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    L.check(L.lib().vqk_dense_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, N, Tt.ptr(y),
+                                   L.VQK_F32, Tt.ptr(work) if work is not None else None, nb,
+                                   Tt.stream()))
+    wd = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], 64)
+    assert_close(_np(y), vo.decode_matmul(_x16(x), wd), what=f"panels {panel_rows}")
 
 
 # ------------------------------------------------------------ grouped GEMM

@@ -55,7 +55,10 @@ SIGNATURES = {
                                            ctypes.POINTER(c_sz)]),
     "vqk_grouped_gemm": (c_i32, [ctypes.POINTER(VQKWeights), c_p, c_i32, c_i64, c_p, c_i64,
                                  c_i64, c_p, c_i32, c_p, c_sz, c_p]),
-    "vqk_dense_gemm": (c_i32, [ctypes.POINTER(VQKWeights), c_p, c_i32, c_i64, c_p, c_i32, c_p]),
+    "vqk_dense_gemm_workspace": (c_i32, [ctypes.POINTER(VQKWeights), c_i64,
+                                         ctypes.POINTER(ctypes.c_size_t)]),
+    "vqk_dense_gemm": (c_i32, [ctypes.POINTER(VQKWeights), c_p, c_i32, c_i64, c_p, c_i32, c_p,
+                               ctypes.c_size_t, c_p]),
     "vqk_moe_decode_layer_workspace": (c_i32, [ctypes.POINTER(VQKMoeDesc), c_i64,
                                                ctypes.POINTER(c_sz)]),
     "vqk_moe_decode_layer": (c_i32, [ctypes.POINTER(VQKMoeDesc), c_p, c_i32, c_i64, c_p, c_p,

@@ -315,13 +315,16 @@ static int64_t group_max_tiles(int64_t N, int64_t E) {
 // The register-decode segment kernel covers whole 32-code blocks per row
 // (rows of NB * BITS words), BITS 2..16, the GEMV's scale-group layouts and
 // 16-byte aligned codebook and activations.
-static bool seg_fits(const Geom &g, const vqk_weights *w, const void *x) {
+static bool seg_fits_geom(const Geom &g, const vqk_weights *w) {
     const int gpb_fast = g.D == 4 ? 2 : (g.D == 8 ? 4 : 1);
     return (g.D == 2 || g.D == 4 || g.D == 8) && g.NSUB % kBlock == 0 && g.row_words > 0 &&
            g.row_words == g.NB * g.BITS && g.BITS >= 2 && g.BITS <= 16 &&
            (g.gpb == 1 || g.gpb == gpb_fast) && g.IN <= INT32_MAX && g.OUT <= INT32_MAX &&
-           (reinterpret_cast<uintptr_t>(w->codebook) & 15) == 0 &&
-           (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+           (reinterpret_cast<uintptr_t>(w->codebook) & 15) == 0;
+}
+
+static bool seg_fits(const Geom &g, const vqk_weights *w, const void *x) {
+    return seg_fits_geom(g, w) && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
 }
 
 static void fill_seg(const vqk_weights *w, const Geom &g, SegParams *p) {
@@ -340,6 +343,20 @@ static void fill_seg(const vqk_weights *w, const Geom &g, SegParams *p) {
     p->IN = int32_t(g.IN);
     p->NB = int32_t(g.NB);
 }
+
+// Dense large-N path: W dequantised panel by panel into the workspace, then the
+// fp16 GEMM (vqk_hgemm.hip).
+int launch_hgemm(const uint16_t *A, const uint16_t *B, void *y, int32_t y_type, int64_t ldy,
+                 int64_t ycol0, int64_t M, int64_t Nc, int64_t K, hipStream_t st);
+int launch_x_to_f16(const void *x, int32_t type, int64_t n, uint16_t *out, hipStream_t st);
+constexpr int64_t kPanelMin = 128;              // weight rows of the smallest panel
+
+static bool hgemm_fits(const Geom &g, const void *x, int64_t N) {
+    return g.IN % 64 == 0 && g.IN <= INT32_MAX && g.OUT <= INT32_MAX && N <= INT32_MAX &&
+           (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+}
+
+static size_t x16_bytes(const Geom &g, int64_t N) { return al256(size_t(N) * size_t(g.IN) * 2); }
 
 static int launch_seg(const SegParams &p, const Geom &g, dim3 grid, hipStream_t st) {
     switch (g.D) {
@@ -408,8 +425,20 @@ int vqk_gemmseg_fits(int32_t D, int64_t K, int32_t G, int32_t pack_bits, int64_t
            IN > 0 && IN % G == 0 && IN % D == 0 && pack_bits >= 0 && pack_bits <= 16;
 }
 
+int vqk_dense_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if (!bytes || N < 0) return set_error(VQK_EINVAL, "bad arguments");
+    // the decode-then-GEMM path: fp16 x plus the whole fp16 weight (one panel)
+    const bool seg = N <= kSegDenseMaxN && seg_fits_geom(g, w);
+    *bytes = (!seg && N > 0 && g.IN % 64 == 0)
+                 ? x16_bytes(g, N) + size_t(g.OUT) * size_t(g.IN) * 2 : 0;
+    return VQK_OK;
+}
+
 int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_t N, void *y,
-                   int32_t y_type, void *stream) {
+                   int32_t y_type, void *workspace, size_t ws_bytes, void *stream) {
     Geom g;
     int rc = make_geom(w, &g);
     if (rc) return rc;
@@ -430,6 +459,31 @@ int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_t 
         const dim3 grid(unsigned((g.OUT + kSegRows - 1) / kSegRows),
                         unsigned((N + kSegTok - 1) / kSegTok), 1);
         return launch_seg(sp, g, grid, hipStream_t(stream));
+    }
+    if (hgemm_fits(g, x, N) && (workspace || ws_bytes)) {
+        hipStream_t st = hipStream_t(stream);
+        const bool cvt = x_type != VQK_F16;
+        const size_t xb = cvt ? x16_bytes(g, N) : 0;
+        const size_t row_b = size_t(g.IN) * 2;
+        if (!workspace || ws_bytes < xb + kPanelMin * row_b)
+            return set_error(VQK_ENOSPACE, "dense GEMM workspace %zu B < %zu B (fp16 x + %lld "
+                             "weight rows)", ws_bytes, xb + kPanelMin * row_b, (long long)kPanelMin);
+        uint8_t *ws = static_cast<uint8_t *>(workspace);
+        const uint16_t *a16 = static_cast<const uint16_t *>(x);
+        if (cvt) {
+            if ((rc = launch_x_to_f16(x, x_type, N * g.IN, reinterpret_cast<uint16_t *>(ws), st)))
+                return rc;
+            a16 = reinterpret_cast<const uint16_t *>(ws);
+        }
+        uint16_t *panel = reinterpret_cast<uint16_t *>(ws + xb);
+        int64_t prow = int64_t((ws_bytes - xb) / row_b);
+        prow = prow >= g.OUT ? g.OUT : prow / kPanelMin * kPanelMin;
+        for (int64_t r0 = 0; r0 < g.OUT; r0 += prow) {
+            const int64_t rows = g.OUT - r0 < prow ? g.OUT - r0 : prow;
+            if ((rc = vqk_dequant(w, r0, rows, panel, stream))) return rc;
+            if ((rc = launch_hgemm(a16, panel, y, y_type, g.OUT, r0, N, rows, g.IN, st))) return rc;
+        }
+        return VQK_OK;
     }
     GemmParams p;
     if ((rc = fill_gemm(w, g, &p))) return rc;

@@ -182,6 +182,15 @@ __device__ __forceinline__ void stage_codebook_fixed(const uint16_t *cb, int K, 
 // asynchronous LDS copies included).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
 
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt
+// left at their maxima, i.e. not waited for).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // Eight activations starting at element i of row `base` -> fp16, as one
 // 16-byte value. 16-byte aligned rows only (checked by the caller).
 __device__ __forceinline__ u32x4 load8_act(const void *x, int32_t type, int64_t i) {

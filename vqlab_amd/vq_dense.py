@@ -42,8 +42,13 @@ def _decode_matmul(xf, codes_in, codebook, scales, group_size, OUT, IN, pack_bit
     w = T.weights(codes_in, codebook, scales, group_size, pack_bits, IN, keep=keep)
     xf = xf.contiguous()
     y = torch.empty((xf.shape[0], int(OUT)), dtype=xf.dtype, device=xf.device)
+    ws = ctypes.c_size_t()
+    L.check(L.lib().vqk_dense_gemm_workspace(ctypes.byref(w), xf.shape[0], ctypes.byref(ws)),
+            "_decode_matmul")
+    work = torch.empty(max(1, ws.value), dtype=torch.uint8, device=xf.device)
     L.check(L.lib().vqk_dense_gemm(ctypes.byref(w), T.ptr(xf), T.act_type(xf), xf.shape[0],
-                                   T.ptr(y), T.act_type(y), T.stream(xf.device)),
+                                   T.ptr(y), T.act_type(y), T.ptr(work), ws.value,
+                                   T.stream(xf.device)),
             "_decode_matmul")
     return y
 
