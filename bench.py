@@ -74,6 +74,20 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def measured_traffic(name):
+    """HBM bytes per call from the committed counter profile of this workload
+    (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_call:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def make_layer(torch, dev, w, g):
     """Random VQ weights of one MoE layer on the device (generator g)."""
     from vqlab_amd.vq_switch import VQSwitchLinear
@@ -465,7 +479,10 @@ def main():
         "us_per_token_layer": round(wall * 1e6 / calls, 3),
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(f"moe_layer_{a.workload}_traffic.md"),
+                     "traffic_source": "profiles/moe_layer_<workload>_traffic.md (rocprofv3 "
+                                       "FETCH_SIZE + WRITE_SIZE per dispatch, copy-calibrated)",
                      "kernel": "k_moe_up + k_moe_down (one fused layer call)",
                      "alg_bytes_per_call": int(alg_per_call), "us_per_call_events": round(us_call, 3)},
         "cpu_baseline": cpu,

@@ -262,9 +262,14 @@ class VQSwitchLinear(torch.nn.Module):
             lead = tuple(indices.shape)
             x2, rep = x.expand(*lead, 1, IN).reshape(N, IN), 1
         eidx = indices.reshape(-1)
-        if N <= VQ_FUSED_MAX_N or not gemmseg_fits(int(self.codebook.shape[1]),
-                                                   int(self.codebook.shape[0]), self.group_size,
-                                                   self.pack_bits, IN):
+        # The fused GEMV reads an expert's rows once per pair; when the pairs
+        # crowd onto few experts (a shared expert under a token batch, N >= 2E)
+        # the grouped GEMM, which reads them once per tile of up to 16 pairs,
+        # wins even below VQ_FUSED_MAX_N. Same outputs either way.
+        crowded = N >= 4 and N >= 2 * self.num_experts
+        if (N <= VQ_FUSED_MAX_N and not crowded) or not gemmseg_fits(
+                int(self.codebook.shape[1]), int(self.codebook.shape[0]), self.group_size,
+                self.pack_bits, IN):
             y = _fused(x2, eidx, self.codes, self.codebook, self.vq_scales,
                        pack_bits=self.pack_bits, xkrep=rep, rowtbl=self.row_table,
                        in_features=IN, out_dtype=out_dtype)
