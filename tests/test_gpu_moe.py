@@ -79,6 +79,25 @@ def test_moe_layer_c3_shape_shared(T):
     _check(blk, projs, sh, shv, rng, T, 64, 4096, 10)
 
 
+def test_moe_layer_repeated_calls_one_workspace():
+    """Many T == 1 calls in a row on one workspace keep giving the oracle's
+    answer (the routing and SwiGLU buffers are rewritten every call)."""
+    print("moe repeated calls", flush=True)
+    rng = np.random.default_rng(7)
+    E, H, I, k = 64, 1024, 256, 6
+    blk, projs, sh, shv = _block(rng, E, H, I, 4, 4096, k)
+    x = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float32)).to("cuda", torch.bfloat16)
+    ys = []
+    for i in range(6):
+        lg = torch.from_numpy(rng.standard_normal((1, E)).astype(np.float32)).cuda()
+        ys.append((blk.fused(x, lg), lg))
+    torch.cuda.synchronize()
+    for y, lg in ys:
+        ref, _, _ = vo.moe_layer(x.float().cpu().numpy(), lg.cpu().numpy(), _spec(projs["gate"]),
+                                 _spec(projs["up"]), _spec(projs["down"]), k, h_round=np.float16)
+        assert_close(y.float().cpu().numpy(), ref, what="repeat")
+
+
 def test_moe_layer_unnormalised_d2():
     print("moe d2 norm=False", flush=True)
     rng = np.random.default_rng(4)

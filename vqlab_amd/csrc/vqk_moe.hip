@@ -185,12 +185,38 @@ __device__ __forceinline__ int64_t moe_row(const MoeW &w, int64_t e, int OUT, in
 }
 
 // ------------------------------------------------------------ K1: gate/up
-template <int D, int BITS, int GPB>
-__global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
+// LDS of the gate/up phase: two codebook tables, then x at the padded stride.
+template <int D, int BITS>
+__host__ __device__ constexpr size_t up_cb_bytes() {
+    return cb_in_lds(D, BITS) ? size_t(2) * (size_t(1) << BITS) * D * 2 : 0;
+}
+
+// Routing of the workgroup's token as wave 0 computed it (LDS).
+struct RouteLds {
+    int route;                 // expert of this workgroup's pair
+    int ids[kMaxTopK];
+    float wts[kMaxTopK];
+};
+
+// Down-phase state a workgroup prepares before it needs the SwiGLU input:
+// its lane's code row, block words and scales for the first row step.
+template <int BITS, int GPB>
+struct DownState {
+    uint32_t a[BITS];
+    float s[GPB];
+    int64_t cr, e;
+    float wj;
+};
+
+// K1 body: routing + gate/up + SwiGLU for pair `pair` of row tile `bx`. The
+// routing is left in `rl` (LDS), and `pre(rl)` runs right after it is
+// published and the first weight loads are out, before the decode.
+template <int D, int BITS, int GPB, typename PRE>
+__device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, uint8_t *smem,
+                                        RouteLds &rl, PRE pre) {
     constexpr bool CBL = cb_in_lds(D, BITS);
     constexpr int CBN = CBL ? (1 << BITS) : 0;
     constexpr int XH = kBlock * D, XS = XH + 8;
-    extern __shared__ __align__(16) uint8_t smem[];
     h2 *cbg_lds = reinterpret_cast<h2 *>(smem);
     h2 *cbu_lds = reinterpret_cast<h2 *>(smem + CBN * D * 2);
     f16 *xs = reinterpret_cast<f16 *>(smem + 2 * CBN * D * 2);
@@ -199,7 +225,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
     const int lpr = 1 << p.lpr1_log2, rpw = kWave >> p.lpr1_log2;
     const int sub = lane >> p.lpr1_log2, blk = lane & (lpr - 1);
     const bool on = blk < p.NB1;
-    const int pair = blockIdx.y, t = pair / p.P, j = pair % p.P;
+    const int t = pair / p.P, j = pair % p.P;
     const bool is_shared = j >= p.top_k;
     const MoeW &wg = is_shared ? p.sgate : p.gate;
     const MoeW &wu = is_shared ? p.sup : p.up;
@@ -209,7 +235,6 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
     // the two codebooks and x into LDS. One barrier publishes the expert id,
     // then all waves issue their weight loads (nothing else is outstanding,
     // so the barrier's wait never drains weight loads).
-    __shared__ int s_route;
     CbPair<D, CBN> cbp{wg.codebook, wu.codebook, wg.K, wu.K, cbg_lds, cbu_lds};
     int my_idx = -1;
     float my_w = 0.f;
@@ -217,15 +242,19 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
         int e_pair;
         route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &e_pair, &my_idx, &my_w,
               &issue_cb_pair<D, CBN>, &cbp);
-        if (lane == 0) s_route = e_pair;
+        if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
+        if (lane == 0) rl.route = e_pair;
+        if (lane < p.top_k) {
+            rl.ids[lane] = my_idx;
+            rl.wts[lane] = my_w;
+        }
     } else {
         issue_cb_pair<D, CBN>(&cbp);
     }
     stage_x<XH, XS>(p.x, p.x_type, int64_t(t) * p.H, p.H, p.NB1, xs);
     // routing / shared-gate outputs, once per token
-    if (blockIdx.x == 0 && j == 0 && wave == 0) {
+    if (bx == 0 && j == 0 && wave == 0) {
         if (lane < p.top_k) {
-            if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
             p.ids[t * p.top_k + lane] = my_idx;
             p.wts[t * p.top_k + lane] = my_w;
             if (p.ids_out) p.ids_out[t * p.top_k + lane] = my_idx;
@@ -243,10 +272,10 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
     __syncthreads();
 
     // a NaN logit can leave a selection empty: such a pair reads nothing
-    const int e_pair = s_route;
+    const int e_pair = rl.route;
     const int64_t e = is_shared ? 0 : ((e_pair >= 0 && e_pair < p.E) ? e_pair : -1);
     const int sidx = GPB == 1 ? blk / p.bpg1 : blk * GPB;
-    const int r_wg = int(blockIdx.x) * p.rows_per_wg1;
+    const int r_wg = bx * p.rows_per_wg1;
     auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * rpw + sub; };
 
     uint32_t ag[BITS], au[BITS];
@@ -260,6 +289,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
         moe_load<BITS, GPB>(wg, crg, blk, sidx, p.ngrp1, ag, sg_);
         moe_load<BITS, GPB>(wu, cru, blk, sidx, p.ngrp1, au, su_);
     }
+    pre(rl);
 
     h2 xr[16 * D];
     load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
@@ -295,53 +325,83 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
     }
 }
 
-// ------------------------------------------------------------ K2: down + combine
+struct NoPre {
+    __device__ void operator()(RouteLds &) const {}
+};
+
 template <int D, int BITS, int GPB>
-__global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
+__global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ RouteLds rl;
+    up_body<D, BITS, GPB>(p, int(blockIdx.x), int(blockIdx.y), smem, rl, NoPre{});
+}
+
+// ------------------------------------------------------------ K2: down + combine
+// Lane geometry of the down phase: lanes are (pair j, block) of one row,
+// LPR2 = next_pow2(P * NB2) lanes per row.
+struct DownLane {
+    int lpr, rpw, sub, v, j, blk;
+    bool on, is_shared;
+    __device__ DownLane(const MoeParams &p) {
+        const int lane = threadIdx.x & (kWave - 1);
+        lpr = 1 << p.lpr2_log2;
+        rpw = kWave >> p.lpr2_log2;
+        sub = lane >> p.lpr2_log2;
+        v = lane & (lpr - 1);
+        j = v / p.NB2;
+        blk = v % p.NB2;
+        on = j < p.P;
+        is_shared = on && j >= p.top_k;
+    }
+};
+
+// Expert, router weight and first-step weights of this lane's pair for row
+// tile `bx`; `eid(j)` / `wt(j)` give the routing (workspace or LDS).
+template <int BITS, int GPB, typename EID, typename WT>
+__device__ __forceinline__ void down_prep(const MoeParams &p, int bx, int t, const DownLane &dl,
+                                          EID eid, WT wt, DownState<BITS, GPB> &ds) {
+    const int wave = threadIdx.x >> 6;
+    const MoeW &wd = dl.is_shared ? p.sdown : p.down;
+    ds.e = -1;
+    ds.wj = 0.f;
+    if (dl.on) {
+        if (dl.is_shared) { ds.e = 0; ds.wj = p.sg[t]; }
+        else {
+            const int id = eid(dl.j);
+            ds.e = (id >= 0 && id < p.E) ? id : -1;
+            ds.wj = wt(dl.j);
+        }
+    }
+    const int sidx = GPB == 1 ? dl.blk / p.bpg2 : dl.blk * GPB;
+    const int r = bx * p.rows_per_wg2 + wave * dl.rpw + dl.sub;
+    ds.cr = (ds.e >= 0 && r < p.H) ? moe_row(wd, ds.e, p.H, r) : -1;
+    moe_load<BITS, GPB>(wd, ds.cr, dl.blk, sidx, p.ngrp2, ds.a, ds.s);
+}
+
+template <int D, int CBN>
+__device__ __forceinline__ void down_stage_cb(const MoeParams &p, uint8_t *smem) {
+    if constexpr (CBN > 0) {
+        stage_codebook_fixed<D, CBN, kThreads>(p.down.codebook, p.down.K, reinterpret_cast<h2 *>(smem));
+        if (p.shared)
+            stage_codebook_fixed<D, CBN, kThreads>(p.sdown.codebook, p.sdown.K,
+                                                   reinterpret_cast<h2 *>(smem + CBN * D * 2));
+    }
+}
+
+// The token's P SwiGLU rows (fp16) -> LDS at the padded block stride, then
+// the down projection of the workgroup's rows, scaled per pair by its router
+// weight and combined over the wave (the DPP row reduction is the sum).
+template <int D, int BITS, int GPB>
+__device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint8_t *smem,
+                                         const DownLane &dl, DownState<BITS, GPB> &ds) {
     constexpr bool CBL = cb_in_lds(D, BITS);
     constexpr int CBN = CBL ? (1 << BITS) : 0;
     constexpr int XH = kBlock * D, XS = XH + 8;
-    extern __shared__ __align__(16) uint8_t smem[];
     h2 *cbd_lds = reinterpret_cast<h2 *>(smem);
     h2 *cbs_lds = reinterpret_cast<h2 *>(smem + CBN * D * 2);
     f16 *xs = reinterpret_cast<f16 *>(smem + (1 + p.shared) * CBN * D * 2);
-
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-    const int lpr = 1 << p.lpr2_log2, rpw = kWave >> p.lpr2_log2;
-    const int sub = lane >> p.lpr2_log2, v = lane & (lpr - 1);
-    const int j = v / p.NB2, blk = v % p.NB2;
-    const bool on = j < p.P;
-    const int t = blockIdx.y;
-    const bool is_shared = on && j >= p.top_k;
-    const MoeW &wd = is_shared ? p.sdown : p.down;
-    if constexpr (CBL) {                       // independent of the routing: first
-        stage_codebook_fixed<D, CBN, kThreads>(p.down.codebook, p.down.K, cbd_lds);
-        if (p.shared) stage_codebook_fixed<D, CBN, kThreads>(p.sdown.codebook, p.sdown.K, cbs_lds);
-    }
-    int64_t e = -1;
-    float wj = 0.f;
-    if (on) {
-        if (is_shared) { e = 0; wj = p.sg[t]; }
-        else {
-            const int id = p.ids[t * p.top_k + j];
-            e = (id >= 0 && id < p.E) ? id : -1;
-            wj = p.wts[t * p.top_k + j];
-        }
-    }
-    const int sidx = GPB == 1 ? blk / p.bpg2 : blk * GPB;
-    const int r_wg = int(blockIdx.x) * p.rows_per_wg2;
-    auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * rpw + sub; };
-    auto code_row = [&](int st) -> int64_t {
-        const int r = row_at(st);
-        return (e >= 0 && r < p.H) ? moe_row(wd, e, p.H, r) : -1;
-    };
-
-    uint32_t a[BITS];
-    float s[GPB];
-    int64_t cr = code_row(0);
-    moe_load<BITS, GPB>(wd, cr, blk, sidx, p.ngrp2, a, s);
-    // the token's P intermediate rows (fp16), blocks at the padded stride;
-    // 16-byte groups, all loads issued before any LDS store
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const MoeW &wd = dl.is_shared ? p.sdown : p.down;
     {
         const uint16_t *hsrc = p.h + int64_t(t) * p.P * p.I;
         const int gpr = p.I / 8;                     // 8-value groups per row
@@ -370,27 +430,48 @@ __global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
     __syncthreads();
 
     h2 xr[16 * D];
-    load_xregs<D>(xs + (on ? j * p.NB2 + blk : 0) * XS, xr);
-    const h2 *cb = CBL ? (is_shared ? cbs_lds : cbd_lds)
+    load_xregs<D>(xs + (dl.on ? dl.j * p.NB2 + dl.blk : 0) * XS, xr);
+    const h2 *cb = CBL ? (dl.is_shared ? cbs_lds : cbd_lds)
                        : reinterpret_cast<const h2 *>(wd.codebook);
     const uint32_t kmax = uint32_t(wd.K - 1);
+    const int sidx = GPB == 1 ? dl.blk / p.bpg2 : dl.blk * GPB;
+    const int r_wg = bx * p.rows_per_wg2;
+    auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * dl.rpw + dl.sub; };
+    auto code_row = [&](int st) -> int64_t {
+        const int r = row_at(st);
+        return (ds.e >= 0 && r < p.H) ? moe_row(wd, ds.e, p.H, r) : -1;
+    };
 
     for (int st = 0; st < p.steps2; ++st) {
         uint32_t n[BITS];
         float ns[GPB];
         const int64_t crn = st + 1 < p.steps2 ? code_row(st + 1) : -1;
-        moe_load<BITS, GPB>(wd, crn, blk, sidx, p.ngrp2, n, ns);
+        moe_load<BITS, GPB>(wd, crn, dl.blk, sidx, p.ngrp2, n, ns);
         float acc = 0.f;
-        if (cr >= 0) acc = wj * block_dot<D, BITS, GPB, CBL>(a, xr, s, cb, kmax);
-        acc = group_sum(acc, lpr);
+        if (ds.cr >= 0) acc = ds.wj * block_dot<D, BITS, GPB, CBL>(ds.a, xr, ds.s, cb, kmax);
+        acc = group_sum(acc, dl.lpr);
         const int r = row_at(st);
-        if (v == lpr - 1 && r < p.H) store_act(p.y, p.y_type, int64_t(t) * p.H + r, acc);
-        cr = crn;
+        if (dl.v == dl.lpr - 1 && r < p.H) store_act(p.y, p.y_type, int64_t(t) * p.H + r, acc);
+        ds.cr = crn;
 #pragma unroll
-        for (int i = 0; i < BITS; ++i) a[i] = n[i];
+        for (int i = 0; i < BITS; ++i) ds.a[i] = n[i];
 #pragma unroll
-        for (int g = 0; g < GPB; ++g) s[g] = ns[g];
+        for (int g = 0; g < GPB; ++g) ds.s[g] = ns[g];
     }
+}
+
+template <int D, int BITS, int GPB>
+__global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
+    constexpr int CBN = cb_in_lds(D, BITS) ? (1 << BITS) : 0;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int t = int(blockIdx.y);
+    down_stage_cb<D, CBN>(p, smem);            // independent of the routing: first
+    const DownLane dl(p);
+    DownState<BITS, GPB> ds;
+    down_prep<BITS, GPB>(p, int(blockIdx.x), t, dl,
+                         [&](int j) { return p.ids[t * p.top_k + j]; },
+                         [&](int j) { return p.wts[t * p.top_k + j]; }, ds);
+    down_run<D, BITS, GPB>(p, int(blockIdx.x), t, smem, dl, ds);
 }
 
 // ------------------------------------------------------------ host side
@@ -551,7 +632,6 @@ template <int D, int BITS, int GPB>
 static int go_down(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
     return launch_with_lds<k_moe_down<D, BITS, GPB>>(grid, dim3(kThreads), smem, st, p);
 }
-
 // Instances: every width for d in {2, 4, 8}, scale groups of 64 weights.
 #define VQK_MOE_BITS(X, D, G) \
     X(D, 2, G) X(D, 3, G) X(D, 4, G) X(D, 5, G) X(D, 6, G) X(D, 7, G) X(D, 8, G) X(D, 9, G) \
