@@ -104,6 +104,56 @@ __device__ __forceinline__ float block_dot(const uint32_t (&w)[BITS], const h2 (
     return acc;
 }
 
+// One codebook entry (D halves) as a vector, and its dot with D x values.
+template <int D> struct EntryT;
+template <> struct EntryT<2> { typedef h2 type; };
+template <> struct EntryT<4> { typedef h4 type; };
+template <> struct EntryT<8> { typedef h8 type; };
+
+template <int D>
+__device__ __forceinline__ float dot_vec(typename EntryT<D>::type e, const h2 *x, float acc) {
+    if constexpr (D == 2) {
+        return __builtin_amdgcn_fdot2(e, x[0], acc, false);
+    } else if constexpr (D == 4) {
+        acc = __builtin_amdgcn_fdot2(h2{e[0], e[1]}, x[0], acc, false);
+        return __builtin_amdgcn_fdot2(h2{e[2], e[3]}, x[1], acc, false);
+    } else {
+        acc = __builtin_amdgcn_fdot2(h2{e[0], e[1]}, x[0], acc, false);
+        acc = __builtin_amdgcn_fdot2(h2{e[2], e[3]}, x[1], acc, false);
+        acc = __builtin_amdgcn_fdot2(h2{e[4], e[5]}, x[2], acc, false);
+        return __builtin_amdgcn_fdot2(h2{e[6], e[7]}, x[3], acc, false);
+    }
+}
+
+// block_dot for a table only partly in LDS: entries below `kl` are read from
+// the LDS copy `cbl`, the rest from the global table `cbg` (clamped to kmax).
+// The two reads run under complementary lane masks into the same registers,
+// so each code costs one read and one set of dot products, and the L2 sees
+// requests only for the codes beyond the LDS part.
+template <int D, int BITS, int GPB>
+__device__ __forceinline__ float block_dot_hyb(const uint32_t (&w)[BITS], const h2 (&xr)[16 * D],
+                                               const float (&s)[GPB], const h2 *cbl, const h2 *cbg,
+                                               uint32_t kl, uint32_t kmax) {
+    typedef typename EntryT<D>::type E;
+    constexpr int CPG = kBlock / GPB;
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < GPB; ++g) {
+        float ga = 0.f;
+#pragma unroll
+        for (int q = 0; q < CPG; ++q) {
+            const int i = g * CPG + q;
+            const uint32_t c = block_field<BITS>(w, i);
+            E e;
+            if (c < kl) e = reinterpret_cast<const E *>(cbl)[c];
+            else e = reinterpret_cast<const E *>(cbg)[min(c, kmax)];
+            ga = dot_vec<D>(e, &xr[i * (D / 2)], ga);
+        }
+        acc = fmaf(s[g], ga, acc);
+    }
+    return acc;
+}
+
 template <int BITS, int GPB>
 __device__ __forceinline__ void load_block(const GemvParams &p, int64_t cr, int blk, int sidx,
                                            uint32_t (&w)[BITS], float (&s)[GPB]) {

@@ -18,6 +18,7 @@
 //               atomics, deterministic.
 #include "vqk_gemv.h"
 #include "vqk_internal.h"
+#include "vqk_big.h"
 
 namespace vqk {
 
@@ -186,9 +187,20 @@ __device__ __forceinline__ int64_t moe_row(const MoeW &w, int64_t e, int OUT, in
 
 // ------------------------------------------------------------ K1: gate/up
 // LDS of the gate/up phase: two codebook tables, then x at the padded stride.
+// Tables beyond the LDS-resident limit keep their first entries in LDS
+// (64 KB per gate/up table, 112 KB of the routed down table) and gather the
+// rest from L2: fewer L2 requests per code, the rate that bounds these kernels.
+constexpr int kHybUpBytes = 64 * 1024;
+constexpr int kHybDownBytes = 112 * 1024;
+
+// Entries of one gate/up table held in LDS, and of the routed down table.
 template <int D, int BITS>
-__host__ __device__ constexpr size_t up_cb_bytes() {
-    return cb_in_lds(D, BITS) ? size_t(2) * (size_t(1) << BITS) * D * 2 : 0;
+__host__ __device__ constexpr int up_cbn() {
+    return cb_in_lds(D, BITS) ? (1 << BITS) : kHybUpBytes / (2 * D);
+}
+template <int D, int BITS>
+__host__ __device__ constexpr int down_cbn() {
+    return cb_in_lds(D, BITS) ? (1 << BITS) : kHybDownBytes / (2 * D);
 }
 
 // Routing of the workgroup's token as wave 0 computed it (LDS).
@@ -215,7 +227,7 @@ template <int D, int BITS, int GPB, typename PRE>
 __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, uint8_t *smem,
                                         RouteLds &rl, PRE pre) {
     constexpr bool CBL = cb_in_lds(D, BITS);
-    constexpr int CBN = CBL ? (1 << BITS) : 0;
+    constexpr int CBN = up_cbn<D, BITS>();         // entries of each table in LDS
     constexpr int XH = kBlock * D, XS = XH + 8;
     h2 *cbg_lds = reinterpret_cast<h2 *>(smem);
     h2 *cbu_lds = reinterpret_cast<h2 *>(smem + CBN * D * 2);
@@ -295,6 +307,7 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
     load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
     const h2 *cbg = CBL ? cbg_lds : reinterpret_cast<const h2 *>(wg.codebook);
     const h2 *cbu = CBL ? cbu_lds : reinterpret_cast<const h2 *>(wu.codebook);
+    const uint32_t klg = uint32_t(min(wg.K, CBN)), klu = uint32_t(min(wu.K, CBN));
     uint16_t *hrow = p.h + (int64_t(t) * p.P + j) * p.I;
 
     for (int st = 0; st < p.steps1; ++st) {
@@ -310,8 +323,13 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
         moe_load<BITS, GPB>(wg, ncg, blk, sidx, p.ngrp1, ng, nsg);
         moe_load<BITS, GPB>(wu, ncu, blk, sidx, p.ngrp1, nu, nsu);
         float vg = 0.f, vu = 0.f;
-        if (crg >= 0) vg = block_dot<D, BITS, GPB, CBL>(ag, xr, sg_, cbg, uint32_t(wg.K - 1));
-        if (cru >= 0) vu = block_dot<D, BITS, GPB, CBL>(au, xr, su_, cbu, uint32_t(wu.K - 1));
+        if constexpr (CBL) {
+            if (crg >= 0) vg = block_dot<D, BITS, GPB, true>(ag, xr, sg_, cbg, uint32_t(wg.K - 1));
+            if (cru >= 0) vu = block_dot<D, BITS, GPB, true>(au, xr, su_, cbu, uint32_t(wu.K - 1));
+        } else {
+            if (crg >= 0) vg = block_dot_hyb<D, BITS, GPB>(ag, xr, sg_, cbg_lds, cbg, klg, uint32_t(wg.K - 1));
+            if (cru >= 0) vu = block_dot_hyb<D, BITS, GPB>(au, xr, su_, cbu_lds, cbu, klu, uint32_t(wu.K - 1));
+        }
         vg = group_sum(vg, lpr);
         vu = group_sum(vu, lpr);
         const int r = row_at(st);
@@ -378,14 +396,15 @@ __device__ __forceinline__ void down_prep(const MoeParams &p, int bx, int t, con
     moe_load<BITS, GPB>(wd, ds.cr, dl.blk, sidx, p.ngrp2, ds.a, ds.s);
 }
 
-template <int D, int CBN>
+// Routed down table (all of it, or its first CBN entries) and, when the
+// whole table fits, the shared expert's; a partly staged routed table leaves
+// the shared expert's to L2.
+template <int D, int CBN, bool CBL>
 __device__ __forceinline__ void down_stage_cb(const MoeParams &p, uint8_t *smem) {
-    if constexpr (CBN > 0) {
-        stage_codebook_fixed<D, CBN, kThreads>(p.down.codebook, p.down.K, reinterpret_cast<h2 *>(smem));
-        if (p.shared)
-            stage_codebook_fixed<D, CBN, kThreads>(p.sdown.codebook, p.sdown.K,
-                                                   reinterpret_cast<h2 *>(smem + CBN * D * 2));
-    }
+    stage_codebook_fixed<D, CBN, kThreads>(p.down.codebook, p.down.K, reinterpret_cast<h2 *>(smem));
+    if (CBL && p.shared)
+        stage_codebook_fixed<D, CBN, kThreads>(p.sdown.codebook, p.sdown.K,
+                                               reinterpret_cast<h2 *>(smem + CBN * D * 2));
 }
 
 // The token's P SwiGLU rows (fp16) -> LDS at the padded block stride, then
@@ -395,11 +414,11 @@ template <int D, int BITS, int GPB>
 __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint8_t *smem,
                                          const DownLane &dl, DownState<BITS, GPB> &ds) {
     constexpr bool CBL = cb_in_lds(D, BITS);
-    constexpr int CBN = CBL ? (1 << BITS) : 0;
+    constexpr int CBN = down_cbn<D, BITS>();
     constexpr int XH = kBlock * D, XS = XH + 8;
     h2 *cbd_lds = reinterpret_cast<h2 *>(smem);
     h2 *cbs_lds = reinterpret_cast<h2 *>(smem + CBN * D * 2);
-    f16 *xs = reinterpret_cast<f16 *>(smem + (1 + p.shared) * CBN * D * 2);
+    f16 *xs = reinterpret_cast<f16 *>(smem + ((CBL && p.shared) ? 2 : 1) * CBN * D * 2);
     const int tid = threadIdx.x, wave = tid >> 6;
     const MoeW &wd = dl.is_shared ? p.sdown : p.down;
     {
@@ -434,6 +453,7 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
     const h2 *cb = CBL ? (dl.is_shared ? cbs_lds : cbd_lds)
                        : reinterpret_cast<const h2 *>(wd.codebook);
     const uint32_t kmax = uint32_t(wd.K - 1);
+    const uint32_t kl = dl.is_shared ? 0u : uint32_t(min(wd.K, CBN));     // partly staged: routed only
     const int sidx = GPB == 1 ? dl.blk / p.bpg2 : dl.blk * GPB;
     const int r_wg = bx * p.rows_per_wg2;
     auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * dl.rpw + dl.sub; };
@@ -448,7 +468,11 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
         const int64_t crn = st + 1 < p.steps2 ? code_row(st + 1) : -1;
         moe_load<BITS, GPB>(wd, crn, dl.blk, sidx, p.ngrp2, n, ns);
         float acc = 0.f;
-        if (ds.cr >= 0) acc = ds.wj * block_dot<D, BITS, GPB, CBL>(ds.a, xr, ds.s, cb, kmax);
+        if constexpr (CBL) {
+            if (ds.cr >= 0) acc = ds.wj * block_dot<D, BITS, GPB, true>(ds.a, xr, ds.s, cb, kmax);
+        } else {
+            if (ds.cr >= 0) acc = ds.wj * block_dot_hyb<D, BITS, GPB>(ds.a, xr, ds.s, cbd_lds, cb, kl, kmax);
+        }
         acc = group_sum(acc, dl.lpr);
         const int r = row_at(st);
         if (dl.v == dl.lpr - 1 && r < p.H) store_act(p.y, p.y_type, int64_t(t) * p.H + r, acc);
@@ -462,10 +486,10 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
 
 template <int D, int BITS, int GPB>
 __global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
-    constexpr int CBN = cb_in_lds(D, BITS) ? (1 << BITS) : 0;
+    constexpr int CBN = down_cbn<D, BITS>();
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = int(blockIdx.y);
-    down_stage_cb<D, CBN>(p, smem);            // independent of the routing: first
+    down_stage_cb<D, CBN, cb_in_lds(D, BITS)>(p, smem);   // independent of the routing: first
     const DownLane dl(p);
     DownState<BITS, GPB> ds;
     down_prep<BITS, GPB>(p, int(blockIdx.x), t, dl,
@@ -474,20 +498,73 @@ __global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
     down_run<D, BITS, GPB>(p, int(blockIdx.x), t, smem, dl, ds);
 }
 
+// ------------------------------------------------ codebooks beyond LDS
+// For tables the block-per-lane kernels would gather from L2 (config 3:
+// d8 K16384), the layer is composed of four launches: routing (one wave per
+// token), the sliced-codebook GEMV over routed + shared gate/up, the same
+// over routed + shared down with silu(g) * u built as its input, and the
+// weighted combine.
+__global__ void __launch_bounds__(kWave) k_route_tokens(const MoeParams p) {
+    const int t = int(blockIdx.x), lane = int(threadIdx.x);
+    int e_pair, my_idx = -1;
+    float my_w = 0.f;
+    CbPair<2, 0> none{};
+    route(p.logits + int64_t(t) * p.E, p.E, p.top_k, p.norm, -1, &e_pair, &my_idx, &my_w,
+          &issue_cb_pair<2, 0>, &none);
+    if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
+    if (lane < p.top_k) {
+        p.ids[t * p.top_k + lane] = my_idx;
+        p.wts[t * p.top_k + lane] = my_w;
+        if (p.ids_out) p.ids_out[t * p.top_k + lane] = my_idx;
+        if (p.wts_out) p.wts_out[t * p.top_k + lane] = my_w;
+    }
+    if (p.shared) {
+        float acc = 0.f;
+        for (int i = lane; i < p.H; i += kWave)
+            acc += load_act(p.x, p.x_type, int64_t(t) * p.H + i) * load_act(p.sg_vec, p.sg_type, i);
+        acc = wave_sum(acc);
+        if (lane == 0) p.sg[t] = 1.f / (1.f + __expf(-acc));
+    }
+}
+
+// y[t, r] = sum_j w[t, j] * yd[t * k + j, r] + sg[t] * ysh[t, r]
+__global__ void __launch_bounds__(256) k_moe_combine(const MoeParams p, const float *yd,
+                                                     const float *ysh) {
+    const int t = int(blockIdx.y);
+    const int r = int(blockIdx.x) * 256 + int(threadIdx.x);
+    if (r >= p.H) return;
+    float acc = 0.f;
+    for (int j = 0; j < p.top_k; ++j)
+        acc += p.wts[t * p.top_k + j] * yd[(int64_t(t) * p.top_k + j) * p.H + r];
+    if (p.shared) acc += p.sg[t] * ysh[int64_t(t) * p.H + r];
+    store_act(p.y, p.y_type, int64_t(t) * p.H + r, acc);
+}
+
 // ------------------------------------------------------------ host side
 static size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
 struct MoeLayout {
     size_t ids, wts, sg, h, total;
+    size_t g, u, sgg, sgu, yd, ysh;      // composed (codebooks beyond LDS) path only
 };
 
-static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I) {
+static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I, int64_t H, bool big) {
     MoeLayout L;
     L.ids = 0;
     L.wts = align_up(L.ids + sizeof(int32_t) * T * k);
     L.sg = align_up(L.wts + sizeof(float) * T * k);
     L.h = align_up(L.sg + sizeof(float) * T);
     L.total = align_up(L.h + 2 * size_t(T) * P * I);
+    L.g = L.u = L.sgg = L.sgu = L.yd = L.ysh = 0;
+    if (big) {
+        L.g = L.total;
+        L.u = align_up(L.g + 4 * size_t(T) * k * I);
+        L.sgg = align_up(L.u + 4 * size_t(T) * k * I);
+        L.sgu = align_up(L.sgg + 4 * size_t(T) * I);
+        L.yd = align_up(L.sgu + 4 * size_t(T) * I);
+        L.ysh = align_up(L.yd + 4 * size_t(T) * k * H);
+        L.total = align_up(L.ysh + 4 * size_t(T) * H);
+    }
     return L;
 }
 
@@ -512,6 +589,7 @@ struct MoePlan {
     MoeLayout lay;
     size_t smem1, smem2;
     dim3 grid1, grid2;
+    bool big;                 // codebooks beyond LDS: the composed sliced-codebook path
 };
 
 static int lg2(int64_t v) {
@@ -610,14 +688,25 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
         p.rows_per_wg2 = int32_t(4 * rpw * st);
         pl->grid2 = dim3(unsigned((gd.OUT + p.rows_per_wg2 - 1) / p.rows_per_wg2), unsigned(T), 1);
     }
-    const size_t cb1 = cb_in_lds(gg.D, gg.BITS) ? (size_t(1) << gg.BITS) * gg.D * 2 : 0;
-    const size_t cb2 = cb_in_lds(gd.D, gd.BITS) ? (size_t(1) << gd.BITS) * gd.D * 2 : 0;
+    const bool full1 = cb_in_lds(gg.D, gg.BITS), full2 = cb_in_lds(gd.D, gd.BITS);
+    const size_t cb1 = full1 ? (size_t(1) << gg.BITS) * gg.D * 2 : size_t(kHybUpBytes);
+    const size_t cb2 = full2 ? (size_t(1) << gd.BITS) * gd.D * 2 : size_t(kHybDownBytes);
     pl->smem1 = 2 * cb1 + size_t(gg.NB) * (kBlock * gg.D + 8) * 2;
-    pl->smem2 = (shared ? 2 : 1) * cb2 + size_t(P) * gd.NB * (kBlock * gd.D + 8) * 2;
+    pl->smem2 = ((shared && full2) ? 2 : 1) * cb2 + size_t(P) * gd.NB * (kBlock * gd.D + 8) * 2;
     if (pl->smem1 > 160 * 1024 || pl->smem2 > 160 * 1024)
         return set_error(VQK_ENOTIMPL, "fused layer: LDS need %zu / %zu B exceeds 160 KB",
                          pl->smem1, pl->smem2);
-    pl->lay = moe_layout(T, k, P, gg.OUT);
+    // batch >= 2: the composed sliced-codebook path; batch 1 keeps the two fused
+    // kernels (partly LDS-staged tables), which measured faster there
+    pl->big = T >= 2 && big_fits(gg, m->gate) && big_fits(gu, m->up) && big_fits(gd, m->down);
+    if (pl->big && shared) {
+        Geom a, b, c;
+        make_geom(m->sh_gate, &a);
+        make_geom(m->sh_up, &b);
+        make_geom(m->sh_down, &c);
+        pl->big = big_fits(a, m->sh_gate) && big_fits(b, m->sh_up) && big_fits(c, m->sh_down);
+    }
+    pl->lay = moe_layout(T, k, P, gg.OUT, gg.IN, pl->big);
     return VQK_OK;
 }
 
@@ -653,6 +742,86 @@ int launch_moe_down(const MoeParams &p, int d, int bits, int gpb, dim3 grid, siz
     VQK_MOE_BITS(VQK_DN_CASE, 8, 4)
     return set_error(VQK_ENOTIMPL, "fused layer: no kernel for d=%d bits=%d (%d groups/block); "
                      "the fused layer takes scale groups of 64 weights", d, bits, gpb);
+}
+
+static void seg_of(const vqk_weights *w, BigSeg *s, const int32_t *eidx, int32_t N, int32_t xkrep,
+                   int32_t wg0, int32_t wgpp, int32_t rows) {
+    Geom g;
+    make_geom(w, &g);
+    big_seg_weights(w, g, s);
+    s->eidx = eidx;
+    s->N = N;
+    s->xkrep = xkrep;
+    s->wg0 = wg0;
+    s->wg_per_pair = wgpp;
+    s->rows_per_wg = rows;
+}
+
+static int launch_moe_big(const vqk_moe_desc *m, const MoePlan &pl, uint8_t *ws, hipStream_t st) {
+    const MoeParams &p = pl.p;
+    const int T = p.T, k = p.top_k;
+    const bool sh = p.shared != 0;
+    float *g = reinterpret_cast<float *>(ws + pl.lay.g), *u = reinterpret_cast<float *>(ws + pl.lay.u);
+    float *sgg = reinterpret_cast<float *>(ws + pl.lay.sgg), *sgu = reinterpret_cast<float *>(ws + pl.lay.sgu);
+    float *yd = reinterpret_cast<float *>(ws + pl.lay.yd), *ysh = reinterpret_cast<float *>(ws + pl.lay.ysh);
+    hipLaunchKernelGGL(k_route_tokens, dim3(unsigned(T)), dim3(kWave), 0, st, p);
+    int rc = hip_status(hipGetLastError(), "routing launch");
+    if (rc) return rc;
+    {   // gate / up, routed and shared: fp32 rows
+        BigParams b;
+        memset(&b, 0, sizeof b);
+        const int rows = big_plan_rows(&b, pl.g1.NB, p.I, int64_t(T) * (sh ? k + 1 : k) * 2 * p.I);
+        const int wgpp = (p.I + rows - 1) / rows;
+        int wg0 = 0, ns = 0;
+        const vqk_weights *mods[4] = {m->gate, m->up, m->sh_gate, m->sh_up};
+        float *outs[4] = {g, u, sgg, sgu};
+        for (int i = 0; i < (sh ? 4 : 2); ++i) {
+            const bool routed = i < 2;
+            const int32_t N = routed ? T * k : T;
+            BigSeg &s = b.seg[ns++];
+            seg_of(mods[i], &s, routed ? p.ids : nullptr, N, routed ? k : 1, wg0, wgpp, rows);
+            s.x = p.x;
+            s.x_type = p.x_type;
+            s.x_stride = p.H;
+            s.y = outs[i];
+            s.y_type = VQK_F32;
+            s.y_stride = p.I;
+            wg0 += N * wgpp;
+        }
+        b.nseg = ns;
+        b.IN = p.H;
+        b.NB = int32_t(pl.g1.NB);
+        if ((rc = launch_gemv_big(b, pl.g1.D, pl.g1.BITS, pl.g1.gpb, dim3(unsigned(big_grid(wg0))), st)))
+            return rc;
+    }
+    {   // down, routed and shared, input silu(g) * u per pair
+        BigParams b;
+        memset(&b, 0, sizeof b);
+        const int rows = big_plan_rows(&b, pl.g2.NB, p.H, int64_t(T) * (sh ? k + 1 : k) * p.H);
+        const int wgpp = (p.H + rows - 1) / rows;
+        int wg0 = 0, ns = 0;
+        for (int i = 0; i < (sh ? 2 : 1); ++i) {
+            const bool routed = i == 0;
+            const int32_t N = routed ? T * k : T;
+            BigSeg &s = b.seg[ns++];
+            seg_of(routed ? m->down : m->sh_down, &s, routed ? p.ids : nullptr, N, 1, wg0, wgpp, rows);
+            s.xg = routed ? g : sgg;
+            s.xu = routed ? u : sgu;
+            s.x_stride = p.I;
+            s.y = routed ? yd : ysh;
+            s.y_type = VQK_F32;
+            s.y_stride = p.H;
+            wg0 += N * wgpp;
+        }
+        b.nseg = ns;
+        b.IN = p.I;
+        b.NB = int32_t(pl.g2.NB);
+        if ((rc = launch_gemv_big(b, pl.g2.D, pl.g2.BITS, pl.g2.gpb, dim3(unsigned(big_grid(wg0))), st)))
+            return rc;
+    }
+    hipLaunchKernelGGL(k_moe_combine, dim3(unsigned((p.H + 255) / 256), unsigned(T)), dim3(256), 0, st,
+                       p, static_cast<const float *>(yd), static_cast<const float *>(ysh));
+    return hip_status(hipGetLastError(), "combine launch");
 }
 
 }  // namespace vqk
@@ -696,6 +865,7 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, i
     p.y = y;
     p.y_type = y_type;
     hipStream_t st = hipStream_t(stream);
+    if (pl.big) return launch_moe_big(m, pl, ws, st);
     rc = launch_moe_up(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.grid1, pl.smem1, st);
     if (rc) return rc;
     return launch_moe_down(p, pl.g2.D, pl.g2.BITS, pl.g2.gpb, pl.grid2, pl.smem2, st);
