@@ -21,6 +21,7 @@ constexpr int kWave = 64;            // CDNA wavefront width
 constexpr int kBlock = 32;           // codes per packing block
 constexpr int kThreads = 256;        // threads per workgroup of the GEMV kernels
 constexpr int kCbLdsMax = 64 * 1024; // largest codebook table staged in LDS (bytes)
+constexpr int kGemvHybBytes = 128 * 1024;  // part of a larger table the GEMV keeps in LDS
 
 // A codebook table of 2^BITS entries of D halves is staged in LDS when it
 // fits kCbLdsMax; larger tables are gathered from L2 / MALL.

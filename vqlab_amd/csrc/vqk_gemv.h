@@ -19,7 +19,9 @@
 //     a lane keeps the same block index for every row it visits, so its slice
 //     of x (32*D fp16 values) is read from LDS once into registers;
 //   * the codebook is staged into LDS as a 2^BITS-entry table when that fits
-//     kCbLdsMax, otherwise gathered from L2 / MALL (codes clamped to K-1);
+//     kCbLdsMax; a larger table keeps its first kGemvHybBytes in LDS and the
+//     codes beyond it gather from L2 / MALL (clamped to K-1), which cuts the
+//     L2 requests -- the rate that bounds such tables -- by that fraction;
 //   * each wave issues the loads of its next row step before it decodes the
 //     current one.
 // Shapes outside the fast kernel's reach (ragged NSUB, rows not word
@@ -317,7 +319,8 @@ __device__ __forceinline__ void load_xregs(const f16 *src, h2 (&xr)[16 * D]) {
 template <int D, int BITS, int GPB>
 __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
     constexpr bool CBL = cb_in_lds(D, BITS);
-    constexpr int CBN = CBL ? (1 << BITS) : 0;   // LDS table entries
+    // LDS table entries: the whole table, or the first kGemvHybBytes of it
+    constexpr int CBN = CBL ? (1 << BITS) : kGemvHybBytes / (2 * D);
     constexpr int XH = kBlock * D;               // x halves per block
     constexpr int XS = XH + 8;                   // padded LDS stride: 16 B skew per block
     extern __shared__ __align__(16) uint8_t smem[];
@@ -349,7 +352,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
     int64_t cr = code_row(0);
     load_block<BITS, GPB>(p, cr, blk, sidx, w, s);   // in flight during staging
 
-    if constexpr (CBL) stage_codebook_fixed<D, CBN, kThreads>(p.codebook, p.K, cb_lds);
+    stage_codebook_fixed<D, CBN, kThreads>(p.codebook, p.K, cb_lds);
     stage_x<XH, XS>(p.x, p.x_type, int64_t(tok) * p.x_stride, p.IN, p.NB, xs);
     wait_vmem();
     __syncthreads();
@@ -358,6 +361,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
     load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
     const h2 *cb = CBL ? cb_lds : reinterpret_cast<const h2 *>(p.codebook);
     const uint32_t kmax = uint32_t(p.K - 1);
+    const uint32_t kl = uint32_t(min(p.K, CBN));
 
     for (int st = 0; st < p.steps; ++st) {
         uint32_t wn[BITS];
@@ -365,7 +369,11 @@ __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
         const int64_t crn = st + 1 < p.steps ? code_row(st + 1) : -1;
         load_block<BITS, GPB>(p, crn, blk, sidx, wn, sn);
         float v = 0.f;
-        if (cr >= 0) v = block_dot<D, BITS, GPB, CBL>(w, xr, s, cb, kmax);
+        if constexpr (CBL) {
+            if (cr >= 0) v = block_dot<D, BITS, GPB, true>(w, xr, s, cb, kmax);
+        } else {
+            if (cr >= 0) v = block_dot_hyb<D, BITS, GPB>(w, xr, s, cb_lds, cb, kl, kmax);
+        }
         v = group_sum(v, lpr);
         const int r = row_at(st);
         if (blk == lpr - 1 && r < p.OUT) store_act(p.y, p.y_type, int64_t(pair) * p.y_stride + r, v);

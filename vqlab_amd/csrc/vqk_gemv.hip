@@ -3,7 +3,6 @@
 // Both validate on the host, pick the fast or the generic kernel and launch.
 #include "vqk_gemv.h"
 #include "vqk_internal.h"
-#include "vqk_big.h"
 
 namespace vqk {
 
@@ -38,7 +37,7 @@ int gemv_fill_params(const vqk_weights *w, const Geom &g, GemvParams *p) {
 }
 
 size_t gemv_fast_lds(const Geom &g) {
-    const size_t cb = cb_in_lds(g.D, g.BITS) ? (size_t(1) << g.BITS) * g.D * 2 : 0;
+    const size_t cb = cb_in_lds(g.D, g.BITS) ? (size_t(1) << g.BITS) * g.D * 2 : size_t(kGemvHybBytes);
     return cb + size_t(g.NB) * (kBlock * g.D + 8) * 2;
 }
 
@@ -67,31 +66,6 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
     p.y_type = y_type;
     p.y_stride = g.OUT;
     const int64_t chunk = (65535 / xkrep) * xkrep;   // grid.y limit, whole tokens per chunk
-    if (big_fits(g, w) && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
-        // codebook beyond LDS: slices through LDS instead of L2 gathers
-        BigParams bp;
-        memset(&bp, 0, sizeof bp);
-        BigSeg &sg = bp.seg[0];
-        big_seg_weights(w, g, &sg);
-        sg.eidx = reinterpret_cast<const int32_t *>(eidx);
-        sg.N = int32_t(N);
-        sg.xkrep = int32_t(xkrep);
-        sg.x = x;
-        sg.x_type = x_type;
-        sg.x_stride = g.IN;
-        sg.y = y;
-        sg.y_type = y_type;
-        sg.y_stride = g.OUT;
-        sg.rows_per_wg = big_plan_rows(&bp, g.NB, g.OUT, N * g.OUT);
-        sg.wg_per_pair = int32_t((g.OUT + sg.rows_per_wg - 1) / sg.rows_per_wg);
-        sg.wg0 = 0;
-        bp.nseg = 1;
-        bp.IN = int32_t(g.IN);
-        bp.NB = int32_t(g.NB);
-        const int64_t items = N * sg.wg_per_pair;
-        if (items > INT32_MAX) return set_error(VQK_ENOTIMPL, "too many rows");
-        return launch_gemv_big(bp, g.D, g.BITS, g.gpb, dim3(unsigned(big_grid(items))), st);
-    }
     if (g.fast_ok) {
         const int rpw = kWave >> p.lpr_log2;
         const int64_t steps_total = N * ((g.OUT + rpw - 1) / rpw);   // wave steps overall
