@@ -16,6 +16,11 @@
 // of an LDS copy of the tokens' activations, so A and B use the same k
 // permutation and the product is the plain dot product.
 //
+// The codebook table sits in LDS (all of it, or its first 88-128 KB when it
+// is larger; those codes beyond it are read from L2), with one zero entry
+// past the staged part: lanes without a block (dead skipzero row, past the
+// row's end) decode code 0 from it with scale 0, i.e. weights +0.
+//
 // Workgroup = 4 waves x 2 row tiles of 16 = 128 weight rows; one token tile
 // of <= 16 rows (grouped: one tile of an expert segment from the device
 // sort, vq_switch.py:4590-4610; dense: 16 consecutive rows of x). The K loop
@@ -84,9 +89,43 @@ __device__ __forceinline__ h8 step_entries(const uint32_t (&w)[BITS], int s, con
     }
 }
 
-// A zero entry for lanes without a block (dead row, past the row's end):
-// their codes read 0 from here and their scale is 0, so their weights are +0.
-static __device__ __align__(16) const uint16_t kSegZeroEntry[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+// The same for a table only partly in LDS: codes below `kl` read the LDS
+// copy, the rest the global table (clamped to kmax), under complementary
+// lane masks into the same registers.
+template <int D>
+__device__ __forceinline__ typename EntryT<D>::type hyb_entry(uint32_t c, const f16 *tl, const f16 *tg,
+                                                              uint32_t kl, uint32_t kmax) {
+    typedef typename EntryT<D>::type E;
+    E e;
+    if (c < kl) e = reinterpret_cast<const E *>(tl)[c];
+    else e = reinterpret_cast<const E *>(tg)[min(c, kmax)];
+    return e;
+}
+
+template <int D, int BITS>
+__device__ __forceinline__ h8 step_entries_hyb(const uint32_t (&w)[BITS], int s, const f16 *tl,
+                                               const f16 *tg, uint32_t kl, uint32_t kmax) {
+    if constexpr (D == 8) {
+        return hyb_entry<8>(block_field<BITS>(w, s), tl, tg, kl, kmax);
+    } else if constexpr (D == 4) {
+        const h4 a = hyb_entry<4>(block_field<BITS>(w, 2 * s), tl, tg, kl, kmax);
+        const h4 b = hyb_entry<4>(block_field<BITS>(w, 2 * s + 1), tl, tg, kl, kmax);
+        return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    } else {
+        const h2 a = hyb_entry<2>(block_field<BITS>(w, 4 * s), tl, tg, kl, kmax);
+        const h2 b = hyb_entry<2>(block_field<BITS>(w, 4 * s + 1), tl, tg, kl, kmax);
+        const h2 e = hyb_entry<2>(block_field<BITS>(w, 4 * s + 2), tl, tg, kl, kmax);
+        const h2 f = hyb_entry<2>(block_field<BITS>(w, 4 * s + 3), tl, tg, kl, kmax);
+        return h8{a[0], a[1], b[0], b[1], e[0], e[1], f[0], f[1]};
+    }
+}
+
+// LDS entries of a table too large for LDS that the kernel stages (what the
+// x double buffer leaves of the 160 KB).
+__host__ __device__ constexpr int seg_hyb_entries(int D) {
+    return (D == 8 ? 88 * 1024 : (D == 4 ? 120 * 1024 : 128 * 1024)) / (2 * D);
+}
+
 
 template <int D, int BITS, int GPB, bool CBL>
 __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
@@ -97,11 +136,12 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     constexpr int PIECES = kSegTok * CC / 8;    // 16-byte pieces per chunk
     constexpr int PPT = PIECES / 256;
     static_assert(PIECES % 256 == 0, "chunk must split evenly over 256 threads");
-    constexpr int CBN = 1 << BITS;              // LDS table entries (CBL)
+    // LDS table entries: the whole table, or the first seg_hyb_entries of it
+    constexpr int CBN = CBL ? (1 << BITS) : seg_hyb_entries(D);
 
     extern __shared__ __align__(16) uint8_t smem[];
     f16 *xs = reinterpret_cast<f16 *>(smem);    // [2][kSegTok][XS]
-    f16 *cbl = xs + 2 * kSegTok * XS;           // [CBN + 1][D] (CBL); entry CBN is zero
+    f16 *cbl = xs + 2 * kSegTok * XS;           // [CBN + 1][D]; entry CBN is zero
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ln = lane & 15, lg = lane >> 4;
@@ -121,7 +161,7 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     }
     const int o0 = int(blockIdx.x) * kSegRows + wave * 32;
 
-    if constexpr (CBL) {
+    {
         const int ent = min(p.K, CBN);
         lds_copy_async(p.codebook, cbl, ent * D * 2, (CBN + 1) * D * 2);
     }
@@ -203,19 +243,22 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
                        const bool (&live)[TN]) {
         const f16 *xb = xs + (buf * kSegTok + ln) * XS + lg * (32 * D);
         const f16 *tab[TN];
+        uint32_t kl[TN];
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) {
-            if constexpr (CBL) tab[tn] = live[tn] ? cbl : cbl + CBN * D;
-            else tab[tn] = live[tn] ? reinterpret_cast<const f16 *>(p.codebook)
-                                    : reinterpret_cast<const f16 *>(kSegZeroEntry);
+            tab[tn] = live[tn] ? cbl : cbl + CBN * D;        // dead lanes: code 0 -> zero entry
+            kl[tn] = live[tn] ? uint32_t(min(p.K, CBN)) : 1u;
         }
+        const f16 *tg = reinterpret_cast<const f16 *>(p.codebook);
 #pragma unroll
         for (int st = 0; st < SPB; ++st) {
             const h8 xf = *reinterpret_cast<const h8 *>(xb + 8 * st);
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) {
                 const int q = (st * GPB) / (4 * D);
-                const h8 e = step_entries<D, BITS>(w[tn], st, tab[tn], kmax, !CBL);
+                h8 e;
+                if constexpr (CBL) e = step_entries<D, BITS>(w[tn], st, tab[tn], kmax, false);
+                else e = step_entries_hyb<D, BITS>(w[tn], st, tab[tn], tg, kl[tn], kmax);
                 const h2 sc = s[tn][q];
                 const h8 wv = e * h8{sc[0], sc[0], sc[0], sc[0], sc[0], sc[0], sc[0], sc[0]};
                 acc[tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv, xf, acc[tn], 0, 0, 0);
@@ -276,7 +319,8 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
 
 // LDS bytes of k_seg_mfma<D, BITS, ...>.
 __host__ __device__ constexpr size_t seg_lds(int D, int BITS, bool cbl) {
-    return size_t(2) * kSegTok * (128 * D + 8) * 2 + (cbl ? (size_t(1) << BITS) * D * 2 + D * 2 : 0);
+    return size_t(2) * kSegTok * (128 * D + 8) * 2 +
+           (size_t(cbl ? (1 << BITS) : seg_hyb_entries(D)) + 1) * D * 2;
 }
 
 // Launches k_seg_mfma for geometry-dependent template arguments; returns a
