@@ -45,6 +45,8 @@ extern "C" {
 #define VQK_U8    3
 #define VQK_U16   4
 #define VQK_U32   5
+#define VQK_I32   6
+#define VQK_I64   7
 
 /* One VQ-coded linear, or a stack of E expert linears sharing one codebook
  * (VQSwitchLinear, vq_switch.py:5198-5234; VQLinear, vq_dense.py:322-334).
@@ -190,6 +192,20 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type,
                          int64_t T, const float *logits, void *y,
                          int32_t y_type, int32_t *topk_ids, float *topk_w,
                          void *workspace, size_t ws_bytes, void *stream);
+
+/* ---- gather-only embeddings: VQEmbedding.__call__ (vq_dense.py:444-502) and
+ * VQPLEEmbedding.__call__ (vq_switch.py:5426-5495) ------------------------------
+ * out[i, :] = row ids[i] of the table, decoded bit-exactly
+ * (fp16(f32(cb[c]) * f32(s))) and converted to out_type (VQK_F16 / VQK_BF16 /
+ * VQK_F32; bf16 is one RNE from the fp16 value, like .astype(bfloat16)).
+ * The table is a vqk_weights with E == 1 and OUT = table rows; d is 1..16.
+ * Code rows: unpacked uint8 / uint16, block-packed uint32 (pack_bits), or the
+ * PLE byte stream -- code_type VQK_U8 with pack_bits > 0: code j at bits
+ * [j * pack_bits, (j + 1) * pack_bits) of the row's code_cols bytes, LSB
+ * first (vq_switch.py:5449-5470). ids: n device VQK_I32 / VQK_I64 entries;
+ * an id outside [0, OUT) yields a row of +0. out: [n, IN] device array. */
+int vqk_embed_gather(const vqk_weights *w, const void *ids, int32_t id_type,
+                     int64_t n, void *out, int32_t out_type, void *stream);
 
 /* ---- capability predicates (1 = this build has a kernel for the shape) -----
  * dense_fits (vq_switch.py:3290-3306), wdec_fits (3505-3514),

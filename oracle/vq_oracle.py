@@ -20,6 +20,8 @@ Reference anchors (paths relative to the reference checkout):
                                                vq_switch.py:4958-4973
   grouped-GEMM tile metadata                   vq_switch.py:4590-4610,
                                                tests/test_routing_memo.py:51-62
+  embeddings (gather-only decode)              vq_dense.py:491-506 (VQEmbedding),
+                                               vq_switch.py:5426-5495 (VQPLEEmbedding)
 
 Pinning (what checks each function; see tests/test_oracle.py):
   pack/unpack      reference golden sha256 prefixes (bits 4) + bit-serial brute
@@ -36,6 +38,13 @@ Pinning (what checks each function; see tests/test_oracle.py):
   skipzero         reference golden sha256 prefixes (sz_codes, sz_scales,
                    sz_rowmask, sz_shape) + cumsum brute force for the table.
   tile_meta        the reference test's double loop, restated.
+  ple_unpack       bit-serial brute force over the byte stream (numpy
+                   unpackbits) for widths 1..16 + the width-8 identity the
+                   reference relies on (vq_switch.py:5456-5467).
+  embed_rows       dequant of the gathered rows == the gathered rows of the
+                   full-table dequant; f16_to_bf16 against torch's own
+                   float -> bfloat16 conversion (round to nearest even) over
+                   every fp16 bit pattern.
 """
 from __future__ import annotations
 
@@ -329,3 +338,41 @@ def tile_meta(idx_sorted: np.ndarray, E: int, rtile: int = 32) -> np.ndarray:
             metas.append((e, start + r0, min(rtile, c - r0)))
         start += c
     return np.asarray(metas, np.int32).reshape(-1, 3)
+
+
+# ------------------------------------------------------------- embeddings
+def ple_unpack(rows_u8: np.ndarray, nsub: int, bits: int) -> np.ndarray:
+    """PLE byte-stream rows [..., row_bytes] uint8 -> [..., nsub] codes:
+    code j is the `bits`-wide field at bit j*bits of the row, LSB first, read
+    through the 3-byte window at byte (j*bits)//8 with the row padded by two
+    zero bytes (vq_switch.py:5449-5478)."""
+    b = np.asarray(rows_u8, np.uint8).astype(np.uint32)
+    pad = np.zeros(b.shape[:-1] + (2,), np.uint32)
+    b = np.concatenate([b, pad], axis=-1)
+    bit0 = np.arange(nsub, dtype=np.int64) * bits
+    b0, sh = bit0 // 8, (bit0 % 8).astype(np.uint32)
+    win = b[..., b0] | (b[..., b0 + 1] << np.uint32(8)) | (b[..., b0 + 2] << np.uint32(16))
+    return (win >> sh) & np.uint32((1 << bits) - 1)
+
+
+def f16_to_bf16(h: np.ndarray) -> np.ndarray:
+    """fp16 values -> bfloat16 bit patterns (uint16), round to nearest even,
+    NaN kept NaN: what .astype(bfloat16) does to an fp16 array
+    (vq_dense.py:506, vq_switch.py:5495). fp16 -> fp32 is exact, so this is
+    one rounding of the fp32 value to 8 significand bits."""
+    u = np.asarray(h, np.float16).astype(np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, (u >> 16) | 0x40, r)
+    return r.astype(np.uint16)
+
+
+def embed_rows(ids: np.ndarray, codes: np.ndarray, codebook: np.ndarray,
+               scales: np.ndarray, group: int) -> np.ndarray:
+    """Rows ids of a VQ table, decoded: fp16 [*ids.shape, IN]
+    (vq_dense.py:491-506; vq_switch.py:5480-5495). codes are the unpacked
+    [rows, NSUB] codes; ids must be valid rows."""
+    ids = np.asarray(ids, np.int64)
+    flat = ids.reshape(-1)
+    w = dequant(np.asarray(codes)[flat], codebook, np.asarray(scales)[flat], group)
+    return w.reshape(ids.shape + (w.shape[-1],))

@@ -149,3 +149,48 @@ def test_gemv_argument_errors(L):
     w2 = _w(L, E=2)
     assert lib.vqk_dense_gemv(ctypes.byref(w2), ctypes.c_void_p(16), L.VQK_BF16, 1,
                               ctypes.c_void_p(16), L.VQK_BF16, None) == L.VQK_EINVAL
+
+
+def _emb(L, **kw):
+    w = L.VQKWeights()
+    w.codes, w.codebook, w.scales = 16, 16, 16       # never dereferenced: refused first
+    w.code_type, w.pack_bits, w.K, w.D, w.group = L.VQK_U8, 11, 2048, 4, 32
+    w.E, w.OUT, w.IN = 1, 100, 160
+    w.code_cols = 55                                  # 40 codes x 11 bits = 55 bytes
+    for k, v in kw.items():
+        setattr(w, k, v)
+    return w
+
+
+@pytest.mark.parametrize("kw,rc", [
+    ({"D": 0}, 1),                                    # no subvector dim
+    ({"D": 32, "IN": 160, "group": 32}, 1),           # d beyond 16
+    ({"E": 2}, 2),                                    # a table is one matrix
+    ({"code_cols": 54}, 2),                           # byte stream too short for 40 x 11 bits
+    ({"K": 4096}, 2),                                 # K does not fit 11-bit codes
+    ({"code_type": 4}, 2),                            # packed rows are bytes or u32 words
+    ({"pack_bits": 0, "code_cols": 40}, 2),           # uint8 codes, K=2048
+    ({"pack_bits": 0, "code_type": 4, "code_cols": 41}, 2),   # NSUB mismatch
+    ({"code_type": 5, "code_cols": 10}, 2),           # u32 words: WPR(40, 11) = 22
+    ({"group": 48}, 2),                               # 48 does not divide 160
+    ({"row_table": 16, "n_live": 4}, 1),              # no skipzero tables for embeddings
+    ({"k_expect": 4096}, 3),                          # sharded codebook
+])
+def test_embed_validation_refuses_before_launch(L, kw, rc):
+    w = _emb(L, **kw)
+    got = L.lib().vqk_embed_gather(ctypes.byref(w), ctypes.c_void_p(16), L.VQK_I64, 3,
+                                   ctypes.c_void_p(16), L.VQK_BF16, None)
+    assert got == rc, L.last_error()
+    assert L.last_error()
+
+
+def test_embed_argument_errors(L):
+    w = _emb(L)
+    lib = L.lib()
+    for id_type, out_type, n in ((L.VQK_F32, L.VQK_BF16, 3), (L.VQK_I32, L.VQK_U8, 3),
+                                 (L.VQK_I32, L.VQK_BF16, -1)):
+        assert lib.vqk_embed_gather(ctypes.byref(w), ctypes.c_void_p(16), id_type, n,
+                                    ctypes.c_void_p(16), out_type, None) == L.VQK_EINVAL
+    # nothing to gather: valid and no launch
+    assert lib.vqk_embed_gather(ctypes.byref(w), None, L.VQK_I32, 0, None, L.VQK_F16,
+                                None) == L.VQK_OK

@@ -362,3 +362,61 @@ def test_sort_routing_inverse():
     assert np.array_equal(flat[order], srt) and np.all(np.diff(srt) >= 0)
     assert np.array_equal(srt[inv], flat)
     assert np.array_equal(src, order // 4)
+
+
+# ------------------------------------------------------------- embeddings
+def _stream_pack(codes, bits):
+    """Codes -> PLE byte-stream rows by an independent route: the LSB-first
+    bit matrix of every code laid end to end, then numpy's packbits."""
+    codes = np.asarray(codes, np.uint32)
+    lead, nsub = codes.shape[:-1], codes.shape[-1]
+    bitmat = ((codes[..., None] >> np.arange(bits, dtype=np.uint32)) & 1).astype(np.uint8)
+    flat = bitmat.reshape(lead + (nsub * bits,))
+    return np.packbits(flat, axis=-1, bitorder="little")
+
+
+@pytest.mark.parametrize("bits", list(range(1, 17)))
+def test_ple_unpack_vs_bitserial(bits):
+    rng = np.random.default_rng(700 + bits)
+    for nsub in (1, 7, 40, 64):
+        codes = rng.integers(0, 1 << bits, (3, nsub)).astype(np.uint32)
+        rows = _stream_pack(codes, bits)
+        assert rows.shape[-1] == (nsub * bits + 7) // 8
+        assert np.array_equal(vo.ple_unpack(rows, nsub, bits), codes)
+        # bit-serial read of the same bytes
+        allbits = np.unpackbits(rows, axis=-1, bitorder="little").astype(np.uint32)
+        ser = np.zeros_like(codes)
+        for j in range(nsub):
+            for k in range(bits):
+                ser[:, j] |= allbits[:, j * bits + k] << np.uint32(k)
+        assert np.array_equal(ser, codes)
+
+
+def test_ple_unpack_width8_is_identity():
+    rng = np.random.default_rng(8)
+    rows = rng.integers(0, 256, (5, 40)).astype(np.uint8)
+    assert np.array_equal(vo.ple_unpack(rows, 40, 8), rows)
+
+
+def test_f16_to_bf16_matches_torch_rounding():
+    torch = pytest.importorskip("torch")
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    got = vo.f16_to_bf16(h)
+    ref = torch.from_numpy(h.astype(np.float32)).to(torch.bfloat16).view(torch.int16).numpy()
+    ref = ref.view(np.uint16)
+    nan = np.isnan(h)
+    assert np.array_equal(got[~nan], ref[~nan])
+    # NaN stays NaN: exponent all ones, nonzero mantissa
+    assert np.all((got[nan] & 0x7F80) == 0x7F80) and np.all((got[nan] & 0x7F) != 0)
+
+
+def test_embed_rows_is_gather_of_full_dequant():
+    rng = np.random.default_rng(9)
+    codes = rng.integers(0, 256, (50, 16)).astype(np.uint8)
+    cb = (rng.standard_normal((256, 4)) * 0.05).astype(np.float16)
+    sc = (rng.random((50, 2)) + 0.5).astype(np.float16)
+    ids = rng.integers(0, 50, (3, 4))
+    full = vo.dequant(codes, cb, sc, 32)
+    got = vo.embed_rows(ids, codes, cb, sc, 32)
+    assert got.shape == (3, 4, 64)
+    assert np.array_equal(got.view(np.uint16), full[ids].view(np.uint16))

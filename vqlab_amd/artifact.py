@@ -1,0 +1,292 @@
+"""VQLab artifact loader: config.json + safetensors shards -> this package's
+VQ modules on a ROCm device.
+
+The reference attaches its VQ modules while the bundle's model.py builds the
+model -- `vq_modules` (VQSwitchLinear, skipzero included) and `vq_ple`
+(VQPLEEmbedding) in bundle/add_model_file.py:70-150, `vq_linear` (VQLinear)
+and `vq_embed` (VQEmbedding) in runtime/dense_shim.py:53-83 -- with
+zero-filled placeholders whose shapes a strict load then checks, and it
+converts skipzero tensors on the way in (skipzero_weights,
+vq_switch.py:4988-5013). Here the same config sections and tensor names
+build the modules directly: each module's tensors are read from its shard,
+checked against the shapes and dtypes the config implies (ValueError naming
+the key otherwise, as a strict load would), moved to the device one module
+at a time, and wrapped in VQSwitchLinear / VQLinear / VQEmbedding /
+VQPLEEmbedding. Tensors that belong to no VQ module are listed, not loaded.
+
+    art = load_artifact("/path/to/artifact", device="cuda")
+    art.modules["model.language_model.layers.0.mlp.switch_mlp.gate_proj"]
+    art.attach(model)          # install every module into a torch model tree
+"""
+from __future__ import annotations
+
+import dataclasses
+import json
+import pathlib
+import re
+
+import torch
+
+from . import vq_pack
+from .vq_dense import VQEmbedding, VQLinear
+from .vq_switch import VQPLEEmbedding, VQSwitchLinear, skipzero_row_table
+
+_DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}
+
+
+def read_config(path) -> dict:
+    return json.loads((pathlib.Path(path) / "config.json").read_text())
+
+
+def shard_map(path) -> dict:
+    """tensor key -> shard file: model.safetensors.index.json's weight_map,
+    else the keys of every *.safetensors file in the directory."""
+    from safetensors import safe_open
+    root = pathlib.Path(path)
+    idx = root / "model.safetensors.index.json"
+    if idx.exists():
+        wm = json.loads(idx.read_text())["weight_map"]
+        return {k: root / v for k, v in wm.items()}
+    out = {}
+    for f in sorted(root.glob("*.safetensors")):
+        with safe_open(str(f), framework="pt") as sf:
+            for k in sf.keys():
+                out[k] = f
+    return out
+
+
+def _model_dtype(cfg) -> torch.dtype:
+    """The artifact's activation dtype (dense_shim.py:40-44)."""
+    name = (cfg.get("dtype") or cfg.get("torch_dtype")
+            or cfg.get("text_config", {}).get("dtype") or "bfloat16")
+    return _DTYPES[name]
+
+
+def module_specs(cfg) -> list:
+    """[(config path, kind, spec)] for every VQ module the config declares:
+    kind 'switch' (vq_modules), 'linear' (vq_linear), 'embed' (vq_embed),
+    'ple' (vq_ple keys, spec = geometry + that key's [rows, cols])."""
+    out = [(p, "switch", m) for p, m in cfg.get("vq_modules", {}).items()]
+    out += [(p, "linear", m) for p, m in cfg.get("vq_linear", {}).items()]
+    out += [(p, "embed", m) for p, m in cfg.get("vq_embed", {}).items()]
+    ple = cfg.get("vq_ple") or {}
+    for key in ple.get("keys", []):
+        rows, cols = ple["shapes"][key]
+        out.append((key, "ple", dict(ple["geometry"], rows=int(rows), cols=int(cols))))
+    return out
+
+
+def _strip(p: str) -> str:
+    """A module path without the layout prefixes the two module trees differ
+    by (`language_model.`, a leading `model.`), so the mlx_lm and mlx_vlm
+    spellings of one module compare equal (arch_resolve.py:186-240)."""
+    p = re.sub(r"\.ngram_embedding\.shard_(\d+)$", r".ngram_embedding.shards.\1", p)
+    p = p.replace("language_model.", "")
+    while p.startswith("model."):
+        p = p[len("model."):]
+    return p
+
+
+def _tensor_prefix(path: str, keys) -> str:
+    """The weight-key prefix of the module at config path `path`: the path
+    itself, else the unique module prefix that is the same module in the
+    other layout's spelling."""
+    if path + ".codebook" in keys:
+        return path
+    want = _strip(path)
+    hits = sorted({k[: -len(".codebook")] for k in keys
+                   if k.endswith(".codebook") and _strip(k[: -len(".codebook")]) == want})
+    if len(hits) != 1:
+        raise KeyError(f"no tensors for VQ module {path!r}" if not hits else
+                       f"VQ module {path!r} matches several tensor prefixes: {hits}")
+    return hits[0]
+
+
+def _expect(key, t, shape, dtypes):
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{key}: expected shape {tuple(shape)}, the artifact holds "
+                         f"{tuple(t.shape)}")
+    if t.dtype not in dtypes:
+        raise ValueError(f"{key}: expected dtype {dtypes[0]}, the artifact holds {t.dtype}")
+
+
+def _code_layout(spec):
+    """(columns, accepted dtypes, pack_bits) of a module's code rows."""
+    nsub = int(spec["in"]) // int(spec["dim"])
+    pb = int(spec.get("pack_bits", 0) or 0)
+    if pb:
+        return vq_pack.words_per_row(nsub, pb), (torch.uint32, torch.int32), pb
+    if int(spec["k"]) <= 256:
+        return nsub, (torch.uint8,), 0
+    return nsub, (torch.uint16, torch.int16), 0
+
+
+def _as_kernel_codes(t):
+    # bit-identical signed views: the kernels read the words / halves as stored
+    if t.dtype == torch.uint32:
+        return t.view(torch.int32)
+    if t.dtype == torch.uint16:
+        return t.view(torch.int16)
+    return t
+
+
+class _Reader:
+    """Reads single tensors from the shards, keeping each shard open."""
+
+    def __init__(self, smap):
+        self.smap = smap
+        self._open = {}
+
+    def __contains__(self, key):
+        return key in self.smap
+
+    def get(self, key):
+        from safetensors import safe_open
+        f = self.smap[key]
+        if f not in self._open:
+            self._open[f] = safe_open(str(f), framework="pt")
+        return self._open[f].get_tensor(key)
+
+    def close(self):
+        self._open.clear()
+
+
+def _build(path, kind, spec, rd, sz_mods, device, out_dtype):
+    q = _tensor_prefix(path, rd.smap)
+    g = int(spec["group"])
+    k, d = int(spec["k"]), int(spec["dim"])
+    cb = rd.get(q + ".codebook")
+    _expect(q + ".codebook", cb, (k, d), (torch.float16,))
+    cb = cb.to(device)
+    if kind == "ple":
+        rows, cols = spec["rows"], spec["cols"]
+        rb = spec.get("row_bytes")
+        codes = rd.get(q + ".codes")
+        if rb:
+            _expect(q + ".codes", codes, (rows, int(rb)), (torch.uint8,))
+        else:
+            _expect(q + ".codes", codes, (rows, cols // d), (torch.uint16, torch.int16))
+        sc = rd.get(q + ".vq_scales")
+        _expect(q + ".vq_scales", sc, (rows, cols // g), (torch.float16,))
+        return VQPLEEmbedding(_as_kernel_codes(codes).to(device), cb, sc.to(device),
+                              group_size=g, packed_nsub=(cols // d) if rb else 0)
+
+    IN = int(spec["in"])
+    cols, cdt, pb = _code_layout(spec)
+    infeat = IN if pb else None
+    if kind == "switch" and q + ".sz_rowmask" in rd:
+        # skipzero: compact live rows + [E, OUT] row table (vq_switch.py:4988-5013)
+        E, OUT = int(spec["experts"]), int(spec["out"])
+        szm = sz_mods.get(path, {})
+        E, OUT = int(szm.get("experts", E)), int(szm.get("out", OUT))
+        mask = rd.get(q + ".sz_rowmask")
+        _expect(q + ".sz_rowmask", mask, (E, (OUT + 7) // 8), (torch.uint8,))
+        if q + ".sz_shape" in rd:
+            shp = [int(v) for v in rd.get(q + ".sz_shape").tolist()]
+            if shp[:2] != [E, OUT]:
+                raise ValueError(f"{q}.sz_shape {shp} disagrees with the config's "
+                                 f"(experts, out) = ({E}, {OUT})")
+        table = skipzero_row_table(mask, E, OUT)
+        n_live = int((table >= 0).sum())
+        codes, sc = rd.get(q + ".sz_codes"), rd.get(q + ".sz_scales")
+        _expect(q + ".sz_codes", codes, (n_live, cols), cdt)
+        _expect(q + ".sz_scales", sc, (n_live, IN // g), (torch.float16,))
+        return VQSwitchLinear(_as_kernel_codes(codes).to(device), cb, sc.to(device),
+                              group_size=g, pack_bits=pb, in_features=infeat,
+                              row_table=table.to(device))
+    codes, sc = rd.get(q + ".codes"), rd.get(q + ".vq_scales")
+    if kind == "switch":
+        E, OUT = int(spec["experts"]), int(spec["out"])
+        _expect(q + ".codes", codes, (E, OUT, cols), cdt)
+        _expect(q + ".vq_scales", sc, (E, OUT, IN // g), (torch.float16,))
+        return VQSwitchLinear(_as_kernel_codes(codes).to(device), cb, sc.to(device),
+                              group_size=g, pack_bits=pb, in_features=infeat)
+    rows = int(spec["rows"] if kind == "embed" else spec["out"])
+    _expect(q + ".codes", codes, (rows, cols), cdt)
+    _expect(q + ".vq_scales", sc, (rows, IN // g), (torch.float16,))
+    if kind == "linear":
+        return VQLinear(_as_kernel_codes(codes).to(device), cb, sc.to(device), group_size=g,
+                        pack_bits=pb, in_features=infeat)
+    return VQEmbedding(_as_kernel_codes(codes).to(device), cb, sc.to(device), group_size=g,
+                       pack_bits=pb, in_features=infeat, out_dtype=out_dtype)
+
+
+def _candidates(path: str) -> list:
+    """Spellings of a module path in the two module trees (arch_resolve.py:186-240):
+    as written, with a leading `language_model.` added or removed, and -- for
+    weight-key spellings such as `model.language_model.layers.N` -- with the
+    inner `language_model.` level dropped."""
+    c = [path]
+    c.append(path[len("language_model."):] if path.startswith("language_model.")
+             else "language_model." + path)
+    flat = path.replace("language_model.", "")
+    if flat not in c:
+        c.append(flat)
+    for p in list(c):
+        m = re.search(r"\.ngram_embedding\.shard_(\d+)$", p)
+        if m:
+            c.append(p[: m.start()] + f".ngram_embedding.shards.{m.group(1)}")
+    return c
+
+
+def attach(root: torch.nn.Module, path: str, module: torch.nn.Module) -> None:
+    """Install `module` at `path` of a torch module tree, trying the path as
+    written, then with `language_model.` added or removed, then the PLE
+    `shard_N` -> `shards.N` spelling; raises naming every candidate when none
+    resolves (a module that silently fails to attach leaves a random dense
+    layer in the model)."""
+    cands = _candidates(path)
+    for cand in cands:
+        obj, parts, ok = root, cand.split("."), True
+        for c in parts[:-1]:
+            try:
+                obj = obj[int(c)] if c.isdigit() else getattr(obj, c)
+            except (AttributeError, IndexError, KeyError, TypeError):
+                ok = False
+                break
+        leaf = parts[-1]
+        if not ok:
+            continue
+        if leaf.isdigit() and isinstance(obj, (list, torch.nn.ModuleList)) and int(leaf) < len(obj):
+            obj[int(leaf)] = module
+            return
+        if hasattr(obj, leaf):
+            setattr(obj, leaf, module)
+            return
+    raise AttributeError(f"VQ module {path!r} does not resolve on {type(root).__name__}; "
+                         f"tried {cands}")
+
+
+@dataclasses.dataclass
+class Artifact:
+    path: pathlib.Path
+    config: dict
+    modules: dict            # config path -> VQ module (device tensors)
+    other_keys: list         # tensors that belong to no VQ module (not loaded)
+
+    def attach(self, model: torch.nn.Module) -> None:
+        for p, m in self.modules.items():
+            attach(model, p, m)
+
+
+def load_artifact(path, device="cuda", only=None) -> Artifact:
+    """Builds every VQ module `path`'s config.json declares (or those whose
+    config path is in `only`), reading each module's tensors from its shard
+    and moving them to `device` one module at a time."""
+    root = pathlib.Path(path)
+    cfg = read_config(root)
+    rd = _Reader(shard_map(root))
+    sz_mods = (cfg.get("vq_skipzero") or {}).get("modules") or {}
+    out_dtype = _model_dtype(cfg)
+    mods, used = {}, set()
+    try:
+        for p, kind, spec in module_specs(cfg):
+            if only is not None and p not in only:
+                continue
+            mods[p] = _build(p, kind, spec, rd, sz_mods, device, out_dtype)
+            q = _tensor_prefix(p, rd.smap)
+            used.update(k for k in rd.smap if k.startswith(q + "."))
+    finally:
+        rd.close()
+    other = sorted(k for k in rd.smap if k not in used)
+    return Artifact(root, cfg, mods, other)

@@ -8,9 +8,11 @@
                                                      vq_dense.py:262-312
   VQEmbedding(codes, codebook, vq_scales, ...)       vq_dense.py:444-513
 
-Small N runs the fused GEMV (vqk_dense_gemv). Large N runs the tiled
-dequant-into-LDS matrix-core GEMM (vqk_dense_gemm), which never materialises
-the fp16 weight.
+Small N runs the fused GEMV (vqk_dense_gemv). Large N runs vqk_dense_gemm:
+up to 64 rows W is decoded straight into matrix-core operands; above, the
+weight is dequantised bit-exactly into a workspace panel and multiplied by an
+LDS-tiled fp16 matrix-core GEMM. VQEmbedding decodes only the gathered rows
+(vqk_embed_gather), in one launch.
 """
 from __future__ import annotations
 
@@ -102,9 +104,30 @@ class VQLinear(torch.nn.Module):
         return y.reshape(*lead, OUT)
 
 
+def embed_gather(w, keep, ids, out_dtype):
+    """rows ids of the table `w` (a vqk_weights with E == 1), decoded and
+    converted to out_dtype in one launch: [*ids.shape, IN]."""
+    dev = T.require_cuda(ids, *[t for t in keep if t is not None])
+    if out_dtype not in T.ACT_TYPES:
+        raise ValueError(f"out_dtype must be float16, bfloat16 or float32, got {out_dtype}")
+    flat = ids.reshape(-1)
+    if flat.dtype not in (torch.int32, torch.int64):
+        flat = flat.to(torch.int64)
+    flat = flat.contiguous()
+    out = torch.empty((flat.numel(), int(w.IN)), dtype=out_dtype, device=dev)
+    L.check(L.lib().vqk_embed_gather(ctypes.byref(w), T.ptr(flat),
+                                     L.VQK_I64 if flat.dtype == torch.int64 else L.VQK_I32,
+                                     flat.numel(), T.ptr(out), T.ACT_TYPES[out_dtype],
+                                     T.stream(dev)),
+            "embedding gather")
+    return out.reshape(*ids.shape, int(w.IN))
+
+
 class VQEmbedding(torch.nn.Module):
     """Drop-in for nn.Embedding whose table is VQ-coded (vq_dense.py:444-513):
-    decodes only the gathered rows, bit-exact, and returns out_dtype."""
+    decodes only the gathered rows, bit-exactly, and returns out_dtype.
+    codes [rows, NSUB] uint8/uint16 or [rows, WPR] uint32 words of
+    pack_bits-wide fields; vq_scales [rows, IN / group_size] fp16."""
 
     def __init__(self, codes, codebook, vq_scales, group_size=64, pack_bits=0,
                  in_features=None, out_dtype=torch.bfloat16):
@@ -130,14 +153,24 @@ class VQEmbedding(torch.nn.Module):
             return int(self._in_features)
         return int(self.codes.shape[1]) * int(self.codebook.shape[1])
 
+    def _desc(self, keep):
+        return T.weights(self.codes, self.codebook, self.vq_scales, self.group_size,
+                         self.pack_bits, self._in_features, k_expect=self._k_expect,
+                         keep=keep)
+
     def forward(self, ids):
-        if int(self.codebook.shape[0]) != self._k_expect:
-            raise RuntimeError("VQ codebook was sharded; must be replicated.")
-        flat = ids.reshape(-1)
-        IN = self.dims
-        # gather the touched rows on device, then decode just those rows
-        rows = self.codes.index_select(0, flat)
-        sc = self.vq_scales.index_select(0, flat)
-        w = VS.wdec_decode(rows, self.codebook, sc, flat.numel(), IN, self.group_size,
-                           self.pack_bits)
-        return w.reshape(*ids.shape, IN).to(self.out_dtype)
+        # a codebook whose K changed was sliced (vq_dense.py:491-494): the
+        # library refuses it (VQK_ESHARDED -> RuntimeError) before any launch
+        keep = []
+        w = self._desc(keep)
+        return embed_gather(w, keep, ids, self.out_dtype)
+
+    def as_linear(self, x):
+        """x @ W.T over the whole decoded table (vq_dense.py:508-513), for a
+        tied output head: the dense large-N path of VQLinear."""
+        OUT, IN = self.num_embeddings, self.dims
+        lead = x.shape[:-1]
+        xf = x.reshape(-1, IN)
+        y = _decode_matmul(xf, self.codes, self.codebook, self.vq_scales, self.group_size,
+                           OUT, IN, self.pack_bits)
+        return y.reshape(*lead, OUT)

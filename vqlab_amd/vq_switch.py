@@ -12,6 +12,8 @@ Module-level functions keep the reference's names and argument meaning:
                                                         vq_switch.py:4725-4782
   dense_fits / wdec_fits / gemmseg_fits                 3290 / 3505 / 4469
   skipzero_row_table / skipzero_weights                 4958-5013
+  VQPLEEmbedding(codes, codebook, vq_scales, group_size, packed_nsub)
+                                                        vq_switch.py:5426-5495
 Tensors are torch tensors on a ROCm device; every call launches on the
 current stream and never synchronises with the host.
 """
@@ -277,3 +279,48 @@ class VQSwitchLinear(torch.nn.Module):
             y = _gemmseg(x2, eidx, self.codes, self.codebook, self.vq_scales, self.pack_bits,
                          IN, rep, self.row_table, out_dtype=out_dtype)
         return y.reshape(*indices.shape, 1, OUT)
+
+
+class VQPLEEmbedding(torch.nn.Module):
+    """VQ-coded embedding / per-layer-embedding (PLE) table shard whose
+    decode is a pure gather (vq_switch.py:5426-5495):
+      codes      uint16 [rows, cols / dim] unpacked, or, with packed_nsub,
+                 uint8 [rows, row_bytes]: packed_nsub codes of
+                 BITS = max(1, bit_length(K - 1)) bits back to back, code j at
+                 bits [j*BITS, (j+1)*BITS) of the row, LSB first
+      codebook   fp16 [K, dim]
+      vq_scales  fp16 [rows, cols / group_size]
+    __call__(ids) -> [*ids.shape, cols] bfloat16: codebook[codes[ids]] times
+    the row's group scales, rounded to fp16 and then to bf16, decoded in one
+    launch of vqk_embed_gather. At BITS == 8 the byte stream is the codes
+    themselves (vq_switch.py:5456-5467) and is read as plain uint8 codes."""
+
+    def __init__(self, codes, codebook, vq_scales, group_size: int = 32,
+                 packed_nsub: int = 0):
+        super().__init__()
+        self.codes = codes
+        self.codebook = codebook
+        self.vq_scales = vq_scales
+        self.group_size = group_size
+        self._pn = int(packed_nsub)
+        self._bits = max(1, (int(codebook.shape[0]) - 1).bit_length())
+        self._byte_codes = bool(packed_nsub) and self._bits == 8
+
+    def _desc(self, keep):
+        d = int(self.codebook.shape[1])
+        if self._pn and not self._byte_codes:
+            if self.codes.dtype != torch.uint8:
+                raise ValueError(f"packed PLE rows must be uint8 bytes, got {self.codes.dtype}")
+            w = T.weights(self.codes, self.codebook, self.vq_scales, self.group_size,
+                          pack_bits=self._bits, in_features=self._pn * d, keep=keep)
+            return w
+        if self._pn and int(self.codes.shape[-1]) != self._pn:
+            raise ValueError(f"byte-coded PLE rows are {self.codes.shape[-1]} bytes, "
+                             f"expected {self._pn} codes")
+        return T.weights(self.codes, self.codebook, self.vq_scales, self.group_size, keep=keep)
+
+    def forward(self, ids):
+        from .vq_dense import embed_gather
+        keep = []
+        w = self._desc(keep)
+        return embed_gather(w, keep, ids, torch.bfloat16)
