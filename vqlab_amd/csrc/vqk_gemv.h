@@ -205,17 +205,17 @@ __device__ __forceinline__ void stage_codebook(const uint16_t *cb, int K, int en
     lds_copy_async(cb, dst, K * D * 2, entries * D * 2);
 }
 
-// Same for a table of compile-time size CBN entries staged by NT threads:
-// every thread issues exactly CBN*D*2 / (16 * NT) direct-to-LDS loads
-// (predicated off past K), so the compiler's vmcnt waits on loads issued
-// before the copy stay exact instead of draining the whole copy.
-template <int D, int CBN, int NT>
+// Same for a table of compile-time size CBN entries staged by the NT threads
+// of waves W0 .. W0 + NT/64 - 1: every one of them issues at most
+// ceil(CBN*D*2 / (16 * NT)) direct-to-LDS loads (predicated off past K), and
+// no global load sits in a loop.
+template <int D, int CBN, int NT, int W0 = 0>
 __device__ __forceinline__ void stage_codebook_fixed(const uint16_t *cb, int K, h2 *dst) {
     constexpr int PIECES = CBN * D * 2 / 16;                 // 16-byte pieces of the table
     constexpr int ROUNDS = (PIECES + NT - 1) / NT;
     const uint8_t *s = reinterpret_cast<const uint8_t *>(cb);
     uint8_t *d = reinterpret_cast<uint8_t *>(dst);
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & (kWave - 1), wave = int(threadIdx.x >> 6) - W0;
     const int valid = (K * D * 2) >> 4;                      // whole valid pieces
 #pragma unroll
     for (int r = 0; r < ROUNDS; ++r) {
@@ -224,10 +224,16 @@ __device__ __forceinline__ void stage_codebook_fixed(const uint16_t *cb, int K, 
             __builtin_amdgcn_global_load_lds((global_void *)(s + int64_t(c + lane) * 16),
                                              (lds_void *)(d + int64_t(c) * 16), 16, 0, 0);
     }
-    // the sub-16-byte tail of the valid bytes, then zeros up to the table end
-    for (int i = valid * 4 + threadIdx.x; i < PIECES * 4; i += NT)
-        reinterpret_cast<uint32_t *>(d)[i] =
-            i < (K * D * 2) / 4 ? reinterpret_cast<const uint32_t *>(s)[i] : 0u;
+    if (valid == PIECES) return;                             // the whole table came over
+    // the sub-16-byte tail of the valid bytes (at most 3 words, one load per
+    // thread), then zeros up to the table end
+    const int tail_words = ((K * D * 2) >> 2) - valid * 4;
+    const int tid = int(threadIdx.x) - W0 * kWave;
+    if (tid < tail_words)
+        reinterpret_cast<uint32_t *>(d)[valid * 4 + tid] =
+            reinterpret_cast<const uint32_t *>(s)[valid * 4 + tid];
+    for (int i = valid * 4 + tail_words + tid; i < PIECES * 4; i += NT)
+        reinterpret_cast<uint32_t *>(d)[i] = 0u;
 }
 
 // Wait for every outstanding vector-memory operation of this wave (the
@@ -271,25 +277,29 @@ __device__ __forceinline__ u32x4 load8_act(const void *x, int32_t type, int64_t 
 // One activation row -> fp16 in LDS, blocks of XH values at a padded stride
 // XS (halves). Vector path: every thread issues all its 16-byte loads before
 // converting any, so the row costs one memory latency.
+// `tid0` / `nthr`: the staging threads' first index and count (default: the
+// whole workgroup).
 template <int XH, int XS>
 __device__ __forceinline__ void stage_x(const void *x, int32_t type, int64_t base, int IN, int NB,
-                                        f16 *xs) {
+                                        f16 *xs, int tid0 = -1, int nthr = 0) {
+    const int me = tid0 < 0 ? int(threadIdx.x) : int(threadIdx.x) - tid0;
+    const int nt = tid0 < 0 ? int(blockDim.x) : nthr;
     const int esz = type == VQK_F32 ? 4 : 2;
     const bool vec = ((reinterpret_cast<uintptr_t>(x) + uint64_t(base) * esz) & 15) == 0 &&
                      (IN & 7) == 0;
     if (vec) {
         constexpr int U = 4;
         const int ng = NB * XH / 8;                      // 8-value groups incl. zero tail
-        for (int g0 = threadIdx.x; g0 < ng; g0 += U * blockDim.x) {
+        for (int g0 = me; g0 < ng; g0 += U * nt) {
             u32x4 v[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int g = g0 + u * blockDim.x;
+                const int g = g0 + u * nt;
                 v[u] = (g < ng && g * 8 < IN) ? load8_act(x, type, base + g * 8) : u32x4{0, 0, 0, 0};
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int g = g0 + u * blockDim.x;
+                const int g = g0 + u * nt;
                 if (g < ng) {
                     const int i = g * 8;
                     *reinterpret_cast<u32x4 *>(xs + (i / XH) * XS + (i % XH)) = v[u];
@@ -298,7 +308,7 @@ __device__ __forceinline__ void stage_x(const void *x, int32_t type, int64_t bas
         }
         return;
     }
-    for (int i = threadIdx.x; i < NB * XH; i += blockDim.x) {
+    for (int i = me; i < NB * XH; i += nt) {
         const float v = i < IN ? load_act(x, type, base + i) : 0.f;
         xs[(i / XH) * XS + (i % XH)] = f16(v);
     }

@@ -72,8 +72,7 @@ struct MoeParams {
 // while k <= number of finite logits.
 template <int NS>
 __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int norm, int want,
-                                           int *e_want, int *my_idx, float *my_w,
-                                           void (*issue)(void *), void *ctx) {
+                                           int *e_want, int *my_idx, float *my_w) {
     const int lane = threadIdx.x & (kWave - 1);
     uint32_t key[NS];
     float raw[NS];
@@ -82,7 +81,7 @@ __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int no
         const int i = s * kWave + lane;
         raw[s] = i < E ? lg[i] : 0.f;
     }
-    issue(ctx);                                          // independent loads go out behind the logits
+    wait_vmem();                                         // the logits are this wave's only loads
 #pragma unroll
     for (int s = 0; s < NS; ++s) key[s] = (s * kWave + lane) < E ? f32_key(raw[s]) : 0u;
     uint32_t lmax = 0;
@@ -133,30 +132,13 @@ __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int no
 }
 
 __device__ __forceinline__ void route(const float *lg, int E, int k, int norm, int want,
-                                      int *e_want, int *my_idx, float *my_w,
-                                      void (*issue)(void *), void *ctx) {
+                                      int *e_want, int *my_idx, float *my_w) {
     const int ns = (E + kWave - 1) / kWave;              // wave-uniform
-    if (ns <= 1) route_wave<1>(lg, E, k, norm, want, e_want, my_idx, my_w, issue, ctx);
-    else if (ns <= 2) route_wave<2>(lg, E, k, norm, want, e_want, my_idx, my_w, issue, ctx);
-    else if (ns <= 4) route_wave<4>(lg, E, k, norm, want, e_want, my_idx, my_w, issue, ctx);
-    else if (ns <= 8) route_wave<8>(lg, E, k, norm, want, e_want, my_idx, my_w, issue, ctx);
-    else route_wave<16>(lg, E, k, norm, want, e_want, my_idx, my_w, issue, ctx);
-}
-
-template <int D, int CBN>
-struct CbPair {            // the two codebook copies K1 queues behind its logits
-    const uint16_t *a, *b;
-    int ka, kb;
-    h2 *da, *db;
-};
-
-template <int D, int CBN>
-__device__ void issue_cb_pair(void *ctx) {
-    if constexpr (CBN > 0) {
-        const CbPair<D, CBN> *c = static_cast<const CbPair<D, CBN> *>(ctx);
-        stage_codebook_fixed<D, CBN, kThreads>(c->a, c->ka, c->da);
-        stage_codebook_fixed<D, CBN, kThreads>(c->b, c->kb, c->db);
-    }
+    if (ns <= 1) route_wave<1>(lg, E, k, norm, want, e_want, my_idx, my_w);
+    else if (ns <= 2) route_wave<2>(lg, E, k, norm, want, e_want, my_idx, my_w);
+    else if (ns <= 4) route_wave<4>(lg, E, k, norm, want, e_want, my_idx, my_w);
+    else if (ns <= 8) route_wave<8>(lg, E, k, norm, want, e_want, my_idx, my_w);
+    else route_wave<16>(lg, E, k, norm, want, e_want, my_idx, my_w);
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.f + __expf(-g)); }
@@ -243,17 +225,17 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
     const MoeW &wu = is_shared ? p.sup : p.up;
     const float *lg = p.logits + int64_t(t) * p.E;
 
-    // Wave 0 loads the logits first and routes; every wave meanwhile streams
-    // the two codebooks and x into LDS. One barrier publishes the expert id,
-    // then all waves issue their weight loads (nothing else is outstanding,
-    // so the barrier's wait never drains weight loads).
-    CbPair<D, CBN> cbp{wg.codebook, wu.codebook, wg.K, wu.K, cbg_lds, cbu_lds};
+    // Wave 0 loads the logits and routes, with no other load in flight (a
+    // wave's loads complete in order, so anything queued ahead of the logits
+    // would delay the routing); waves 1-3 meanwhile stream the two codebooks
+    // and x into LDS. One barrier publishes the expert id, then all waves
+    // issue their weight loads (nothing else is outstanding, so the
+    // barrier's wait never drains weight loads).
     int my_idx = -1;
     float my_w = 0.f;
     if (wave == 0) {
         int e_pair;
-        route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &e_pair, &my_idx, &my_w,
-              &issue_cb_pair<D, CBN>, &cbp);
+        route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &e_pair, &my_idx, &my_w);
         if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
         if (lane == 0) rl.route = e_pair;
         if (lane < p.top_k) {
@@ -261,9 +243,11 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
             rl.wts[lane] = my_w;
         }
     } else {
-        issue_cb_pair<D, CBN>(&cbp);
+        constexpr int NT = kThreads - kWave;
+        stage_codebook_fixed<D, CBN, NT, 1>(wg.codebook, wg.K, cbg_lds);
+        stage_codebook_fixed<D, CBN, NT, 1>(wu.codebook, wu.K, cbu_lds);
+        stage_x<XH, XS>(p.x, p.x_type, int64_t(t) * p.H, p.H, p.NB1, xs, kWave, NT);
     }
-    stage_x<XH, XS>(p.x, p.x_type, int64_t(t) * p.H, p.H, p.NB1, xs);
     // routing / shared-gate outputs, once per token
     if (bx == 0 && j == 0 && wave == 0) {
         if (lane < p.top_k) {
@@ -489,12 +473,21 @@ __global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
     constexpr int CBN = down_cbn<D, BITS>();
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = int(blockIdx.y);
-    down_stage_cb<D, CBN, cb_in_lds(D, BITS)>(p, smem);   // independent of the routing: first
     const DownLane dl(p);
+    // The routing is read first: the weight addresses wait on it, and a
+    // wave's vector-memory loads complete in issue order, so it must not
+    // queue behind the table copy (which only the decode needs).
+    int id = -1;
+    float wt = 0.f;
+    if (dl.on && !dl.is_shared) {
+        id = p.ids[t * p.top_k + dl.j];
+        wt = p.wts[t * p.top_k + dl.j];
+    }
+    wait_vmem();
     DownState<BITS, GPB> ds;
-    down_prep<BITS, GPB>(p, int(blockIdx.x), t, dl,
-                         [&](int j) { return p.ids[t * p.top_k + j]; },
-                         [&](int j) { return p.wts[t * p.top_k + j]; }, ds);
+    down_prep<BITS, GPB>(p, int(blockIdx.x), t, dl, [&](int) { return id; },
+                         [&](int) { return wt; }, ds);
+    down_stage_cb<D, CBN, cb_in_lds(D, BITS)>(p, smem);
     down_run<D, BITS, GPB>(p, int(blockIdx.x), t, smem, dl, ds);
 }
 
@@ -508,9 +501,7 @@ __global__ void __launch_bounds__(kWave) k_route_tokens(const MoeParams p) {
     const int t = int(blockIdx.x), lane = int(threadIdx.x);
     int e_pair, my_idx = -1;
     float my_w = 0.f;
-    CbPair<2, 0> none{};
-    route(p.logits + int64_t(t) * p.E, p.E, p.top_k, p.norm, -1, &e_pair, &my_idx, &my_w,
-          &issue_cb_pair<2, 0>, &none);
+    route(p.logits + int64_t(t) * p.E, p.E, p.top_k, p.norm, -1, &e_pair, &my_idx, &my_w);
     if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
     if (lane < p.top_k) {
         p.ids[t * p.top_k + lane] = my_idx;
