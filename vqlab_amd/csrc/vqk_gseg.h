@@ -120,10 +120,12 @@ __device__ __forceinline__ h8 step_entries_hyb(const uint32_t (&w)[BITS], int s,
     }
 }
 
-// LDS entries of a table too large for LDS that the kernel stages (what the
-// x double buffer leaves of the 160 KB).
+// LDS entries of a table too large for LDS that the kernel stages: what the
+// x chunk (kSegTok x (128 D + 8) halves) leaves of the 160 KB -- 124 KB of a
+// d8 table (7936 of K16384's entries), all of a d4 K16384 table, 144 KB of a
+// d2 one.
 __host__ __device__ constexpr int seg_hyb_entries(int D) {
-    return (D == 8 ? 88 * 1024 : (D == 4 ? 120 * 1024 : 128 * 1024)) / (2 * D);
+    return (D == 8 ? 124 * 1024 : (D == 4 ? 128 * 1024 : 144 * 1024)) / (2 * D);
 }
 
 
@@ -138,10 +140,11 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     static_assert(PIECES % 256 == 0, "chunk must split evenly over 256 threads");
     // LDS table entries: the whole table, or the first seg_hyb_entries of it
     constexpr int CBN = CBL ? (1 << BITS) : seg_hyb_entries(D);
+    static_assert(kSegTok * XS * 2 + (CBN + 1) * D * 2 <= 160 * 1024, "LDS beyond 160 KB");
 
     extern __shared__ __align__(16) uint8_t smem[];
-    f16 *xs = reinterpret_cast<f16 *>(smem);    // [2][kSegTok][XS]
-    f16 *cbl = xs + 2 * kSegTok * XS;           // [CBN + 1][D]; entry CBN is zero
+    f16 *xs = reinterpret_cast<f16 *>(smem);    // [kSegTok][XS]
+    f16 *cbl = xs + kSegTok * XS;               // [CBN + 1][D]; entry CBN is zero
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ln = lane & 15, lg = lane >> 4;
@@ -202,11 +205,11 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
                                                 : u32x4{0, 0, 0, 0};
         }
     };
-    auto store_x = [&](int buf, const u32x4 (&v)[PPT]) {
+    auto store_x = [&](const u32x4 (&v)[PPT]) {
 #pragma unroll
         for (int r = 0; r < PPT; ++r) {
             const int pc = tid + 256 * r;
-            *reinterpret_cast<u32x4 *>(xs + (buf * kSegTok + pc / (CC / 8)) * XS + (pc % (CC / 8)) * 8) = v[r];
+            *reinterpret_cast<u32x4 *>(xs + (pc / (CC / 8)) * XS + (pc % (CC / 8)) * 8) = v[r];
         }
     };
     // words and scales of block 4*sb + lg of each row; lanes without one get
@@ -239,9 +242,9 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) acc[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](int buf, const uint32_t (&w)[TN][BITS], const h2 (&s)[TN][GPB],
+    auto compute = [&](const uint32_t (&w)[TN][BITS], const h2 (&s)[TN][GPB],
                        const bool (&live)[TN]) {
-        const f16 *xb = xs + (buf * kSegTok + ln) * XS + lg * (32 * D);
+        const f16 *xb = xs + ln * XS + lg * (32 * D);
         const f16 *tab[TN];
         uint32_t kl[TN];
 #pragma unroll
@@ -271,9 +274,13 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     bool l0[TN], l1[TN];
     u32x4 xr[PPT];
 
+    // One x chunk in LDS (the room a second one would take holds codebook
+    // entries instead): the next superstep's x and weights are loaded into
+    // registers before the current one multiplies, so their latency stays
+    // hidden; the chunk is overwritten between two barriers.
     load_x(0, xr);
     load_w(0, w0, s0, l0);
-    store_x(0, xr);
+    store_x(xr);
     wait_vmem();
     __syncthreads();
     for (int sb = 0; sb < NSS; sb += 2) {
@@ -282,17 +289,20 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
             load_x(sb + 1, xr);
             load_w(sb + 1, w1, s1, l1);
         }
-        compute(0, w0, s0, l0);
-        if (more1) store_x(1, xr);
-        __syncthreads();
+        compute(w0, s0, l0);
         if (!more1) break;
+        __syncthreads();                        // every wave is done with chunk sb
+        store_x(xr);
+        __syncthreads();                        // chunk sb + 1 is in place
         const bool more2 = sb + 2 < NSS;
         if (more2) {
             load_x(sb + 2, xr);
             load_w(sb + 2, w0, s0, l0);
         }
-        compute(1, w1, s1, l1);
-        if (more2) store_x(0, xr);
+        compute(w1, s1, l1);
+        if (!more2) break;
+        __syncthreads();
+        store_x(xr);
         __syncthreads();
     }
 
@@ -319,7 +329,7 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
 
 // LDS bytes of k_seg_mfma<D, BITS, ...>.
 __host__ __device__ constexpr size_t seg_lds(int D, int BITS, bool cbl) {
-    return size_t(2) * kSegTok * (128 * D + 8) * 2 +
+    return size_t(kSegTok) * (128 * D + 8) * 2 +
            (size_t(cbl ? (1 << BITS) : seg_hyb_entries(D)) + 1) * D * 2;
 }
 
