@@ -212,7 +212,10 @@ def _skipzero_proj(torch, dev, g, e, out, inn, d, K, bits, dead):
 
 
 def run_mtp(torch, dev, a, w):
-    """c4: MTP verify batch through the skipzero config-3 layer (composed path)."""
+    """c4: MTP verify batch through the skipzero config-3 layer: one
+    vqk_moe_decode_layer call per layer (routing, one sort, grouped GEMMs,
+    combine on device), or with --mtp-path composed torch's routing and
+    combine around per-projection grouped calls."""
     from vqlab_amd.moe import VQSparseMoeBlock, VQSwitchGLU
     from vqlab_amd.vq_switch import VQSwitchLinear
     from oracle import vq_oracle as vo
@@ -245,7 +248,10 @@ def run_mtp(torch, dev, a, w):
 
     def step(s):
         for l in range(L):
-            ys[l] = layers[l].composed(xs[l], logits[s, l])
+            if a.mtp_path == "composed":
+                ys[l] = layers[l].composed(xs[l], logits[s, l])
+            else:
+                ys[l] = layers[l].fused(xs[l], logits[s, l])
 
     wall, ev_ms = _graph_time(torch, step, a.warmup, a.steps, dev)
     # bytes of the live rows of the experts each call touched (+ the shared expert)
@@ -277,7 +283,8 @@ def run_mtp(torch, dev, a, w):
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_seg_mfma (grouped gate/up/down) + routing/SwiGLU glue",
+                     "kernel": "k_seg_mfma (grouped gate/up/down) + routing / sort / combine",
+                     "path": a.mtp_path,
                      "alg_bytes_per_call": int(alg_per_call),
                      "us_per_call_events": round(us_call, 3)},
         "cpu_baseline": cpu,
@@ -365,6 +372,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--mtp-path", default="fused", choices=("fused", "composed"),
+                    help="c4 workloads: the layer entry point, or torch glue around grouped calls")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "

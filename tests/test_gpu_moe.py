@@ -137,3 +137,37 @@ def test_routing_ties_pick_lower_ids():
     rids, rw = vo.route(lg.astype(np.float32), 6)
     assert np.array_equal(ids.cpu().numpy(), rids)
     assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("D,K,T,shared", [(8, 16384, 8, True), (8, 16384, 16, False),
+                                          (4, 4096, 12, True), (2, 512, 40, False)])
+def test_moe_layer_batched_grouped_path(D, K, T, shared):
+    """T * top_k >= 64 pairs: the layer runs as one routing + one sort +
+    grouped matrix-core GEMMs (SwiGLU built while down's input is staged) +
+    the weighted combine; same oracle, same bar."""
+    print(f"moe batched grouped D={D} K={K} T={T} shared={shared}", flush=True)
+    rng = np.random.default_rng(20 + T + D)
+    E, H, I, k = 32, 1024, 256, 8
+    blk, projs, sh, shv = _block(rng, E, H, I, D, K, k, shared=shared)
+    _check(blk, projs, sh, shv, rng, T, E, H, k)
+
+
+def test_moe_layer_batched_skipzero():
+    """The grouped layer over compact skipzero experts (20% dead rows): dead
+    rows contribute exact zeros, as in the expanded oracle."""
+    from vq_cases import skipzero
+    from vqlab_amd.vq_switch import VQSwitchLinear
+    print("moe batched skipzero", flush=True)
+    rng = np.random.default_rng(31)
+    E, H, I, k, T = 32, 1024, 256, 8, 16
+    blk, projs, _, _ = _block(rng, E, H, I, 8, 16384, k)
+    for name, (o, i) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+        m = make_module(rng, E, o, i, 8, 16384, dead_frac=0.2)
+        projs[name] = m
+        sz, rt = skipzero(m)
+        cb = torch.from_numpy(m["codebook"]).cuda()
+        mod = VQSwitchLinear(torch.from_numpy(sz["sz_codes"].view(np.int32)).cuda(), cb,
+                             torch.from_numpy(sz["sz_scales"]).cuda(), pack_bits=m["pack_bits"],
+                             in_features=i, row_table=torch.from_numpy(rt).cuda())
+        setattr(blk.switch_mlp, name + "_proj", mod)
+    _check(blk, projs, None, None, rng, T, E, H, k)

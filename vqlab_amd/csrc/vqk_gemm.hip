@@ -414,6 +414,64 @@ static int check_acts(const void *x, int32_t x_type, const void *y, int32_t y_ty
     return VQK_OK;
 }
 
+// ---- pieces of the grouped path for callers that sort one routing and run
+// several projections over it (the batched MoE layer)
+static size_t sort_order_bytes(int64_t N) { return al256(sizeof(int32_t) * size_t(N)); }
+static size_t sort_meta_bytes(int64_t N, int64_t E) {
+    return al256(sizeof(int32_t) * 3 * size_t(group_max_tiles(N, E)));
+}
+
+size_t seg_sort_bytes(int64_t N, int64_t E) {
+    return sort_order_bytes(N) + sort_meta_bytes(N, E) + 256;
+}
+
+bool seg_ok(const vqk_weights *w, int64_t N) {
+    Geom g;
+    if (make_geom(w, &g)) return false;
+    return seg_fits_geom(g, w) && g.E <= kMaxSortExperts && group_max_tiles(N, g.E) <= 65535 &&
+           N <= INT32_MAX / 2;
+}
+
+int seg_sort(const uint32_t *eidx, int64_t N, int64_t E, void *ws, hipStream_t st) {
+    if (N == 0) return VQK_OK;
+    uint8_t *b = static_cast<uint8_t *>(ws);
+    const int64_t mt = group_max_tiles(N, E);
+    int32_t *order = reinterpret_cast<int32_t *>(b);
+    int32_t *tmeta = reinterpret_cast<int32_t *>(b + sort_order_bytes(N));
+    int32_t *ntiles = reinterpret_cast<int32_t *>(b + sort_order_bytes(N) + sort_meta_bytes(N, E));
+    const size_t sort_lds = sizeof(int) * (3 * size_t(E + 1) + kSortThreads);
+    hipLaunchKernelGGL(k_group_sort, dim3(1), dim3(kSortThreads), sort_lds, st, eidx, int(N), int(E),
+                       kSegTok, int(mt), order, tmeta, ntiles);
+    return hip_status(hipGetLastError(), "group sort launch");
+}
+
+int seg_run(const vqk_weights *w, const SegCall &c, const void *sort_ws, hipStream_t st) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if (c.N == 0) return VQK_OK;
+    SegParams sp;
+    fill_seg(w, g, &sp);
+    sp.x = c.x;
+    sp.x_type = c.x_type;
+    sp.xg = c.xg;
+    sp.xu = c.xu;
+    sp.xkrep = int32_t(c.xkrep);
+    sp.y = c.y;
+    sp.y_type = c.y_type;
+    sp.N = int32_t(c.N);
+    int64_t tiles = (c.N + kSegTok - 1) / kSegTok;
+    if (sort_ws) {
+        const uint8_t *b = static_cast<const uint8_t *>(sort_ws);
+        sp.order = reinterpret_cast<const int32_t *>(b);
+        sp.tmeta = reinterpret_cast<const int32_t *>(b + sort_order_bytes(c.N));
+        sp.ntiles = reinterpret_cast<const int32_t *>(b + sort_order_bytes(c.N) + sort_meta_bytes(c.N, g.E));
+        tiles = group_max_tiles(c.N, g.E);
+    }
+    const dim3 grid(unsigned((g.OUT + kSegRows - 1) / kSegRows), unsigned(tiles), 1);
+    return launch_seg(sp, g, grid, st);
+}
+
 }  // namespace vqk
 
 using namespace vqk;
@@ -514,8 +572,7 @@ int vqk_grouped_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes) {
     int rc = make_geom(w, &g);
     if (rc) return rc;
     if (!bytes || N < 0) return set_error(VQK_EINVAL, "bad arguments");
-    const int64_t mt = group_max_tiles(N, g.E);
-    *bytes = al256(sizeof(int32_t) * size_t(N)) + al256(sizeof(int32_t) * 3 * size_t(mt)) + 256;
+    *bytes = seg_sort_bytes(N, g.E);
     return VQK_OK;
 }
 
@@ -542,28 +599,13 @@ int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_
     if (mt > 65535) return set_error(VQK_ENOTIMPL, "%lld tiles exceed one launch", (long long)mt);
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     int32_t *order = reinterpret_cast<int32_t *>(ws);
-    int32_t *tmeta = reinterpret_cast<int32_t *>(ws + al256(sizeof(int32_t) * size_t(N)));
-    int32_t *ntiles = reinterpret_cast<int32_t *>(ws + al256(sizeof(int32_t) * size_t(N)) +
-                                                  al256(sizeof(int32_t) * 3 * size_t(mt)));
+    int32_t *tmeta = reinterpret_cast<int32_t *>(ws + sort_order_bytes(N));
+    int32_t *ntiles = reinterpret_cast<int32_t *>(ws + sort_order_bytes(N) + sort_meta_bytes(N, g.E));
     hipStream_t st = hipStream_t(stream);
-    const size_t sort_lds = sizeof(int) * (3 * size_t(g.E + 1) + kSortThreads);
-    hipLaunchKernelGGL(k_group_sort, dim3(1), dim3(kSortThreads), sort_lds, st, eidx, int(N),
-                       int(g.E), kSegTok, int(mt), order, tmeta, ntiles);
-    if ((rc = hip_status(hipGetLastError(), "group sort launch"))) return rc;
+    if ((rc = seg_sort(eidx, N, g.E, ws, st))) return rc;
     if (seg_fits(g, w, x)) {
-        SegParams sp;
-        fill_seg(w, g, &sp);
-        sp.x = x;
-        sp.x_type = x_type;
-        sp.xkrep = int32_t(xkrep);
-        sp.y = y;
-        sp.y_type = y_type;
-        sp.N = int32_t(N);
-        sp.tmeta = tmeta;
-        sp.ntiles = ntiles;
-        sp.order = order;
-        const dim3 grid(unsigned((g.OUT + kSegRows - 1) / kSegRows), unsigned(mt), 1);
-        return launch_seg(sp, g, grid, st);
+        const SegCall c{x, x_type, nullptr, nullptr, xkrep, y, y_type, N};
+        return seg_run(w, c, ws, st);
     }
     GemmParams p;
     if ((rc = fill_gemm(w, g, &p))) return rc;

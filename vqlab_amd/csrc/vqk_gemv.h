@@ -216,15 +216,17 @@ __device__ __forceinline__ void stage_codebook_fixed(const uint16_t *cb, int K, 
     const uint8_t *s = reinterpret_cast<const uint8_t *>(cb);
     uint8_t *d = reinterpret_cast<uint8_t *>(dst);
     const int lane = threadIdx.x & (kWave - 1), wave = int(threadIdx.x >> 6) - W0;
-    const int valid = (K * D * 2) >> 4;                      // whole valid pieces
+    // whole pieces to copy: all of a table that fits, the first CBN entries
+    // of a larger one (ROUNDS * NT may exceed PIECES: never copy past it)
+    const int valid = min((K * D * 2) >> 4, PIECES);
 #pragma unroll
     for (int r = 0; r < ROUNDS; ++r) {
         const int c = (r * (NT / kWave) + wave) * kWave;     // first piece of this wave's chunk
-        if (c + lane < valid)                                // valid <= PIECES
+        if (c + lane < valid)
             __builtin_amdgcn_global_load_lds((global_void *)(s + int64_t(c + lane) * 16),
                                              (lds_void *)(d + int64_t(c) * 16), 16, 0, 0);
     }
-    if (valid == PIECES) return;                             // the whole table came over
+    if (valid == PIECES) return;                             // the LDS table is full
     // the sub-16-byte tail of the valid bytes (at most 3 words, one load per
     // thread), then zeros up to the table end
     const int tail_words = ((K * D * 2) >> 2) - valid * 4;

@@ -18,4 +18,30 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
                 const uint32_t *eidx, int64_t N, int64_t xkrep, void *y, int32_t y_type,
                 hipStream_t st);
 
+// ---- grouped expert GEMM pieces (vqk_gemm.hip): sort one routing, then run
+// several projections over it with the register-decode segment kernel.
+struct SegCall {
+    const void *x;             // activations (x_type), or NULL with xg / xu:
+    int32_t x_type;
+    const float *xg, *xu;      //   row = fp16(silu(xg) * xu), fp32 rows of the module's IN
+    int64_t xkrep;             // x row of pair n = n / xkrep
+    void *y;                   // y[pair, OUT] in y_type
+    int32_t y_type;
+    int64_t N;                 // pairs (sorted) or dense rows (sort_ws == NULL)
+};
+
+// Workspace of seg_sort for N pairs over E experts.
+size_t seg_sort_bytes(int64_t N, int64_t E);
+
+// True when the segment kernel takes module `w` for N pairs.
+bool seg_ok(const vqk_weights *w, int64_t N);
+
+// Counting sort of N pair experts (device uint32, out-of-range ids form dead
+// tiles) into `ws`: pair order, tile records and the tile count.
+int seg_sort(const uint32_t *eidx, int64_t N, int64_t E, void *ws, hipStream_t st);
+
+// One projection over a routing sorted into `sort_ws` (or over N dense rows
+// of expert 0 when sort_ws is NULL).
+int seg_run(const vqk_weights *w, const SegCall &c, const void *sort_ws, hipStream_t st);
+
 }  // namespace vqk

@@ -25,6 +25,12 @@ namespace vqk {
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxSlots = kMaxExperts / kWave;   // logits per lane
 constexpr int kMaxTopK = 64;
+// (token, expert) pairs from which a layer call runs as grouped GEMMs: at
+// least this many, and at least one per expert on average (fewer leave most
+// expert tiles with a single pair, where the GEMV paths measured faster:
+// config-3 layer, T = 16 -> 160 pairs over 512 experts: 698 us sliced GEMV
+// against 745 us grouped; T = 64: 2583 us against 1588 us)
+constexpr int64_t kMoeGroupedMinPairs = 64;
 
 struct MoeW {            // one projection of the layer, as the kernels see it
     const uint32_t *codes;
@@ -536,18 +542,24 @@ static size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
 struct MoeLayout {
     size_t ids, wts, sg, h, total;
-    size_t g, u, sgg, sgu, yd, ysh;      // composed (codebooks beyond LDS) path only
+    size_t g, u, sgg, sgu, yd, ysh;      // composed paths (sliced-codebook GEMV, grouped GEMM)
+    size_t sort;                         // grouped path: pair order and tile records
 };
 
-static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I, int64_t H, bool big) {
+// Paths of the layer: the two fused decode kernels, the sliced-codebook GEMV
+// composition (codebooks beyond LDS, batch >= 2), the grouped-GEMM
+// composition (many pairs).
+enum MoePath { kMoeFused = 0, kMoeBig = 1, kMoeGrouped = 2 };
+
+static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I, int64_t H, int path, int64_t E) {
     MoeLayout L;
     L.ids = 0;
     L.wts = align_up(L.ids + sizeof(int32_t) * T * k);
     L.sg = align_up(L.wts + sizeof(float) * T * k);
     L.h = align_up(L.sg + sizeof(float) * T);
-    L.total = align_up(L.h + 2 * size_t(T) * P * I);
-    L.g = L.u = L.sgg = L.sgu = L.yd = L.ysh = 0;
-    if (big) {
+    L.total = align_up(L.h + (path == kMoeFused ? 2 * size_t(T) * P * I : 0));
+    L.g = L.u = L.sgg = L.sgu = L.yd = L.ysh = L.sort = 0;
+    if (path != kMoeFused) {
         L.g = L.total;
         L.u = align_up(L.g + 4 * size_t(T) * k * I);
         L.sgg = align_up(L.u + 4 * size_t(T) * k * I);
@@ -555,6 +567,10 @@ static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I, int64_t H, bool 
         L.yd = align_up(L.sgu + 4 * size_t(T) * I);
         L.ysh = align_up(L.yd + 4 * size_t(T) * k * H);
         L.total = align_up(L.ysh + 4 * size_t(T) * H);
+    }
+    if (path == kMoeGrouped) {
+        L.sort = L.total;
+        L.total = align_up(L.sort + seg_sort_bytes(T * k, E));
     }
     return L;
 }
@@ -580,7 +596,7 @@ struct MoePlan {
     MoeLayout lay;
     size_t smem1, smem2;
     dim3 grid1, grid2;
-    bool big;                 // codebooks beyond LDS: the composed sliced-codebook path
+    int path;                 // MoePath
 };
 
 static int lg2(int64_t v) {
@@ -684,20 +700,28 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     const size_t cb2 = full2 ? (size_t(1) << gd.BITS) * gd.D * 2 : size_t(kHybDownBytes);
     pl->smem1 = 2 * cb1 + size_t(gg.NB) * (kBlock * gg.D + 8) * 2;
     pl->smem2 = ((shared && full2) ? 2 : 1) * cb2 + size_t(P) * gd.NB * (kBlock * gd.D + 8) * 2;
-    if (pl->smem1 > 160 * 1024 || pl->smem2 > 160 * 1024)
-        return set_error(VQK_ENOTIMPL, "fused layer: LDS need %zu / %zu B exceeds 160 KB",
-                         pl->smem1, pl->smem2);
-    // batch >= 2: the composed sliced-codebook path; batch 1 keeps the two fused
-    // kernels (partly LDS-staged tables), which measured faster there
-    pl->big = T >= 2 && big_fits(gg, m->gate) && big_fits(gu, m->up) && big_fits(gd, m->down);
-    if (pl->big && shared) {
+    // Many pairs: sort once and run each projection as a grouped matrix-core
+    // GEMM (weights decoded once per tile of up to 16 pairs of an expert).
+    // Batch >= 2 with tables beyond LDS: the sliced-codebook GEMV composition.
+    // Otherwise the two fused kernels (partly LDS-staged tables).
+    const int64_t N = T * k;
+    bool grouped = N >= kMoeGroupedMinPairs && N >= E && seg_ok(m->gate, N) && seg_ok(m->up, N) &&
+                   seg_ok(m->down, N);
+    if (grouped && shared)
+        grouped = seg_ok(m->sh_gate, T) && seg_ok(m->sh_up, T) && seg_ok(m->sh_down, T);
+    bool big = T >= 2 && big_fits(gg, m->gate) && big_fits(gu, m->up) && big_fits(gd, m->down);
+    if (big && shared) {
         Geom a, b, c;
         make_geom(m->sh_gate, &a);
         make_geom(m->sh_up, &b);
         make_geom(m->sh_down, &c);
-        pl->big = big_fits(a, m->sh_gate) && big_fits(b, m->sh_up) && big_fits(c, m->sh_down);
+        big = big_fits(a, m->sh_gate) && big_fits(b, m->sh_up) && big_fits(c, m->sh_down);
     }
-    pl->lay = moe_layout(T, k, P, gg.OUT, gg.IN, pl->big);
+    pl->path = grouped ? kMoeGrouped : (big ? kMoeBig : kMoeFused);
+    if (pl->path == kMoeFused && (pl->smem1 > 160 * 1024 || pl->smem2 > 160 * 1024))
+        return set_error(VQK_ENOTIMPL, "fused layer: LDS need %zu / %zu B exceeds 160 KB",
+                         pl->smem1, pl->smem2);
+    pl->lay = moe_layout(T, k, P, gg.OUT, gg.IN, pl->path, E);
     return VQK_OK;
 }
 
@@ -815,6 +839,41 @@ static int launch_moe_big(const vqk_moe_desc *m, const MoePlan &pl, uint8_t *ws,
     return hip_status(hipGetLastError(), "combine launch");
 }
 
+// Many pairs: routing (one wave per token), one counting sort of the pairs by
+// expert, gate and up as grouped GEMMs into fp32 rows, down as a grouped GEMM
+// whose input rows are built as fp16(silu(g) * u) while they are staged, the
+// shared expert as the same kernels over the token rows, and the weighted
+// combine.
+static int launch_moe_grouped(const vqk_moe_desc *m, const MoePlan &pl, uint8_t *ws, hipStream_t st) {
+    const MoeParams &p = pl.p;
+    const int64_t T = p.T, k = p.top_k, N = T * k;
+    float *g = reinterpret_cast<float *>(ws + pl.lay.g), *u = reinterpret_cast<float *>(ws + pl.lay.u);
+    float *sgg = reinterpret_cast<float *>(ws + pl.lay.sgg), *sgu = reinterpret_cast<float *>(ws + pl.lay.sgu);
+    float *yd = reinterpret_cast<float *>(ws + pl.lay.yd), *ysh = reinterpret_cast<float *>(ws + pl.lay.ysh);
+    void *sort = ws + pl.lay.sort;
+    hipLaunchKernelGGL(k_route_tokens, dim3(unsigned(T)), dim3(kWave), 0, st, p);
+    int rc = hip_status(hipGetLastError(), "routing launch");
+    if (rc) return rc;
+    if ((rc = seg_sort(reinterpret_cast<const uint32_t *>(p.ids), N, p.E, sort, st))) return rc;
+    SegCall c{p.x, p.x_type, nullptr, nullptr, k, g, VQK_F32, N};
+    if ((rc = seg_run(m->gate, c, sort, st))) return rc;
+    c.y = u;
+    if ((rc = seg_run(m->up, c, sort, st))) return rc;
+    SegCall d{nullptr, VQK_F32, g, u, 1, yd, VQK_F32, N};
+    if ((rc = seg_run(m->down, d, sort, st))) return rc;
+    if (p.shared) {
+        SegCall cs{p.x, p.x_type, nullptr, nullptr, 1, sgg, VQK_F32, T};
+        if ((rc = seg_run(m->sh_gate, cs, nullptr, st))) return rc;
+        cs.y = sgu;
+        if ((rc = seg_run(m->sh_up, cs, nullptr, st))) return rc;
+        SegCall ds{nullptr, VQK_F32, sgg, sgu, 1, ysh, VQK_F32, T};
+        if ((rc = seg_run(m->sh_down, ds, nullptr, st))) return rc;
+    }
+    hipLaunchKernelGGL(k_moe_combine, dim3(unsigned((p.H + 255) / 256), unsigned(T)), dim3(256), 0, st,
+                       p, static_cast<const float *>(yd), static_cast<const float *>(ysh));
+    return hip_status(hipGetLastError(), "combine launch");
+}
+
 }  // namespace vqk
 
 using namespace vqk;
@@ -856,7 +915,12 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, i
     p.y = y;
     p.y_type = y_type;
     hipStream_t st = hipStream_t(stream);
-    if (pl.big) return launch_moe_big(m, pl, ws, st);
+    if (pl.path == kMoeGrouped) {
+        if ((reinterpret_cast<uintptr_t>(x) & 15) != 0)
+            return set_error(VQK_EINVAL, "batched layer: x must be 16-byte aligned");
+        return launch_moe_grouped(m, pl, ws, st);
+    }
+    if (pl.path == kMoeBig) return launch_moe_big(m, pl, ws, st);
     rc = launch_moe_up(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.grid1, pl.smem1, st);
     if (rc) return rc;
     return launch_moe_down(p, pl.g2.D, pl.g2.BITS, pl.g2.gpb, pl.grid2, pl.smem2, st);
