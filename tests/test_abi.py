@@ -194,3 +194,33 @@ def test_embed_argument_errors(L):
     # nothing to gather: valid and no launch
     assert lib.vqk_embed_gather(ctypes.byref(w), None, L.VQK_I32, 0, None, L.VQK_F16,
                                 None) == L.VQK_OK
+
+
+def _staged_pieces(K, D, CBN, NT):
+    """The 16-byte pieces stage_codebook_fixed<D, CBN, NT> copies (vqk_gemv.h),
+    restated: round r, wave w, lane l copies piece (r*NT/64 + w)*64 + l when
+    it is below min(K*D*2/16, CBN*D*2/16)."""
+    pieces = CBN * D * 2 // 16
+    valid = min(K * D * 2 // 16, pieces)
+    rounds = -(-pieces // NT)
+    out = set()
+    for r in range(rounds):
+        for w in range(NT // 64):
+            c = (r * (NT // 64) + w) * 64
+            out.update(c + l for l in range(64) if c + l < valid)
+    return out, pieces, valid
+
+
+@pytest.mark.parametrize("D,BITS", [(2, 9), (4, 12), (4, 14), (8, 12), (8, 14), (8, 16), (2, 16)])
+@pytest.mark.parametrize("NT", [256, 192])
+def test_codebook_staging_stays_in_its_table(D, BITS, NT):
+    """Every launch shape that stages a table (whole tables of 2^BITS entries
+    up to 64 KB; the first 64 KB / 128 KB of larger ones) copies each valid
+    piece exactly once and nothing past the LDS table, also when NT threads
+    do not divide the table (the 192 staging threads of the fused layer)."""
+    full = (1 << BITS) * D * 2 <= 64 * 1024
+    for cbn_bytes in ([(1 << BITS) * D * 2] if full else [64 * 1024, 128 * 1024]):
+        CBN = cbn_bytes // (2 * D)
+        for K in {1 << BITS, (1 << BITS) - 8, 8}:
+            got, pieces, valid = _staged_pieces(K, D, CBN, NT)
+            assert got == set(range(valid)) and max(got, default=0) < pieces
