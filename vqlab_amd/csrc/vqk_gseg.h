@@ -130,22 +130,6 @@ __host__ __device__ constexpr int seg_hyb_entries(int D) {
 }
 
 
-// Eight fp16 values fp16(silu(g) * u) of fp32 gate / up rows (the SwiGLU
-// product the fused layer writes), packed as four words; 32-byte aligned.
-__device__ __forceinline__ u32x4 swiglu8(const float *g, const float *u) {
-    const u32x4 g0 = reinterpret_cast<const u32x4 *>(g)[0], g1 = reinterpret_cast<const u32x4 *>(g)[1];
-    const u32x4 u0 = reinterpret_cast<const u32x4 *>(u)[0], u1 = reinterpret_cast<const u32x4 *>(u)[1];
-    const uint32_t gw[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-    const uint32_t uw[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-    uint32_t h[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float gv = __uint_as_float(gw[i]);
-        h[i] = f32_to_h(gv / (1.f + __expf(-gv)) * __uint_as_float(uw[i]));
-    }
-    return u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-}
-
 template <int D, int BITS, int GPB, bool CBL>
 __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     constexpr int TN = 2;                       // 16-row tiles per wave

@@ -63,6 +63,7 @@ struct MoeParams {
     float *wts;          // workspace [T, top_k]
     float *sg;           // workspace [T]
     uint16_t *h;         // workspace [T, P, I] fp16
+    float *gbuf, *ubuf;  // split gate/up phase: workspace [T, P, I] fp32 each, else NULL
     int32_t *ids_out;    // optional user copies
     float *wts_out;
 };
@@ -344,6 +345,100 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
     up_body<D, BITS, GPB>(p, int(blockIdx.x), int(blockIdx.y), smem, rl, NoPre{});
 }
 
+// K1 for tables beyond LDS: one projection per workgroup (blockIdx.z: 0 gate,
+// 1 up), so its table gets the LDS of two (the first kHybSplitBytes of it)
+// and more of the codes read LDS instead of L2 -- the request rate that
+// bounds these tables. The rows go out as fp32; K2 builds silu(g) * u from
+// them as it stages its input.
+constexpr int kHybSplitBytes = 128 * 1024;
+
+template <int D, int BITS, int GPB>
+__global__ void __launch_bounds__(kThreads) k_moe_up_split(const MoeParams p) {
+    constexpr int CBN = kHybSplitBytes / (2 * D);
+    constexpr int XH = kBlock * D, XS = XH + 8;
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ RouteLds rl;
+    h2 *cb_lds = reinterpret_cast<h2 *>(smem);
+    f16 *xs = reinterpret_cast<f16 *>(smem + CBN * D * 2);
+
+    const int bx = int(blockIdx.x), pair = int(blockIdx.y), proj = int(blockIdx.z);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int lpr = 1 << p.lpr1_log2, rpw = kWave >> p.lpr1_log2;
+    const int sub = lane >> p.lpr1_log2, blk = lane & (lpr - 1);
+    const bool on = blk < p.NB1;
+    const int t = pair / p.P, j = pair % p.P;
+    const bool is_shared = j >= p.top_k;
+    const MoeW &w = proj == 0 ? (is_shared ? p.sgate : p.gate) : (is_shared ? p.sup : p.up);
+    const float *lg = p.logits + int64_t(t) * p.E;
+
+    // wave 0 routes with nothing else in flight; waves 1-3 stage the table and x
+    int my_idx = -1;
+    float my_w = 0.f;
+    if (wave == 0) {
+        int e_pair;
+        route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &e_pair, &my_idx, &my_w);
+        if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
+        if (lane == 0) rl.route = e_pair;
+    } else {
+        constexpr int NT = kThreads - kWave;
+        stage_codebook_fixed<D, CBN, NT, 1>(w.codebook, w.K, cb_lds);
+        stage_x<XH, XS>(p.x, p.x_type, int64_t(t) * p.H, p.H, p.NB1, xs, kWave, NT);
+    }
+    if (bx == 0 && j == 0 && proj == 0 && wave == 0) {
+        if (lane < p.top_k) {
+            p.ids[t * p.top_k + lane] = my_idx;
+            p.wts[t * p.top_k + lane] = my_w;
+            if (p.ids_out) p.ids_out[t * p.top_k + lane] = my_idx;
+            if (p.wts_out) p.wts_out[t * p.top_k + lane] = my_w;
+        }
+        if (p.shared) {
+            float acc = 0.f;
+            for (int i = lane; i < p.H; i += kWave)
+                acc += load_act(p.x, p.x_type, int64_t(t) * p.H + i) * load_act(p.sg_vec, p.sg_type, i);
+            acc = wave_sum(acc);
+            if (lane == 0) p.sg[t] = 1.f / (1.f + __expf(-acc));
+        }
+    }
+    wait_vmem();
+    __syncthreads();
+
+    const int e_pair = rl.route;
+    const int64_t e = is_shared ? 0 : ((e_pair >= 0 && e_pair < p.E) ? e_pair : -1);
+    const int sidx = GPB == 1 ? blk / p.bpg1 : blk * GPB;
+    const int r_wg = bx * p.rows_per_wg1;
+    auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * rpw + sub; };
+    auto code_row = [&](int st) -> int64_t {
+        const int r = row_at(st);
+        return (on && e >= 0 && r < p.I) ? moe_row(w, e, p.I, r) : -1;
+    };
+
+    uint32_t a[BITS];
+    float sc[GPB];
+    int64_t cr = code_row(0);
+    moe_load<BITS, GPB>(w, cr, blk, sidx, p.ngrp1, a, sc);
+    h2 xr[16 * D];
+    load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
+    const h2 *cbg = reinterpret_cast<const h2 *>(w.codebook);
+    const uint32_t kl = uint32_t(min(w.K, CBN));
+    float *out = (proj == 0 ? p.gbuf : p.ubuf) + (int64_t(t) * p.P + j) * p.I;
+    for (int st = 0; st < p.steps1; ++st) {
+        uint32_t n[BITS];
+        float ns[GPB];
+        const int64_t crn = st + 1 < p.steps1 ? code_row(st + 1) : -1;
+        moe_load<BITS, GPB>(w, crn, blk, sidx, p.ngrp1, n, ns);
+        float v = 0.f;
+        if (cr >= 0) v = block_dot_hyb<D, BITS, GPB>(a, xr, sc, cb_lds, cbg, kl, uint32_t(w.K - 1));
+        v = group_sum(v, lpr);
+        const int r = row_at(st);
+        if (blk == lpr - 1 && r < p.I) out[r] = v;
+        cr = crn;
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) a[i] = n[i];
+#pragma unroll
+        for (int g = 0; g < GPB; ++g) sc[g] = ns[g];
+    }
+}
+
 // ------------------------------------------------------------ K2: down + combine
 // Lane geometry of the down phase: lanes are (pair j, block) of one row,
 // LPR2 = next_pow2(P * NB2) lanes per row.
@@ -413,6 +508,7 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
     const MoeW &wd = dl.is_shared ? p.sdown : p.down;
     {
         const uint16_t *hsrc = p.h + int64_t(t) * p.P * p.I;
+        const int64_t f0 = int64_t(t) * p.P * p.I;   // split phase: fp32 g / u rows
         const int gpr = p.I / 8;                     // 8-value groups per row
         const int ng = p.P * gpr;
         constexpr int U = 8;
@@ -421,8 +517,12 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int g = g0 + u * blockDim.x;
-                hv[u] = g < ng ? *reinterpret_cast<const u32x4 *>(hsrc + int64_t(g) * 8)
-                               : u32x4{0, 0, 0, 0};
+                if (p.gbuf)
+                    hv[u] = g < ng ? swiglu8(p.gbuf + f0 + int64_t(g) * 8, p.ubuf + f0 + int64_t(g) * 8)
+                                   : u32x4{0, 0, 0, 0};
+                else
+                    hv[u] = g < ng ? *reinterpret_cast<const u32x4 *>(hsrc + int64_t(g) * 8)
+                                   : u32x4{0, 0, 0, 0};
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -544,6 +644,7 @@ struct MoeLayout {
     size_t ids, wts, sg, h, total;
     size_t g, u, sgg, sgu, yd, ysh;      // composed paths (sliced-codebook GEMV, grouped GEMM)
     size_t sort;                         // grouped path: pair order and tile records
+    size_t gs, us;                       // fused path, split K1: fp32 gate / up rows
 };
 
 // Paths of the layer: the two fused decode kernels, the sliced-codebook GEMV
@@ -551,14 +652,20 @@ struct MoeLayout {
 // composition (many pairs).
 enum MoePath { kMoeFused = 0, kMoeBig = 1, kMoeGrouped = 2 };
 
-static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I, int64_t H, int path, int64_t E) {
+static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I, int64_t H, int path, int64_t E,
+                            bool split) {
     MoeLayout L;
     L.ids = 0;
     L.wts = align_up(L.ids + sizeof(int32_t) * T * k);
     L.sg = align_up(L.wts + sizeof(float) * T * k);
     L.h = align_up(L.sg + sizeof(float) * T);
-    L.total = align_up(L.h + (path == kMoeFused ? 2 * size_t(T) * P * I : 0));
-    L.g = L.u = L.sgg = L.sgu = L.yd = L.ysh = L.sort = 0;
+    L.total = align_up(L.h + (path == kMoeFused && !split ? 2 * size_t(T) * P * I : 0));
+    L.g = L.u = L.sgg = L.sgu = L.yd = L.ysh = L.sort = L.gs = L.us = 0;
+    if (path == kMoeFused && split) {
+        L.gs = L.total;
+        L.us = align_up(L.gs + 4 * size_t(T) * P * I);
+        L.total = align_up(L.us + 4 * size_t(T) * P * I);
+    }
     if (path != kMoeFused) {
         L.g = L.total;
         L.u = align_up(L.g + 4 * size_t(T) * k * I);
@@ -597,6 +704,7 @@ struct MoePlan {
     size_t smem1, smem2;
     dim3 grid1, grid2;
     int path;                 // MoePath
+    bool split;               // fused path, tables beyond LDS: one projection per K1 workgroup
 };
 
 static int lg2(int64_t v) {
@@ -677,14 +785,18 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     p.sg_vec = m->sh_gate_vec;
     p.sg_type = m->sh_gate_vec_type;
     const int64_t target = 2048;
-    {   // K1: T*P pairs x I rows
+    const bool full1 = cb_in_lds(gg.D, gg.BITS), full2 = cb_in_lds(gd.D, gd.BITS);
+    pl->split = !full1;
+    {   // K1: T*P pairs x I rows (x 2 projections when split)
         const int rpw = kWave >> p.lpr1_log2;
-        const int64_t steps_total = T * P * ((gg.OUT + rpw - 1) / rpw);
+        const int nz = pl->split ? 2 : 1;
+        const int64_t steps_total = T * P * nz * ((gg.OUT + rpw - 1) / rpw);
         int64_t st = (steps_total + target - 1) / target;
         st = st < 1 ? 1 : (st > 16 ? 16 : st);
         p.steps1 = int32_t(st);
         p.rows_per_wg1 = int32_t(4 * rpw * st);
-        pl->grid1 = dim3(unsigned((gg.OUT + p.rows_per_wg1 - 1) / p.rows_per_wg1), unsigned(T * P), 1);
+        pl->grid1 = dim3(unsigned((gg.OUT + p.rows_per_wg1 - 1) / p.rows_per_wg1), unsigned(T * P),
+                         unsigned(nz));
     }
     {   // K2: T tokens x H rows
         const int rpw = kWave >> p.lpr2_log2;
@@ -695,10 +807,9 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
         p.rows_per_wg2 = int32_t(4 * rpw * st);
         pl->grid2 = dim3(unsigned((gd.OUT + p.rows_per_wg2 - 1) / p.rows_per_wg2), unsigned(T), 1);
     }
-    const bool full1 = cb_in_lds(gg.D, gg.BITS), full2 = cb_in_lds(gd.D, gd.BITS);
     const size_t cb1 = full1 ? (size_t(1) << gg.BITS) * gg.D * 2 : size_t(kHybUpBytes);
     const size_t cb2 = full2 ? (size_t(1) << gd.BITS) * gd.D * 2 : size_t(kHybDownBytes);
-    pl->smem1 = 2 * cb1 + size_t(gg.NB) * (kBlock * gg.D + 8) * 2;
+    pl->smem1 = (pl->split ? size_t(kHybSplitBytes) : 2 * cb1) + size_t(gg.NB) * (kBlock * gg.D + 8) * 2;
     pl->smem2 = ((shared && full2) ? 2 : 1) * cb2 + size_t(P) * gd.NB * (kBlock * gd.D + 8) * 2;
     // Many pairs: sort once and run each projection as a grouped matrix-core
     // GEMM (weights decoded once per tile of up to 16 pairs of an expert).
@@ -721,7 +832,7 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     if (pl->path == kMoeFused && (pl->smem1 > 160 * 1024 || pl->smem2 > 160 * 1024))
         return set_error(VQK_ENOTIMPL, "fused layer: LDS need %zu / %zu B exceeds 160 KB",
                          pl->smem1, pl->smem2);
-    pl->lay = moe_layout(T, k, P, gg.OUT, gg.IN, pl->path, E);
+    pl->lay = moe_layout(T, k, P, gg.OUT, gg.IN, pl->path, E, pl->split);
     return VQK_OK;
 }
 
@@ -731,6 +842,21 @@ int launch_moe_down(const MoeParams &p, int D, int bits, int gpb, dim3 grid, siz
 template <int D, int BITS, int GPB>
 static int go_up(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
     return launch_with_lds<k_moe_up<D, BITS, GPB>>(grid, dim3(kThreads), smem, st, p);
+}
+template <int D, int BITS, int GPB>
+static int go_up_split(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
+    return launch_with_lds<k_moe_up_split<D, BITS, GPB>>(grid, dim3(kThreads), smem, st, p);
+}
+// Split gate/up kernel: only the widths whose table exceeds the LDS-resident
+// limit (d2 15-16 bits, d4 14-16, d8 13-16).
+#define VQK_SPLIT_CASE(D, B, G) \
+    if (d == D && bits == B && gpb == G) return go_up_split<D, B, G>(p, grid, smem, st);
+static int launch_moe_up_split(const MoeParams &p, int d, int bits, int gpb, dim3 grid, size_t smem,
+                               hipStream_t st) {
+    VQK_SPLIT_CASE(2, 15, 1) VQK_SPLIT_CASE(2, 16, 1)
+    VQK_SPLIT_CASE(4, 14, 2) VQK_SPLIT_CASE(4, 15, 2) VQK_SPLIT_CASE(4, 16, 2)
+    VQK_SPLIT_CASE(8, 13, 4) VQK_SPLIT_CASE(8, 14, 4) VQK_SPLIT_CASE(8, 15, 4) VQK_SPLIT_CASE(8, 16, 4)
+    return set_error(VQK_ENOTIMPL, "fused layer: no split gate/up kernel for d=%d bits=%d", d, bits);
 }
 template <int D, int BITS, int GPB>
 static int go_down(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
@@ -907,6 +1033,9 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, i
     p.wts = reinterpret_cast<float *>(ws + pl.lay.wts);
     p.sg = reinterpret_cast<float *>(ws + pl.lay.sg);
     p.h = reinterpret_cast<uint16_t *>(ws + pl.lay.h);
+    const bool split = pl.path == kMoeFused && pl.split;
+    p.gbuf = split ? reinterpret_cast<float *>(ws + pl.lay.gs) : nullptr;
+    p.ubuf = split ? reinterpret_cast<float *>(ws + pl.lay.us) : nullptr;
     p.ids_out = topk_ids;
     p.wts_out = topk_w;
     p.x = x;
@@ -921,7 +1050,8 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, i
         return launch_moe_grouped(m, pl, ws, st);
     }
     if (pl.path == kMoeBig) return launch_moe_big(m, pl, ws, st);
-    rc = launch_moe_up(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.grid1, pl.smem1, st);
+    rc = split ? launch_moe_up_split(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.grid1, pl.smem1, st)
+               : launch_moe_up(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.grid1, pl.smem1, st);
     if (rc) return rc;
     return launch_moe_down(p, pl.g2.D, pl.g2.BITS, pl.g2.gpb, pl.grid2, pl.smem2, st);
 }
