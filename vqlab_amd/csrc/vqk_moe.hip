@@ -150,6 +150,54 @@ __device__ __forceinline__ void route(const float *lg, int E, int k, int norm, i
 
 __device__ __forceinline__ float silu(float g) { return g / (1.f + __expf(-g)); }
 
+// Eight activations of a 16-bit type (raw words) as fp32: exact widening.
+__device__ __forceinline__ float act16_f32(uint32_t w, int k, int32_t type) {
+    const uint16_t h = uint16_t(k ? (w >> 16) : w);
+    return type == VQK_BF16 ? bf16_to_f32(h) : h_to_f32(h);
+}
+
+// sum_i x[t, i] * sg_vec[i] over the wave (every lane gets it): the shared
+// expert's gate logit. 16-bit x and gate vector, 16-byte aligned: each lane
+// issues the 16-byte loads of up to 8 chunks of 8 before it multiplies, so
+// the dot costs one memory latency per 4096 values; other layouts take the
+// element loop.
+__device__ __forceinline__ float shared_gate_dot(const void *x, int32_t x_type, const void *sg_vec,
+                                                int32_t sg_type, int H, int t) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t xb = int64_t(t) * H;
+    const bool vec = x_type != VQK_F32 && sg_type != VQK_F32 && (H % 8) == 0 &&
+                     ((reinterpret_cast<uintptr_t>(x) + uint64_t(xb) * 2) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(sg_vec) & 15) == 0;
+    float acc = 0.f;
+    if (vec) {
+        constexpr int U = 8;
+        const int nc = H / 8;
+        const uint16_t *xr = static_cast<const uint16_t *>(x) + xb;
+        const uint16_t *gr = static_cast<const uint16_t *>(sg_vec);
+        for (int c0 = 0; c0 < nc; c0 += U * kWave) {
+            u32x4 xv[U], gv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + lane + u * kWave;
+                xv[u] = c < nc ? *reinterpret_cast<const u32x4 *>(xr + int64_t(c) * 8) : u32x4{0, 0, 0, 0};
+                gv[u] = c < nc ? *reinterpret_cast<const u32x4 *>(gr + int64_t(c) * 8) : u32x4{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t xw[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+                const uint32_t gw[4] = {gv[u].x, gv[u].y, gv[u].z, gv[u].w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    acc = fmaf(act16_f32(xw[k >> 1], k & 1, x_type), act16_f32(gw[k >> 1], k & 1, sg_type), acc);
+            }
+        }
+    } else {
+        for (int i = lane; i < H; i += kWave)
+            acc += load_act(x, x_type, xb + i) * load_act(sg_vec, sg_type, i);
+    }
+    return wave_sum(acc);
+}
+
 template <int BITS, int GPB>
 __device__ __forceinline__ void moe_load(const MoeW &w, int64_t cr, int blk, int sidx, int ngrp,
                                          uint32_t (&wd)[BITS], float (&s)[GPB]) {
@@ -264,10 +312,7 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
             if (p.wts_out) p.wts_out[t * p.top_k + lane] = my_w;
         }
         if (p.shared) {
-            float acc = 0.f;
-            for (int i = lane; i < p.H; i += kWave)
-                acc += load_act(p.x, p.x_type, int64_t(t) * p.H + i) * load_act(p.sg_vec, p.sg_type, i);
-            acc = wave_sum(acc);
+            const float acc = shared_gate_dot(p.x, p.x_type, p.sg_vec, p.sg_type, p.H, t);
             if (lane == 0) p.sg[t] = 1.f / (1.f + __expf(-acc));
         }
     }
@@ -392,10 +437,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_up_split(const MoeParams p) {
             if (p.wts_out) p.wts_out[t * p.top_k + lane] = my_w;
         }
         if (p.shared) {
-            float acc = 0.f;
-            for (int i = lane; i < p.H; i += kWave)
-                acc += load_act(p.x, p.x_type, int64_t(t) * p.H + i) * load_act(p.sg_vec, p.sg_type, i);
-            acc = wave_sum(acc);
+            const float acc = shared_gate_dot(p.x, p.x_type, p.sg_vec, p.sg_type, p.H, t);
             if (lane == 0) p.sg[t] = 1.f / (1.f + __expf(-acc));
         }
     }
@@ -616,10 +658,7 @@ __global__ void __launch_bounds__(kWave) k_route_tokens(const MoeParams p) {
         if (p.wts_out) p.wts_out[t * p.top_k + lane] = my_w;
     }
     if (p.shared) {
-        float acc = 0.f;
-        for (int i = lane; i < p.H; i += kWave)
-            acc += load_act(p.x, p.x_type, int64_t(t) * p.H + i) * load_act(p.sg_vec, p.sg_type, i);
-        acc = wave_sum(acc);
+        const float acc = shared_gate_dot(p.x, p.x_type, p.sg_vec, p.sg_type, p.H, t);
         if (lane == 0) p.sg[t] = 1.f / (1.f + __expf(-acc));
     }
 }
