@@ -171,3 +171,16 @@ def test_moe_layer_batched_skipzero():
                              in_features=i, row_table=torch.from_numpy(rt).cuda())
         setattr(blk.switch_mlp, name + "_proj", mod)
     _check(blk, projs, None, None, rng, T, E, H, k)
+
+
+@pytest.mark.parametrize("D,K,shared", [(4, 16384, True), (2, 65536, False), (8, 8192, True)])
+def test_moe_layer_decode_tables_beyond_lds(D, K, shared):
+    """Decode (T = 1, 2) with codebooks larger than the LDS-resident limit:
+    gate and up in separate workgroups, each with the first 128 KB of its
+    table in LDS (all of a d4 K16384 table) and the rest read from L2."""
+    print(f"moe decode big tables D={D} K={K} shared={shared}", flush=True)
+    rng = np.random.default_rng(40 + D)
+    E, H, I, k = 32, 1024, 512, 6
+    blk, projs, sh, shv = _block(rng, E, H, I, D, K, k, shared=shared)
+    for T in (1, 2):
+        _check(blk, projs, sh, shv, rng, T, E, H, k)

@@ -62,11 +62,24 @@ struct BigParams {
 // sum_g s[g] * sum_{codes i of g in the slice} <cb[c_i - base], x_i>; codes
 // outside [base, base + cnt) read the zero entry `zero` (branch-free, so the
 // gathers of a block can all be in flight together).
+// All 32 entry reads are issued before the first product (a scheduling
+// barrier keeps the compiler from interleaving them with the dot chain): at
+// one wave per SIMD nothing else hides an LDS read's latency, and 32 reads in
+// flight per lane run the random gathers near the LDS's rate.
 template <int D, int BITS, int GPB>
 __device__ __forceinline__ float block_dot_slice(const uint32_t (&w)[BITS], const h2 (&xr)[16 * D],
                                                  const float (&s)[GPB], const h2 *cb,
                                                  uint32_t base, uint32_t cnt, uint32_t zero) {
+    typedef typename EntryT<D>::type E;
     constexpr int CPG = kBlock / GPB;
+    E e[kBlock];
+#pragma unroll
+    for (int i = 0; i < kBlock; ++i) {
+        uint32_t c = block_field<BITS>(w, i) - base;               // wraps below base
+        c = c < cnt ? c : zero;
+        e[i] = reinterpret_cast<const E *>(cb)[c];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float acc = 0.f;
 #pragma unroll
     for (int g = 0; g < GPB; ++g) {
@@ -74,9 +87,7 @@ __device__ __forceinline__ float block_dot_slice(const uint32_t (&w)[BITS], cons
 #pragma unroll
         for (int q = 0; q < CPG; ++q) {
             const int i = g * CPG + q;
-            uint32_t c = block_field<BITS>(w, i) - base;           // wraps below base
-            c = c < cnt ? c : zero;
-            ga = dot_entry<D>(cb, c, &xr[i * (D / 2)], ga);
+            ga = dot_vec<D>(e[i], &xr[i * (D / 2)], ga);
         }
         acc = fmaf(s[g], ga, acc);
     }

@@ -823,33 +823,38 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     p.P = P;
     p.sg_vec = m->sh_gate_vec;
     p.sg_type = m->sh_gate_vec_type;
-    const int64_t target = 2048;
     const bool full1 = cb_in_lds(gg.D, gg.BITS), full2 = cb_in_lds(gd.D, gd.BITS);
     pl->split = !full1;
+    const size_t cb1 = full1 ? (size_t(1) << gg.BITS) * gg.D * 2 : size_t(kHybUpBytes);
+    const size_t cb2 = full2 ? (size_t(1) << gd.BITS) * gd.D * 2 : size_t(kHybDownBytes);
+    pl->smem1 = (pl->split ? size_t(kHybSplitBytes) : 2 * cb1) + size_t(gg.NB) * (kBlock * gg.D + 8) * 2;
+    pl->smem2 = ((shared && full2) ? 2 : 1) * cb2 + size_t(P) * gd.NB * (kBlock * gd.D + 8) * 2;
+    // Row steps per workgroup: about 2048 row steps per launch spread over the
+    // grid; a workgroup whose LDS leaves room for no second one on a CU gets
+    // enough steps that the grid fits the CUs in one round (each round would
+    // repeat the routing, the table copy and the first weight latency).
+    const int64_t target = 2048, ncu = big_grid(int64_t(1) << 30);
+    auto plan_steps = [&](int64_t row_steps, int64_t cols, size_t smem, int32_t *steps) {
+        int64_t st = (row_steps * cols + target - 1) / target;
+        st = st < 1 ? 1 : (st > 16 ? 16 : st);
+        if (smem > 80 * 1024)
+            while (st < 16 && ((row_steps + 4 * st - 1) / (4 * st)) * cols > ncu) ++st;
+        *steps = int32_t(st);
+    };
     {   // K1: T*P pairs x I rows (x 2 projections when split)
         const int rpw = kWave >> p.lpr1_log2;
         const int nz = pl->split ? 2 : 1;
-        const int64_t steps_total = T * P * nz * ((gg.OUT + rpw - 1) / rpw);
-        int64_t st = (steps_total + target - 1) / target;
-        st = st < 1 ? 1 : (st > 16 ? 16 : st);
-        p.steps1 = int32_t(st);
-        p.rows_per_wg1 = int32_t(4 * rpw * st);
+        plan_steps((gg.OUT + rpw - 1) / rpw, T * P * nz, pl->smem1, &p.steps1);
+        p.rows_per_wg1 = int32_t(4 * rpw * p.steps1);
         pl->grid1 = dim3(unsigned((gg.OUT + p.rows_per_wg1 - 1) / p.rows_per_wg1), unsigned(T * P),
                          unsigned(nz));
     }
     {   // K2: T tokens x H rows
         const int rpw = kWave >> p.lpr2_log2;
-        const int64_t steps_total = T * ((gd.OUT + rpw - 1) / rpw);
-        int64_t st = (steps_total + target - 1) / target;
-        st = st < 1 ? 1 : (st > 16 ? 16 : st);
-        p.steps2 = int32_t(st);
-        p.rows_per_wg2 = int32_t(4 * rpw * st);
+        plan_steps((gd.OUT + rpw - 1) / rpw, T, pl->smem2, &p.steps2);
+        p.rows_per_wg2 = int32_t(4 * rpw * p.steps2);
         pl->grid2 = dim3(unsigned((gd.OUT + p.rows_per_wg2 - 1) / p.rows_per_wg2), unsigned(T), 1);
     }
-    const size_t cb1 = full1 ? (size_t(1) << gg.BITS) * gg.D * 2 : size_t(kHybUpBytes);
-    const size_t cb2 = full2 ? (size_t(1) << gd.BITS) * gd.D * 2 : size_t(kHybDownBytes);
-    pl->smem1 = (pl->split ? size_t(kHybSplitBytes) : 2 * cb1) + size_t(gg.NB) * (kBlock * gg.D + 8) * 2;
-    pl->smem2 = ((shared && full2) ? 2 : 1) * cb2 + size_t(P) * gd.NB * (kBlock * gd.D + 8) * 2;
     // Many pairs: sort once and run each projection as a grouped matrix-core
     // GEMM (weights decoded once per tile of up to 16 pairs of an expert).
     // Batch >= 2 with tables beyond LDS: the sliced-codebook GEMV composition.
