@@ -138,7 +138,7 @@ __global__ void __launch_bounds__(kBigThreads) k_gemv_big(const BigParams p) {
 
         // every code block this lane uses for the item, before anything waits
         uint32_t w[S][BITS];
-        float sc[S][GPB];
+        uint32_t sc[S][GPB];     // raw fp16 bits: converted at use, so the S loads overlap
         bool live[S];
         const int sidx = GPB == 1 ? blk / sg.bpg : blk * GPB;
 #pragma unroll
@@ -157,12 +157,12 @@ __global__ void __launch_bounds__(kBigThreads) k_gemv_big(const BigParams p) {
                 for (int i = 0; i < BITS; ++i) w[s][i] = __builtin_nontemporal_load(src + i);
                 const uint16_t *sr = sg.scales + cr * sg.ngrp + sidx;
 #pragma unroll
-                for (int g = 0; g < GPB; ++g) sc[s][g] = h_to_f32(__builtin_nontemporal_load(sr + g));
+                for (int g = 0; g < GPB; ++g) sc[s][g] = __builtin_nontemporal_load(sr + g);
             } else {
 #pragma unroll
                 for (int i = 0; i < BITS; ++i) w[s][i] = 0u;
 #pragma unroll
-                for (int g = 0; g < GPB; ++g) sc[s][g] = 0.f;
+                for (int g = 0; g < GPB; ++g) sc[s][g] = 0u;
             }
         }
 
@@ -216,7 +216,7 @@ __global__ void __launch_bounds__(kBigThreads) k_gemv_big(const BigParams p) {
             const uint32_t cnt = uint32_t(min(SE, sg.K - pass * SE));
 #pragma unroll
             for (int s = 0; s < S; ++s)
-                if (live[s]) acc[s] += block_dot_slice<D, BITS, GPB>(w[s], xr, sc[s], cbl, base, cnt, SE);
+                if (live[s]) acc[s] += block_dot_slice<D, BITS, GPB>(w[s], xr, ScalesF32<GPB>(sc[s]).v, cbl, base, cnt, SE);
         }
 #pragma unroll
         for (int s = 0; s < S; ++s) {

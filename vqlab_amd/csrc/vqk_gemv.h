@@ -158,7 +158,7 @@ __device__ __forceinline__ float block_dot_hyb(const uint32_t (&w)[BITS], const 
 
 template <int BITS, int GPB>
 __device__ __forceinline__ void load_block(const GemvParams &p, int64_t cr, int blk, int sidx,
-                                           uint32_t (&w)[BITS], float (&s)[GPB]) {
+                                           uint32_t (&w)[BITS], uint32_t (&s)[GPB]) {
     if (cr >= 0) {
         const uint32_t *src = static_cast<const uint32_t *>(p.codes) + cr * p.row_words +
                               int64_t(blk) * BITS;
@@ -166,14 +166,26 @@ __device__ __forceinline__ void load_block(const GemvParams &p, int64_t cr, int 
         for (int i = 0; i < BITS; ++i) w[i] = __builtin_nontemporal_load(src + i);
         const uint16_t *sr = p.scales + cr * p.ngrp + sidx;
 #pragma unroll
-        for (int g = 0; g < GPB; ++g) s[g] = h_to_f32(__builtin_nontemporal_load(sr + g));
+        for (int g = 0; g < GPB; ++g) s[g] = __builtin_nontemporal_load(sr + g);
     } else {
 #pragma unroll
         for (int i = 0; i < BITS; ++i) w[i] = 0u;
 #pragma unroll
-        for (int g = 0; g < GPB; ++g) s[g] = 0.f;
+        for (int g = 0; g < GPB; ++g) s[g] = 0u;
     }
 }
+
+// Raw fp16 scale bits (as loaded) -> fp32, at their use: converting them in
+// the load helper would be the loads' first use and put a wait right behind
+// them, serialising the wave's next loads (table copy, next projection).
+template <int GPB>
+struct ScalesF32 {
+    float v[GPB];
+    __device__ __forceinline__ explicit ScalesF32(const uint32_t (&r)[GPB]) {
+#pragma unroll
+        for (int g = 0; g < GPB; ++g) v[g] = h_to_f32(uint16_t(r[g]));
+    }
+};
 
 typedef __attribute__((address_space(1))) void global_void;
 typedef __attribute__((address_space(3))) void lds_void;
@@ -337,8 +349,12 @@ __device__ __forceinline__ void stage_x(const void *x, int32_t type, int64_t bas
 // bit-casting elements of a u32x4 value miscompiled, every element read as
 // element 0.
 template <int D>
+// `src` is 16-byte aligned at every call (block strides are multiples of 16
+// bytes), which lets the reads go out as 16-byte LDS loads: half the
+// instructions of 8-byte pairs, and the padded stride keeps them free of
+// bank conflicts.
 __device__ __forceinline__ void load_xregs(const f16 *src, h2 (&xr)[16 * D]) {
-    const uint32_t *s = reinterpret_cast<const uint32_t *>(src);
+    const uint32_t *s = static_cast<const uint32_t *>(__builtin_assume_aligned(src, 16));
 #pragma unroll
     for (int j = 0; j < 16 * D; ++j) xr[j] = __builtin_bit_cast(h2, s[j]);
 }
@@ -376,7 +392,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
     };
 
     uint32_t w[BITS];
-    float s[GPB];
+    uint32_t s[GPB];
     int64_t cr = code_row(0);
     load_block<BITS, GPB>(p, cr, blk, sidx, w, s);   // in flight during staging
 
@@ -393,14 +409,15 @@ __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
 
     for (int st = 0; st < p.steps; ++st) {
         uint32_t wn[BITS];
-        float sn[GPB];
+        uint32_t sn[GPB];
         const int64_t crn = st + 1 < p.steps ? code_row(st + 1) : -1;
         load_block<BITS, GPB>(p, crn, blk, sidx, wn, sn);
         float v = 0.f;
+        const ScalesF32<GPB> fs(s);
         if constexpr (CBL) {
-            if (cr >= 0) v = block_dot<D, BITS, GPB, true>(w, xr, s, cb, kmax);
+            if (cr >= 0) v = block_dot<D, BITS, GPB, true>(w, xr, fs.v, cb, kmax);
         } else {
-            if (cr >= 0) v = block_dot_hyb<D, BITS, GPB>(w, xr, s, cb_lds, cb, kl, kmax);
+            if (cr >= 0) v = block_dot_hyb<D, BITS, GPB>(w, xr, fs.v, cb_lds, cb, kl, kmax);
         }
         v = group_sum(v, lpr);
         const int r = row_at(st);

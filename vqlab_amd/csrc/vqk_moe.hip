@@ -198,21 +198,24 @@ __device__ __forceinline__ float shared_gate_dot(const void *x, int32_t x_type, 
     return wave_sum(acc);
 }
 
+// One lane's code block and its scales' raw fp16 bits; the scales become
+// fp32 at their use (ScalesF32), so the wave's next loads (the up projection
+// after the gate, the table copy after the down weights) issue at once.
 template <int BITS, int GPB>
 __device__ __forceinline__ void moe_load(const MoeW &w, int64_t cr, int blk, int sidx, int ngrp,
-                                         uint32_t (&wd)[BITS], float (&s)[GPB]) {
+                                         uint32_t (&wd)[BITS], uint32_t (&s)[GPB]) {
     if (cr >= 0) {
         const uint32_t *src = w.codes + cr * w.row_words + int64_t(blk) * BITS;
 #pragma unroll
         for (int i = 0; i < BITS; ++i) wd[i] = __builtin_nontemporal_load(src + i);
         const uint16_t *sr = w.scales + cr * ngrp + sidx;
 #pragma unroll
-        for (int g = 0; g < GPB; ++g) s[g] = h_to_f32(__builtin_nontemporal_load(sr + g));
+        for (int g = 0; g < GPB; ++g) s[g] = __builtin_nontemporal_load(sr + g);
     } else {
 #pragma unroll
         for (int i = 0; i < BITS; ++i) wd[i] = 0u;
 #pragma unroll
-        for (int g = 0; g < GPB; ++g) s[g] = 0.f;
+        for (int g = 0; g < GPB; ++g) s[g] = 0u;
     }
 }
 
@@ -252,7 +255,7 @@ struct RouteLds {
 template <int BITS, int GPB>
 struct DownState {
     uint32_t a[BITS];
-    float s[GPB];
+    uint32_t s[GPB];     // raw fp16 bits
     int64_t cr, e;
     float wj;
 };
@@ -327,7 +330,7 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
     auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * rpw + sub; };
 
     uint32_t ag[BITS], au[BITS];
-    float sg_[GPB], su_[GPB];
+    uint32_t sg_[GPB], su_[GPB];
     int64_t crg, cru;
     {
         const int r = row_at(0);
@@ -348,7 +351,7 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
 
     for (int st = 0; st < p.steps1; ++st) {
         uint32_t ng[BITS], nu[BITS];
-        float nsg[GPB], nsu[GPB];
+        uint32_t nsg[GPB], nsu[GPB];
         int64_t ncg = -1, ncu = -1;
         if (st + 1 < p.steps1) {
             const int r = row_at(st + 1);
@@ -359,12 +362,13 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
         moe_load<BITS, GPB>(wg, ncg, blk, sidx, p.ngrp1, ng, nsg);
         moe_load<BITS, GPB>(wu, ncu, blk, sidx, p.ngrp1, nu, nsu);
         float vg = 0.f, vu = 0.f;
+        const ScalesF32<GPB> fg(sg_), fu(su_);
         if constexpr (CBL) {
-            if (crg >= 0) vg = block_dot<D, BITS, GPB, true>(ag, xr, sg_, cbg, uint32_t(wg.K - 1));
-            if (cru >= 0) vu = block_dot<D, BITS, GPB, true>(au, xr, su_, cbu, uint32_t(wu.K - 1));
+            if (crg >= 0) vg = block_dot<D, BITS, GPB, true>(ag, xr, fg.v, cbg, uint32_t(wg.K - 1));
+            if (cru >= 0) vu = block_dot<D, BITS, GPB, true>(au, xr, fu.v, cbu, uint32_t(wu.K - 1));
         } else {
-            if (crg >= 0) vg = block_dot_hyb<D, BITS, GPB>(ag, xr, sg_, cbg_lds, cbg, klg, uint32_t(wg.K - 1));
-            if (cru >= 0) vu = block_dot_hyb<D, BITS, GPB>(au, xr, su_, cbu_lds, cbu, klu, uint32_t(wu.K - 1));
+            if (crg >= 0) vg = block_dot_hyb<D, BITS, GPB>(ag, xr, fg.v, cbg_lds, cbg, klg, uint32_t(wg.K - 1));
+            if (cru >= 0) vu = block_dot_hyb<D, BITS, GPB>(au, xr, fu.v, cbu_lds, cbu, klu, uint32_t(wu.K - 1));
         }
         vg = group_sum(vg, lpr);
         vu = group_sum(vu, lpr);
@@ -455,7 +459,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_up_split(const MoeParams p) {
     };
 
     uint32_t a[BITS];
-    float sc[GPB];
+    uint32_t sc[GPB];
     int64_t cr = code_row(0);
     moe_load<BITS, GPB>(w, cr, blk, sidx, p.ngrp1, a, sc);
     h2 xr[16 * D];
@@ -465,11 +469,12 @@ __global__ void __launch_bounds__(kThreads) k_moe_up_split(const MoeParams p) {
     float *out = (proj == 0 ? p.gbuf : p.ubuf) + (int64_t(t) * p.P + j) * p.I;
     for (int st = 0; st < p.steps1; ++st) {
         uint32_t n[BITS];
-        float ns[GPB];
+        uint32_t ns[GPB];
         const int64_t crn = st + 1 < p.steps1 ? code_row(st + 1) : -1;
         moe_load<BITS, GPB>(w, crn, blk, sidx, p.ngrp1, n, ns);
         float v = 0.f;
-        if (cr >= 0) v = block_dot_hyb<D, BITS, GPB>(a, xr, sc, cb_lds, cbg, kl, uint32_t(w.K - 1));
+        const ScalesF32<GPB> fs(sc);
+        if (cr >= 0) v = block_dot_hyb<D, BITS, GPB>(a, xr, fs.v, cb_lds, cbg, kl, uint32_t(w.K - 1));
         v = group_sum(v, lpr);
         const int r = row_at(st);
         if (blk == lpr - 1 && r < p.I) out[r] = v;
@@ -596,14 +601,15 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
 
     for (int st = 0; st < p.steps2; ++st) {
         uint32_t n[BITS];
-        float ns[GPB];
+        uint32_t ns[GPB];
         const int64_t crn = st + 1 < p.steps2 ? code_row(st + 1) : -1;
         moe_load<BITS, GPB>(wd, crn, dl.blk, sidx, p.ngrp2, n, ns);
         float acc = 0.f;
+        const ScalesF32<GPB> fs(ds.s);
         if constexpr (CBL) {
-            if (ds.cr >= 0) acc = ds.wj * block_dot<D, BITS, GPB, true>(ds.a, xr, ds.s, cb, kmax);
+            if (ds.cr >= 0) acc = ds.wj * block_dot<D, BITS, GPB, true>(ds.a, xr, fs.v, cb, kmax);
         } else {
-            if (ds.cr >= 0) acc = ds.wj * block_dot_hyb<D, BITS, GPB>(ds.a, xr, ds.s, cbd_lds, cb, kl, kmax);
+            if (ds.cr >= 0) acc = ds.wj * block_dot_hyb<D, BITS, GPB>(ds.a, xr, fs.v, cbd_lds, cb, kl, kmax);
         }
         acc = group_sum(acc, dl.lpr);
         const int r = row_at(st);
