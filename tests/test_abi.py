@@ -64,6 +64,32 @@ def test_host_pack_unpack_vs_oracle(L, bits):
         vq_pack.pack(np.full((1, 1, 32), 1 << bits, np.uint32), bits)
 
 
+def test_codepack_rule_and_round_trip(L, monkeypatch):
+    """codepack.pack_codes (codepack.py:33-52) on the reference's own
+    fit-pack geometry (tests/test_fit_pack.py:22, 79-99): gate d4 K512 packs
+    to 9-bit uint32 words, up d4 K256 stays byte-aligned; a packer whose
+    output does not round-trip stops the process."""
+    from vqlab_amd import codepack, vq_pack
+    rng = np.random.default_rng(9)
+    E, I, NSUB = 2, 8, 128 // 4
+    gate = rng.integers(0, 512, (E, I, NSUB)).astype(np.uint16)
+    up = rng.integers(0, 256, (E, I, NSUB)).astype(np.uint8)
+    pg, bg = codepack.pack_codes("gate_proj", gate, 512)
+    assert bg == 9 and pg.dtype == np.uint32
+    assert np.array_equal(pg, vo.pack(gate, 9))
+    pu, bu = codepack.pack_codes("up_proj", up, 256)
+    assert bu == 0 and pu is up
+    odd = rng.integers(0, 512, (1, 2, 40)).astype(np.uint16)       # NSUB % 32 != 0
+    assert codepack.pack_codes("x", odd, 512)[1] == 0
+    assert codepack.pack_codes("x", odd, 512, pack_unaligned=True)[1] == 9
+    for k, nsub, un in ((256, 512, 0), (4096, 512, 0), (4096, 80, 0), (4096, 80, 1), (65536, 64, 0)):
+        assert codepack.pack_bits_for(k, nsub, bool(un)) == vo.pack_bits_for(k, nsub, bool(un))
+    real = vq_pack.unpack
+    monkeypatch.setattr(vq_pack, "unpack", lambda p, n, b: real(p, n, b) ^ 1)
+    with pytest.raises(SystemExit):
+        codepack.pack_codes("gate_proj", gate, 512)
+
+
 def test_host_pack_matches_reference_golden(L):
     from golden import writer_fixture as wf
     from vqlab_amd import vq_pack

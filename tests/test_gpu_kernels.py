@@ -55,6 +55,17 @@ def test_device_pack_matches_reference_golden():
         assert wf.sha16(got) == gold[m + ".codes"]["sha"], m
 
 
+def test_codepack_device_round_trip():
+    from vqlab_amd import codepack
+    rng = np.random.default_rng(19)
+    for k, bits in ((512, 9), (4096, 12), (16384, 14)):
+        print(f"codepack device K={k}", flush=True)
+        codes = rng.integers(0, k, (3, 4, 64)).astype(np.uint16)
+        packed, b = codepack.pack_codes("m", torch.from_numpy(codes.view(np.int16)).cuda(), k)
+        assert b == bits
+        assert np.array_equal(packed.cpu().numpy().view(np.uint32), vo.pack(codes, bits))
+
+
 # ----------------------------------------------------------------- dequant
 @pytest.mark.parametrize("D", [2, 4, 8])
 @pytest.mark.parametrize("K,packed", [(16, True), (256, False), (512, True), (4096, True),
