@@ -128,10 +128,13 @@ def test_routing_ties_pick_lower_ids():
     print("routing ties", flush=True)
     rng = np.random.default_rng(6)
     blk, projs, sh, shv = _block(rng, 64, 256, 128, 4, 256, 6)
-    x = torch.from_numpy(rng.standard_normal((3, 256)).astype(np.float32)).to("cuda", torch.bfloat16)
-    lg = np.round(rng.standard_normal((3, 64)) * 2) / 2           # many exact ties
+    x = torch.from_numpy(rng.standard_normal((4, 256)).astype(np.float32)).to("cuda", torch.bfloat16)
+    lg = np.round(rng.standard_normal((4, 64)) * 2) / 2           # many exact ties
     lg[1, :] = 0.0                                                  # all tied
     lg[2, 10:] = -np.inf                                            # only 10 finite
+    lg[3, :] = -1.0                                                 # -0 and +0 tie (equal floats)
+    lg[3, rng.permutation(64)[:12]] = 0.0
+    lg[3, rng.permutation(64)[:12]] = -0.0
     lgt = torch.from_numpy(lg.astype(np.float32)).cuda()
     _, ids, w = blk.fused(x, lgt, return_route=True)
     rids, rw = vo.route(lg.astype(np.float32), 6)

@@ -126,10 +126,22 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return uint32_t(__builtin_amdgcn_readlane(int(v), kWave - 1));
 }
 
-// Order-preserving map float -> uint32 (NaN maps below every number) and back.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, dpp_u<kDppQuadXor1>(v));
+    v = min(v, dpp_u<kDppQuadXor2>(v));
+    v = min(v, dpp_u<kDppRowHalfMirror>(v));
+    v = min(v, dpp_u<kDppRowMirror>(v));
+    v = min(v, dpp_u<kDppRowBcast15, 0xA>(v));
+    v = min(v, dpp_u<kDppRowBcast31, 0xC>(v));
+    return uint32_t(__builtin_amdgcn_readlane(int(v), kWave - 1));
+}
+
+// Order-preserving map float -> uint32 (NaN maps below every number, -0 to
+// the key of +0, as they compare equal) and back.
 __device__ __forceinline__ uint32_t f32_key(float f) {
-    const uint32_t b = __float_as_uint(f);
+    uint32_t b = __float_as_uint(f);
     if ((b & 0x7fffffffu) > 0x7f800000u) return 0u;          // NaN: never selected
+    if (b == 0x80000000u) b = 0u;
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 __device__ __forceinline__ float key_f32(uint32_t k) {

@@ -69,19 +69,43 @@ struct MoeParams {
 };
 
 // ------------------------------------------------------------ routing
+// Keys of one lane in descending order, equal keys by lower index: Batcher's
+// odd-even merge sort network over NS (a power of two) slots, fully unrolled.
+template <int NS>
+__device__ __forceinline__ void sort_keys_desc(uint32_t (&key)[NS], uint32_t (&idx)[NS]) {
+#pragma unroll
+    for (int p = 1; p < NS; p <<= 1)
+#pragma unroll
+        for (int k = p; k >= 1; k >>= 1)
+#pragma unroll
+            for (int j = k % p; j + k < NS; j += 2 * k)
+#pragma unroll
+                for (int i = 0; i < k && i + j + k < NS; ++i)
+                    if ((i + j) / (2 * p) == (i + j + k) / (2 * p)) {
+                        const int a = i + j, b = i + j + k;
+                        const bool sw = key[b] > key[a] || (key[b] == key[a] && idx[b] < idx[a]);
+                        const uint32_t ka = key[a], ia = idx[a];
+                        key[a] = sw ? key[b] : ka;
+                        idx[a] = sw ? idx[b] : ia;
+                        key[b] = sw ? ka : key[b];
+                        idx[b] = sw ? ia : idx[b];
+                    }
+}
+
 // Wave-level softmax + top-k of one token's logits (fp32, like the
 // reference's precise softmax), NS logits per lane (NS * 64 >= E). Every lane
 // returns the expert of pair `want` (or -1) in *e_want; lane r < k holds
 // selection r in (*my_idx, *my_w). Argmax is exact: logits become
-// order-preserving integer keys, a DPP max finds the best key and a ballot
-// per slot the lowest index holding it, so ties go to the lower expert id
-// (stable descending order). NaN logits sort below -inf and are never chosen
-// while k <= number of finite logits.
+// order-preserving integer keys, each lane sorts its own keys once, and each
+// selection is a DPP max over the lanes' head keys; the lane holding it (on a
+// tie between lanes, the one whose head has the lowest index) pops its head,
+// so ties go to the lower expert id (stable descending order). NaN logits sort
+// below -inf and are never chosen while k <= number of finite logits.
 template <int NS>
 __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int norm, int want,
                                            int *e_want, int *my_idx, float *my_w) {
     const int lane = threadIdx.x & (kWave - 1);
-    uint32_t key[NS];
+    uint32_t key[NS], idx[NS];
     float raw[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -90,11 +114,13 @@ __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int no
     }
     wait_vmem();                                         // the logits are this wave's only loads
 #pragma unroll
-    for (int s = 0; s < NS; ++s) key[s] = (s * kWave + lane) < E ? f32_key(raw[s]) : 0u;
-    uint32_t lmax = 0;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) lmax = max(lmax, key[s]);
-    const float m = key_f32(wave_max_u32(lmax));
+    for (int s = 0; s < NS; ++s) {
+        const int i = s * kWave + lane;
+        key[s] = i < E ? f32_key(raw[s]) : 0u;
+        idx[s] = uint32_t(i);
+    }
+    sort_keys_desc<NS>(key, idx);
+    const float m = key_f32(wave_max_u32(key[0]));
     float den = 1.f;
     if (!norm) {                                         // renormalised weights do not need it
         float lsum = 0.f;
@@ -107,20 +133,26 @@ __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int no
     int e_w = -1, midx = -1;
     uint32_t mykey = 0;
     for (int r = 0; r < k; ++r) {
-        uint32_t cur = 0;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) cur = max(cur, key[s]);
-        const uint32_t best = wave_max_u32(cur);
+        const uint32_t best = wave_max_u32(key[0]);
         int bi = -1;
         if (best) {
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                const uint64_t hit = __ballot(key[s] == best);
-                if (bi < 0 && hit) bi = s * kWave + (__ffsll((unsigned long long)hit) - 1);
+            const uint64_t hit = __ballot(key[0] == best);
+            int wl;
+            if ((hit & (hit - 1)) == 0) {
+                wl = __ffsll((unsigned long long)hit) - 1;
+            } else {                                     // tie between lanes: lowest index
+                const uint32_t mi = wave_min_u32(key[0] == best ? idx[0] : 0xffffffffu);
+                wl = int(mi & (kWave - 1));
             }
+            bi = __builtin_amdgcn_readlane(int(idx[0]), wl);
+            if (lane == wl) {
 #pragma unroll
-            for (int s = 0; s < NS; ++s)
-                if (s * kWave + lane == bi) key[s] = 0u;         // taken
+                for (int s = 0; s + 1 < NS; ++s) {
+                    key[s] = key[s + 1];
+                    idx[s] = idx[s + 1];
+                }
+                key[NS - 1] = 0u;
+            }
         }
         if (r == want) e_w = bi;
         if (lane == r) { midx = bi; mykey = bi >= 0 ? best : 0u; }
