@@ -367,6 +367,13 @@ def f16_to_bf16(h: np.ndarray) -> np.ndarray:
     return r.astype(np.uint16)
 
 
+def bf16_values(h: np.ndarray) -> np.ndarray:
+    """fp16 values -> the float32 values of their bfloat16 casts: the weight
+    operand of the reference's GEMM when x is bf16 (`xf @ w.T.astype(xf.dtype)`,
+    vq_dense.py:288, 294)."""
+    return (f16_to_bf16(h).astype(np.uint32) << 16).view(np.float32)
+
+
 def embed_rows(ids: np.ndarray, codes: np.ndarray, codebook: np.ndarray,
                scales: np.ndarray, group: int) -> np.ndarray:
     """Rows ids of a VQ table, decoded: fp16 [*ids.shape, IN]

@@ -3,8 +3,11 @@
 vqk_dense_gemm (_decode_matmul, vq_dense.py:262-312) and vqk_grouped_gemm
 (_gemmseg_prefill, vq_switch.py:4569-4722): outputs within rtol 2e-2 /
 atol 1e-3 of the float64 decode-then-matmul oracle with x rounded to fp16
-(the operand the matrix cores take). The device-side sort must build the
-oracle's tile metadata (tile_meta, vq_switch.py:4590-4610) exactly.
+(the operand the matrix cores take). With bf16 x and y, N > 64 and
+IN % 64 == 0 the dense GEMM is the reference's own arithmetic -- W cast to bf16, one bf16
+GEMM (vq_dense.py:288, 294) -- and the oracle rounds W the same way. The
+device-side sort must build the oracle's tile metadata (tile_meta,
+vq_switch.py:4590-4610) exactly.
 """
 import ctypes
 
@@ -53,7 +56,11 @@ def test_dense_gemm(case):
     y = VD._decode_matmul(x, codes[0], cb, sc[0], G, OUT, IN, m["pack_bits"])
     assert y.shape == (N, OUT) and y.dtype == x.dtype
     w = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], G)
-    assert_close(_np(y), vo.decode_matmul(_x16(x), w), what=f"dense gemm {case}")
+    if N > 64 and IN % 64 == 0:     # decode-then-GEMM: the reference's bf16 operands
+        ref = vo.decode_matmul(_np(x), vo.bf16_values(w))
+    else:                           # register-decode / LDS tile kernels: fp16 operands
+        ref = vo.decode_matmul(_x16(x), w)
+    assert_close(_np(y), ref, what=f"dense gemm {case}")
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.float32])

@@ -408,6 +408,10 @@ def test_f16_to_bf16_matches_torch_rounding():
     assert np.array_equal(got[~nan], ref[~nan])
     # NaN stays NaN: exponent all ones, nonzero mantissa
     assert np.all((got[nan] & 0x7F80) == 0x7F80) and np.all((got[nan] & 0x7F) != 0)
+    # the float values of those casts (the reference's bf16 GEMM operand)
+    vals = vo.bf16_values(h)
+    tv = torch.from_numpy(h.astype(np.float32)).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(vals[~nan], tv[~nan])
 
 
 def test_embed_rows_is_gather_of_full_dequant():

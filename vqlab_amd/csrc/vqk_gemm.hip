@@ -349,7 +349,12 @@ static void fill_seg(const vqk_weights *w, const Geom &g, SegParams *p) {
 int launch_hgemm(const uint16_t *A, const uint16_t *B, void *y, int32_t y_type, int64_t ldy,
                  int64_t ycol0, int64_t M, int64_t Nc, int64_t K, hipStream_t st);
 int launch_x_to_f16(const void *x, int32_t type, int64_t n, uint16_t *out, hipStream_t st);
+int lt_gemm_nt(int32_t type, const void *W, int64_t ldw, const void *X, int64_t ldx, void *Y,
+               int64_t ldy, int64_t M, int64_t N, int64_t K, void *ws, size_t ws_bytes,
+               hipStream_t st);
+int dequant_rows_bf16(const vqk_weights *w, int64_t r0, int64_t rows, uint16_t *out, hipStream_t st);
 constexpr int64_t kPanelMin = 128;              // weight rows of the smallest panel
+constexpr size_t kLtScratch = size_t(64) << 20;  // hipBLASLt scratch in the workspace
 
 static bool hgemm_fits(const Geom &g, const void *x, int64_t N) {
     return g.IN % 64 == 0 && g.IN <= INT32_MAX && g.OUT <= INT32_MAX && N <= INT32_MAX &&
@@ -357,6 +362,36 @@ static bool hgemm_fits(const Geom &g, const void *x, int64_t N) {
 }
 
 static size_t x16_bytes(const Geom &g, int64_t N) { return al256(size_t(N) * size_t(g.IN) * 2); }
+
+// fp16 or bf16 x and y of one type: the weight decoded panel by panel in that
+// type (bf16 = one RNE of the fp16 value, the reference's cast), each panel's
+// GEMM on hipBLASLt with the rest of the workspace as its scratch.
+// VQK_ENOTIMPL before any launch when the library has no algorithm.
+static int dense_lt(const vqk_weights *w, const Geom &g, const void *x, int32_t type, int64_t N,
+                    void *y, void *workspace, size_t ws_bytes, hipStream_t st) {
+    const size_t row_b = size_t(g.IN) * 2;
+    if (ws_bytes < kPanelMin * row_b)
+        return set_error(VQK_ENOSPACE, "dense GEMM workspace %zu B < %lld weight rows", ws_bytes,
+                         (long long)kPanelMin);
+    int64_t prow = int64_t(ws_bytes / row_b);
+    prow = prow >= g.OUT ? g.OUT : prow / kPanelMin * kPanelMin;
+    uint16_t *panel = static_cast<uint16_t *>(workspace);
+    const size_t used = al256(size_t(prow) * row_b);
+    uint8_t *lws = used < ws_bytes ? static_cast<uint8_t *>(workspace) + used : nullptr;
+    const size_t lwb = used < ws_bytes ? ws_bytes - used : 0;
+    for (int64_t r0 = 0; r0 < g.OUT; r0 += prow) {
+        const int64_t rows = g.OUT - r0 < prow ? g.OUT - r0 : prow;
+        int rc = type == VQK_BF16 ? dequant_rows_bf16(w, r0, rows, panel, st)
+                                  : vqk_dequant(w, r0, rows, panel, st);
+        if (rc) return rc;
+        rc = lt_gemm_nt(type, panel, g.IN, x, g.IN, static_cast<uint16_t *>(y) + r0, g.OUT, rows, N,
+                        g.IN, lws, lwb, st);
+        if (rc == VQK_ENOTIMPL && r0 > 0)
+            return set_error(VQK_EINVAL, "library GEMM refused a later panel");
+        if (rc) return rc;
+    }
+    return VQK_OK;
+}
 
 static int launch_seg(const SegParams &p, const Geom &g, dim3 grid, hipStream_t st) {
     switch (g.D) {
@@ -488,10 +523,11 @@ int vqk_dense_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes) {
     int rc = make_geom(w, &g);
     if (rc) return rc;
     if (!bytes || N < 0) return set_error(VQK_EINVAL, "bad arguments");
-    // the decode-then-GEMM path: fp16 x plus the whole fp16 weight (one panel)
+    // the decode-then-GEMM path: fp16 x plus the whole fp16 weight (one panel),
+    // plus the library GEMM's scratch (fp16 / bf16 activations)
     const bool seg = N <= kSegDenseMaxN && seg_fits_geom(g, w);
     *bytes = (!seg && N > 0 && g.IN % 64 == 0)
-                 ? x16_bytes(g, N) + size_t(g.OUT) * size_t(g.IN) * 2 : 0;
+                 ? x16_bytes(g, N) + al256(size_t(g.OUT) * size_t(g.IN) * 2) + kLtScratch : 0;
     return VQK_OK;
 }
 
@@ -520,6 +556,11 @@ int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_t 
     }
     if (hgemm_fits(g, x, N) && (workspace || ws_bytes)) {
         hipStream_t st = hipStream_t(stream);
+        if (x_type == y_type && (x_type == VQK_F16 || x_type == VQK_BF16) &&
+            (reinterpret_cast<uintptr_t>(y) & 15) == 0 && workspace) {
+            rc = dense_lt(w, g, x, x_type, N, y, workspace, ws_bytes, st);
+            if (rc != VQK_ENOTIMPL) return rc;
+        }
         const bool cvt = x_type != VQK_F16;
         const size_t xb = cvt ? x16_bytes(g, N) : 0;
         const size_t row_b = size_t(g.IN) * 2;

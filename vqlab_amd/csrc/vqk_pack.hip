@@ -80,6 +80,7 @@ struct DequantArgs {
     int64_t OUT, IN, NSUB;
     int64_t r0, rows;        // output rows: flat rows [r0, r0+rows) or ne*OUT
     uint16_t *out;
+    int bf16;                // 1: write bf16(the fp16 value), one RNE
 };
 
 // One thread per (output row, code): writes D halves with one vector store.
@@ -110,12 +111,19 @@ __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
             else c = static_cast<const uint16_t *>(a.codes)[cr * a.code_cols + j];
             if (c >= uint32_t(a.K)) c = uint32_t(a.K - 1);   // never read past the table
             const float s = h_to_f32(a.scales[cr * a.ngrp + (j * D) / a.G]);
-            const uint16_t *e = a.codebook + int64_t(c) * D;
+            // the entry as ONE vector load (D * 2 bytes): a gather per half
+            // would multiply the L2 requests that bound this kernel
+            uint16_t e[D];
+            __builtin_memcpy(e, a.codebook + int64_t(c) * D, sizeof e);
 #pragma unroll
             for (int u = 0; u < D; ++u) {
                 // a group boundary can fall inside a subvector only if G % D != 0,
                 // which validation refuses; one scale serves all D values.
                 vals[u] = f32_to_h(s * h_to_f32(e[u]));
+            }
+            if (a.bf16) {
+#pragma unroll
+                for (int u = 0; u < D; ++u) vals[u] = f32_to_bf16(h_to_f32(vals[u]));   // fp16 -> f32 exact
             }
         }
         uint16_t *dst = a.out + orow * a.IN + j * D;
@@ -142,8 +150,9 @@ static dim3 rows_grid(int64_t cols, int64_t rows) {
 }
 
 static int launch_dequant(const vqk_weights *w, const Geom &g, const uint32_t *eidx, int64_t r0,
-                          int64_t rows, uint16_t *out, hipStream_t st) {
+                          int64_t rows, uint16_t *out, hipStream_t st, int bf16 = 0) {
     DequantArgs a;
+    a.bf16 = bf16;
     a.codes = w->codes;
     a.code_cols = w->code_cols;
     a.bits = g.packed ? g.BITS : 0;
@@ -168,6 +177,15 @@ static int launch_dequant(const vqk_weights *w, const Geom &g, const uint32_t *e
         default: hipLaunchKernelGGL(k_dequant<8>, grid, dim3(256), 0, st, a); break;
     }
     return hip_status(hipGetLastError(), "dequant launch");
+}
+
+// Rows [r0, r0 + rows) of a validated module as bf16 (the reference's cast of
+// the fp16 weight to the activation dtype before its GEMM, vq_dense.py:300-306).
+int dequant_rows_bf16(const vqk_weights *w, int64_t r0, int64_t rows, uint16_t *out, hipStream_t st) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    return launch_dequant(w, g, nullptr, r0, rows, out, st, 1);
 }
 
 }  // namespace vqk
