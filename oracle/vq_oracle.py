@@ -187,21 +187,22 @@ def expert_gemv(x, eidx, codes, codebook, scales, group, xkrep=1,
         out = codes.shape[1]
     else:
         out = row_table.shape[1]
-    y = np.zeros((n_pairs, out), np.float64 if acc == "f64" else np.float32)
-    cache = {}
+    dt = np.float64 if acc == "f64" else np.float32
+    y = np.zeros((n_pairs, out), dt)
+    cache = {}                      # expert -> its dequantized fp16 weight, widened once
     for n in range(n_pairs):
         e = int(eidx[n])
         if e not in cache:
             if row_table is None:
-                cache[e] = dequant(codes[e], codebook, scales[e], group)
+                w = dequant(codes[e], codebook, scales[e], group)
             else:
                 rt = np.asarray(row_table)[e]
                 live = rt >= 0
                 w = np.zeros((out, codes.shape[-1] * codebook.shape[1]), np.float16)
                 if live.any():
                     w[live] = dequant(codes[rt[live]], codebook, scales[rt[live]], group)
-                cache[e] = w
-        y[n] = decode_matmul(x[n // xkrep][None, :], cache[e], acc)[0]
+            cache[e] = w.astype(dt)
+        y[n] = x[n // xkrep].astype(dt) @ cache[e].T
     return y
 
 

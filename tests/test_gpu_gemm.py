@@ -173,6 +173,58 @@ def test_grouped_gemm_shapes(shape):
     assert_close(_np(y), _np(yg), rtol=2e-2, atol=2e-3, what="grouped vs gemv")
 
 
+@pytest.mark.parametrize("shape", [
+    # (T, k, E, OUT, IN, D, K): tables past the LDS-resident part (their
+    # other entries gathered from L2), fp32 output as the MoE layer uses it
+    (64, 10, 40, 1024, 4096, 8, 16384),
+    (16, 10, 48, 4096, 1024, 8, 16384),
+    (16, 10, 64, 4096, 512, 8, 16384),        # half a superstep per row
+    (24, 6, 20, 4000, 1024, 8, 32768),        # OUT not a multiple of 128
+    (32, 8, 24, 2560, 1024, 4, 32768),
+    (32, 8, 24, 2048, 512, 2, 65536),
+])
+def test_grouped_gemm_fp32_out_large_tables(shape):
+    """fp32 output with a table beyond LDS, against the oracle; the bf16
+    output of the same call agrees."""
+    from vqlab_amd import vq_switch as VS
+    T, k, E, OUT, IN, D, K = shape
+    print(f"grouped gemm fp32 out {shape}", flush=True)
+    rng = np.random.default_rng(sum(shape) + 7)
+    m = make_module(rng, E, OUT, IN, D, K)
+    codes, cb, sc = to_device(m)
+    ids = _routes(rng, T, k, E).reshape(-1)
+    x = _x(rng, T, IN)
+    e = torch.from_numpy(ids.astype(np.int32)).cuda()
+    y = VS._gemmseg(x, e, codes, cb, sc, m["pack_bits"], IN, k, out_dtype=torch.float32)
+    assert y.dtype == torch.float32 and y.shape == (T * k, OUT)
+    ref = vo.expert_gemv(_x16(x), ids, m["codes"], m["codebook"], m["scales"], 64, xkrep=k)
+    assert_close(_np(y), ref, what=f"fp32 out {shape}")
+    yb = VS._gemmseg(x, e, codes, cb, sc, m["pack_bits"], IN, k)
+    assert_close(_np(yb), _np(y), rtol=2e-2, atol=2e-3, what="bf16 vs fp32 out")
+
+
+def test_grouped_gemm_fp32_out_skipzero():
+    """fp32 output over compact skipzero rows: dead rows are exact zeros."""
+    from vqlab_amd import vq_switch as VS
+    print("grouped gemm fp32 out skipzero", flush=True)
+    rng = np.random.default_rng(29)
+    E, OUT, IN, T, k = 32, 2048, 1024, 16, 10
+    m = make_module(rng, E, OUT, IN, 8, 16384, dead_frac=0.2)
+    codes, cb, sc = to_device(m)
+    sz, rt = skipzero(m)
+    zc = torch.from_numpy(sz["sz_codes"].view(np.int32)).cuda()
+    zs = torch.from_numpy(sz["sz_scales"]).cuda()
+    rtd = torch.from_numpy(rt).cuda()
+    ids = _routes(rng, T, k, E).reshape(-1)
+    x = _x(rng, T, IN)
+    e = torch.from_numpy(ids.astype(np.int32)).cuda()
+    yc = VS._gemmseg(x, e, zc, cb, zs, 14, IN, k, rtd, out_dtype=torch.float32)
+    dead = rt[ids] < 0
+    assert dead.any() and (_np(yc)[dead] == 0).all()
+    ref = vo.expert_gemv(_x16(x), ids, m["codes"], m["codebook"], m["scales"], 64, xkrep=k)
+    assert_close(_np(yc), ref, what="fp32 out skipzero")
+
+
 def test_grouped_gemm_skipzero_mtp_verify():
     """The c4 case: MTP verify on the c3 layer format, 20 % of rows dead,
     stored compact with a row table; dead rows give exact zeros."""
