@@ -1,11 +1,17 @@
 // The plain GEMM of the dense decode-then-matmul path (after the bit-exact
 // weight decode), on hipBLASLt: y[N, M] = x[N, K] . W[M, K]^T in fp16 or bf16
 // with fp32 accumulation, the reference's `xf @ w.T.astype(xf.dtype)`
-// (vq_dense.py:288, 294). One hipBLASLt handle per device and one plan
-// (descriptors + the heuristic's first algorithm whose scratch fits) per
+// (vq_dense.py:288, 294). One hipBLASLt handle per device and one plan per
 // shape are created on first use and kept for the process; the caller's
-// workspace is the only device memory a call uses.
+// workspace is the only device memory a call uses. The plan's algorithm is
+// the fastest of the heuristic's first candidates whose scratch fits, timed
+// on that first call with the caller's own buffers (the heuristic's first
+// pick ran 35 % slower than its second on a config-5 linear); the timing
+// synchronises the stream once per shape, and is skipped (first pick) while
+// the stream is being captured into a graph or with VQK_GEMM_TUNE=0.
 #include <hipblaslt/hipblaslt.h>
+
+#include <stdlib.h>
 
 #include <mutex>
 #include <vector>
@@ -30,7 +36,43 @@ std::mutex g_mu;
 hipblasLtHandle_t g_handle[64];
 std::vector<LtPlan> g_plans;
 
-bool make_plan(hipblasLtHandle_t h, LtPlan *p) {
+struct LtCall {             // the first call's operands, used to time candidates
+    const void *W, *X;
+    void *Y, *ws;
+    hipStream_t st;
+};
+
+bool tuning_allowed(hipStream_t st) {
+    const char *v = getenv("VQK_GEMM_TUNE");
+    if (v && v[0] == '0') return false;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return false;
+    return cs == hipStreamCaptureStatusNone;
+}
+
+// Average time of `algo` over a few runs on the caller's stream, or a
+// negative value when it fails.
+float time_algo(hipblasLtHandle_t h, const LtPlan &p, const hipblasLtMatmulAlgo_t &algo,
+                const LtCall &c) {
+    const float alpha = 1.f, beta = 0.f;
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess) return -1.f;
+    if (hipEventCreate(&e1) != hipSuccess) { hipEventDestroy(e0); return -1.f; }
+    float ms = -1.f;
+    bool ok = hipblasLtMatmul(h, p.md, &alpha, c.W, p.lw, c.X, p.lx, &beta, c.Y, p.ly, c.Y, p.ly,
+                              &algo, p.ws ? c.ws : nullptr, p.ws, c.st) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipEventRecord(e0, c.st) == hipSuccess;
+    for (int i = 0; ok && i < 3; ++i)
+        ok = hipblasLtMatmul(h, p.md, &alpha, c.W, p.lw, c.X, p.lx, &beta, c.Y, p.ly, c.Y, p.ly,
+                             &algo, p.ws ? c.ws : nullptr, p.ws, c.st) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipEventRecord(e1, c.st) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+         hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return ok ? ms : -1.f;
+}
+
+bool make_plan(hipblasLtHandle_t h, LtPlan *p, const LtCall &c) {
     const hipDataType dt = p->type == VQK_BF16 ? HIP_R_16BF : HIP_R_16F;
     p->ok = false;
     if (hipblasLtMatmulDescCreate(&p->md, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
@@ -54,13 +96,24 @@ bool make_plan(hipblasLtHandle_t h, LtPlan *p) {
                                                               pref, 8, res, &n);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (s != HIPBLAS_STATUS_SUCCESS) return false;
-    for (int i = 0; i < n; ++i)            // the heuristic's order; first that fits the scratch
-        if (res[i].workspaceSize <= p->ws) {
+    const bool tune = tuning_allowed(c.st);
+    float best = -1.f;
+    for (int i = 0, tried = 0; i < n && tried < 4; ++i) {   // the heuristic's order
+        if (res[i].workspaceSize > p->ws) continue;
+        if (!tune) {
             p->algo = res[i].algo;
             p->ok = true;
             return true;
         }
-    return false;
+        ++tried;
+        const float ms = time_algo(h, *p, res[i].algo, c);
+        if (ms >= 0.f && (best < 0.f || ms < best)) {
+            best = ms;
+            p->algo = res[i].algo;
+            p->ok = true;
+        }
+    }
+    return p->ok;
 }
 
 }  // namespace
@@ -95,7 +148,7 @@ int lt_gemm_nt(int32_t type, const void *W, int64_t ldw, const void *X, int64_t 
             LtPlan q{};
             q.dev = dev; q.type = type; q.m = M; q.n = N; q.k = K;
             q.ldw = ldw; q.ldx = ldx; q.ldy = ldy; q.ws = wsc;
-            make_plan(h, &q);
+            make_plan(h, &q, LtCall{W, X, Y, ws, st});
             g_plans.push_back(q);
             found = &g_plans.back();
         }
