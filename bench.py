@@ -1,6 +1,6 @@
 """Benchmark of the VQ MoE decode layer on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c3b4|c4|c4t16|c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1|c2|c3|c3b4|c4|c4t16|c5]
 
 Default workload: a Qwen3.6-35B-A3B-shaped MoE
 decode layer -- hidden 2048, 256 experts of intermediate 512, top-8 softmax
@@ -29,6 +29,12 @@ stored compact (skipzero row table); the block runs its composed path
 T*k pairs: vqk_grouped_gemm above 512 pairs, the fused GEMV below).
 value = packed GB/s of the live rows of the touched experts.
 
+--workload c1 (the reference's CPU-runnable case): one
+dense VQ GEMV per call (W 4096x4096, d=2, K=256, uint8 codes, x [1, 4096]
+bf16) over 48 distinct weights (403 MB) so each call streams from HBM; value
+= packed GB/s of codes + scales; cpu_baseline: the numpy oracle of the same
+GEMV, single-threaded.
+
 --workload c5: dense VQ prefill, x [2048, 5120]
 through VQLinear 5120->17408 then 17408->5120 (d8, K=65536 uint16 codes);
 value = TFLOP/s of the two GEMMs, roofline against the fp16 MFMA peak.
@@ -47,6 +53,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 
 WORKLOADS = {
+    # the reference's CPU-runnable case, on the GPU: one dense VQ GEMV per call
+    "c1": dict(OUT=4096, IN=4096, d=2, K=256, G=64, layers=48, kind="dense_gemv",
+               desc="Single dense VQ linear, decode GEMV: W 4096x4096, d=2, K=256, uint8 codes, "
+                    "x [1, 4096] (BASELINE configs[0])"),
     # name: (H, E, I, top_k, shared, d, K, bits, T, layers)
     "c2": dict(H=2048, E=256, I=512, k=8, shared=False, d=4, K=4096, bits=12, T=1, layers=8,
                desc="Qwen3.6-35B-A3B-shaped MoE decode layer (BASELINE configs[1])"),
@@ -324,6 +334,93 @@ def cpu_prefill_baseline(w, budget_s=10.0):
                       f"numpy oracle, 1 thread"}
 
 
+def cpu_gemv_baseline(w, budget_s=10.0):
+    """Numpy oracle of the dense GEMV (fp16 dequant + float64 matvec) on the
+    full 4096 x 4096 weight, single-threaded, repeated for ~budget_s."""
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:
+        threadpool_limits = None
+    from oracle import vq_oracle as vo
+    rng = np.random.default_rng(11)
+    OUT, IN, d, K, G = w["OUT"], w["IN"], w["d"], w["K"], w["G"]
+    codes = rng.integers(0, K, (OUT, IN // d)).astype(np.uint8)
+    cb = (rng.standard_normal((K, d)) * 0.02).astype(np.float16)
+    sc = rng.uniform(0.5, 1.5, (OUT, IN // G)).astype(np.float16)
+    x = rng.standard_normal((1, IN)).astype(np.float32)
+    ctx = threadpool_limits(1) if threadpool_limits else None
+    n, t0 = 0, time.perf_counter()
+    try:
+        if ctx:
+            ctx.__enter__()
+        while n < 2 or (time.perf_counter() - t0 < budget_s and n < 200):
+            vo.decode_matmul(x, vo.dequant(codes, cb, sc, G))
+            n += 1
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    dt = (time.perf_counter() - t0) / n
+    packed = OUT * (IN // d) + OUT * (IN // G) * 2
+    return {"value": round(packed / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "us_per_call": round(dt * 1e6, 1),
+            "sample": f"{n} calls of the full 4096x4096 GEMV (numpy oracle: fp16 dequant + "
+                      f"float64 matvec), 1 thread"}
+
+
+def run_dense_gemv(torch, dev, a, w):
+    """c1: one dense VQ GEMV per call (VQLinear, N = 1 -> vqk_dense_gemv), over
+    `layers` distinct weights (403 MB, past the 256 MB MALL) so every call
+    streams its weight from HBM."""
+    from vqlab_amd.vq_dense import VQLinear
+    from oracle import vq_oracle as vo
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    OUT, IN, d, K, G, L = (w[n] for n in ("OUT", "IN", "d", "K", "G", "layers"))
+    log(f"building {L} linears of {w['desc']}")
+    lins, xs = [], []
+    for _ in range(L):
+        codes = torch.randint(0, K, (OUT, IN // d), dtype=torch.int32, device=dev,
+                              generator=g).to(torch.uint8)
+        cb = (torch.randn((K, d), device=dev, generator=g) * 0.02).to(torch.float16)
+        sc = (torch.rand((OUT, IN // G), device=dev, generator=g) + 0.5).to(torch.float16)
+        lins.append(VQLinear(codes, cb, sc, group_size=G, pack_bits=0))
+        xs.append(torch.randn((1, IN), device=dev, generator=g).to(torch.bfloat16))
+    ys = [None] * L
+
+    def step(s):
+        for l in range(L):
+            ys[l] = lins[l](xs[l])
+
+    wall, ev_ms = _graph_time(torch, step, a.warmup, a.steps, dev)
+    # sanity: the last call of linear 0 is the oracle's (rtol 2e-2 / atol 1e-3)
+    l0 = lins[0]
+    ref = vo.decode_matmul(xs[0].float().cpu().numpy(),
+                           vo.dequant(l0.codes.cpu().numpy(), l0.codebook.cpu().numpy(),
+                                      l0.vq_scales.cpu().numpy(), G))
+    got = ys[0].float().cpu().numpy()
+    if not np.allclose(got, ref, rtol=2e-2, atol=1e-3):
+        raise SystemExit("c1: GEMV output differs from the oracle")
+    calls = a.steps * L
+    packed = OUT * (IN // d) + OUT * (IN // G) * 2                 # codes + scales
+    alg = packed + K * d * 2 + IN * 2 + OUT * 2                     # + codebook, x, y
+    us_call = ev_ms * 1e3 / calls
+    cpu = None if a.no_cpu else cpu_gemv_baseline(w)
+    return {
+        "metric": "packed-weight GB/s (% of HBM peak) of the dense VQ decode GEMV",
+        "value": round(packed * calls / wall / 1e9, 2), "unit": "GB/s", "dtype": "fp16",
+        "config": {"workload": w["desc"], "out": OUT, "in": IN, "d": d, "K": K,
+                   "index_bits": 8, "group": G, "batch": 1, "io_dtype": "bf16",
+                   "weights_rotated": L},
+        "us_per_call": round(us_call, 3),
+        "roofline": {"bound": "hbm", "achieved": round(alg / (us_call * 1e-6) / 1e9, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(alg / (us_call * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "k_gemv_fast<2, 8, 1> (vqk_dense_gemv)",
+                     "alg_bytes_per_call": alg, "us_per_call_events": round(us_call, 3)},
+        "cpu_baseline": cpu,
+    }, wall, a.steps
+
+
 def run_prefill(torch, dev, a, w):
     """c5: dense VQ prefill, two linears through VQLinear (vqk_dense_gemm)."""
     from vqlab_amd.vq_dense import VQLinear
@@ -386,8 +483,8 @@ def main():
     w = WORKLOADS[a.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if w.get("kind") in ("mtp", "prefill"):
-        fn = run_mtp if w["kind"] == "mtp" else run_prefill
+    if w.get("kind") in ("mtp", "prefill", "dense_gemv"):
+        fn = {"mtp": run_mtp, "prefill": run_prefill, "dense_gemv": run_dense_gemv}[w["kind"]]
         body, wall, _ = fn(torch, dev, a, w)
         out = {"metric": body.pop("metric"), "value": body.pop("value"), "unit": body.pop("unit"),
                "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
