@@ -84,14 +84,14 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def measured_traffic(name):
-    """HBM bytes per call from the committed counter profile of this workload
-    (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+def measured_traffic(name, key="traffic_bytes_per_call"):
+    """HBM bytes per call (or per step) from the committed counter profile of
+    this workload (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
     path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_call:"):
+                if line.startswith(key + ":"):
                     return int(line.split(":", 1)[1])
     except OSError:
         pass
@@ -292,7 +292,10 @@ def run_mtp(torch, dev, a, w):
         "us_per_call": round(wall * 1e6 / calls, 3),
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": (measured_traffic(f"mtp_verify_{a.workload}_traffic.md")
+                                 if a.mtp_path == "fused" else None),
+                     "traffic_source": "profiles/mtp_verify_<workload>_traffic.md",
                      "kernel": "k_seg_mfma (grouped gate/up/down) + routing / sort / combine",
                      "path": a.mtp_path,
                      "alg_bytes_per_call": int(alg_per_call),
@@ -415,7 +418,9 @@ def run_dense_gemv(torch, dev, a, w):
         "roofline": {"bound": "hbm", "achieved": round(alg / (us_call * 1e-6) / 1e9, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(alg / (us_call * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "k_gemv_fast<2, 8, 1> (vqk_dense_gemv)",
+                     "traffic": measured_traffic("dense_gemv_c1_traffic.md"),
+                     "traffic_source": "profiles/dense_gemv_c1_traffic.md",
+                     "kernel": "k_gemv_fast<2, 8, 1> (vqk_dense_gemv)",
                      "alg_bytes_per_call": alg, "us_per_call_events": round(us_call, 3)},
         "cpu_baseline": cpu,
     }, wall, a.steps
@@ -456,7 +461,10 @@ def run_prefill(torch, dev, a, w):
         "us_per_step_events": round(ev_ms * 1e3 / a.steps, 2),
         "roofline": {"bound": "mfma", "achieved": round(ev_tfs, 2), "peak": MFMA_F16_PEAK_TFS,
                      "unit": "TFLOP/s", "frac": round(ev_tfs / MFMA_F16_PEAK_TFS, 4),
-                     "traffic": None, "kernel": "vqk_dense_gemm (both linears)",
+                     "traffic": measured_traffic("dense_prefill_c5_traffic.md",
+                                                 "traffic_bytes_per_step"),
+                     "traffic_source": "profiles/dense_prefill_c5_traffic.md (per step)",
+                     "kernel": "vqk_dense_gemm (both linears)",
                      "flop_per_step": flop},
         "cpu_baseline": cpu,
     }, wall, a.steps
