@@ -264,15 +264,18 @@ __device__ __forceinline__ int64_t moe_row(const MoeW &w, int64_t e, int OUT, in
 // rest from L2: fewer L2 requests per code, the rate that bounds these kernels.
 constexpr int kHybUpBytes = 64 * 1024;
 constexpr int kHybDownBytes = 112 * 1024;
+// Larger LDS parts when the workgroup's activations leave room (the host
+// checks): every entry moved into LDS is an L2 request per code saved.
+constexpr int kHybDownWideBytes = 136 * 1024;
 
 // Entries of one gate/up table held in LDS, and of the routed down table.
 template <int D, int BITS>
 __host__ __device__ constexpr int up_cbn() {
     return cb_in_lds(D, BITS) ? (1 << BITS) : kHybUpBytes / (2 * D);
 }
-template <int D, int BITS>
+template <int D, int BITS, bool W = false>
 __host__ __device__ constexpr int down_cbn() {
-    return cb_in_lds(D, BITS) ? (1 << BITS) : kHybDownBytes / (2 * D);
+    return cb_in_lds(D, BITS) ? (1 << BITS) : (W ? kHybDownWideBytes : kHybDownBytes) / (2 * D);
 }
 
 // Routing of the workgroup's token as wave 0 computed it (LDS).
@@ -432,10 +435,11 @@ __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
 // bounds these tables. The rows go out as fp32; K2 builds silu(g) * u from
 // them as it stages its input.
 constexpr int kHybSplitBytes = 128 * 1024;
+constexpr int kHybSplitWideBytes = 150 * 1024;   // when x leaves room (the host checks)
 
-template <int D, int BITS, int GPB>
+template <int D, int BITS, int GPB, bool W = false>
 __global__ void __launch_bounds__(kThreads) k_moe_up_split(const MoeParams p) {
-    constexpr int CBN = kHybSplitBytes / (2 * D);
+    constexpr int CBN = (W ? kHybSplitWideBytes : kHybSplitBytes) / (2 * D);
     constexpr int XH = kBlock * D, XS = XH + 8;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ RouteLds rl;
@@ -574,11 +578,11 @@ __device__ __forceinline__ void down_stage_cb(const MoeParams &p, uint8_t *smem)
 // The token's P SwiGLU rows (fp16) -> LDS at the padded block stride, then
 // the down projection of the workgroup's rows, scaled per pair by its router
 // weight and combined over the wave (the DPP row reduction is the sum).
-template <int D, int BITS, int GPB>
+template <int D, int BITS, int GPB, bool W = false>
 __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint8_t *smem,
                                          const DownLane &dl, DownState<BITS, GPB> &ds) {
     constexpr bool CBL = cb_in_lds(D, BITS);
-    constexpr int CBN = down_cbn<D, BITS>();
+    constexpr int CBN = down_cbn<D, BITS, W>();
     constexpr int XH = kBlock * D, XS = XH + 8;
     h2 *cbd_lds = reinterpret_cast<h2 *>(smem);
     h2 *cbs_lds = reinterpret_cast<h2 *>(smem + CBN * D * 2);
@@ -654,9 +658,9 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
     }
 }
 
-template <int D, int BITS, int GPB>
+template <int D, int BITS, int GPB, bool W = false>
 __global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
-    constexpr int CBN = down_cbn<D, BITS>();
+    constexpr int CBN = down_cbn<D, BITS, W>();
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = int(blockIdx.y);
     const DownLane dl(p);
@@ -674,7 +678,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
     down_prep<BITS, GPB>(p, int(blockIdx.x), t, dl, [&](int) { return id; },
                          [&](int) { return wt; }, ds);
     down_stage_cb<D, CBN, cb_in_lds(D, BITS)>(p, smem);
-    down_run<D, BITS, GPB>(p, int(blockIdx.x), t, smem, dl, ds);
+    down_run<D, BITS, GPB, W>(p, int(blockIdx.x), t, smem, dl, ds);
 }
 
 // ------------------------------------------------ codebooks beyond LDS
@@ -782,6 +786,7 @@ struct MoePlan {
     dim3 grid1, grid2;
     int path;                 // MoePath
     bool split;               // fused path, tables beyond LDS: one projection per K1 workgroup
+    bool wide1, wide2;        // the larger LDS parts of a partly staged table fit
 };
 
 static int lg2(int64_t v) {
@@ -865,8 +870,15 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     pl->split = !full1;
     const size_t cb1 = full1 ? (size_t(1) << gg.BITS) * gg.D * 2 : size_t(kHybUpBytes);
     const size_t cb2 = full2 ? (size_t(1) << gd.BITS) * gd.D * 2 : size_t(kHybDownBytes);
-    pl->smem1 = (pl->split ? size_t(kHybSplitBytes) : 2 * cb1) + size_t(gg.NB) * (kBlock * gg.D + 8) * 2;
-    pl->smem2 = ((shared && full2) ? 2 : 1) * cb2 + size_t(P) * gd.NB * (kBlock * gd.D + 8) * 2;
+    const size_t xs1 = size_t(gg.NB) * (kBlock * gg.D + 8) * 2;
+    const size_t xs2 = size_t(P) * gd.NB * (kBlock * gd.D + 8) * 2;
+    // LDS a workgroup may take, kept clear of the 160 KB by the static routing
+    // block (and slack for alignment)
+    const size_t lds_room = 160 * 1024 - sizeof(RouteLds) - 256;
+    pl->wide1 = pl->split && gg.K * gg.D * 2 > kHybSplitBytes && kHybSplitWideBytes + xs1 <= lds_room;
+    pl->wide2 = !full2 && gd.K * gd.D * 2 > kHybDownBytes && kHybDownWideBytes + xs2 <= lds_room;
+    pl->smem1 = (pl->split ? size_t(pl->wide1 ? kHybSplitWideBytes : kHybSplitBytes) : 2 * cb1) + xs1;
+    pl->smem2 = ((shared && full2) ? 2 : 1) * (pl->wide2 ? size_t(kHybDownWideBytes) : cb2) + xs2;
     // Row steps per workgroup: about 2048 row steps per launch spread over the
     // grid; a workgroup whose LDS leaves room for no second one on a CU gets
     // enough steps that the grid fits the CUs in one round (each round would
@@ -925,24 +937,36 @@ template <int D, int BITS, int GPB>
 static int go_up(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
     return launch_with_lds<k_moe_up<D, BITS, GPB>>(grid, dim3(kThreads), smem, st, p);
 }
-template <int D, int BITS, int GPB>
+template <int D, int BITS, int GPB, bool W>
 static int go_up_split(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
-    return launch_with_lds<k_moe_up_split<D, BITS, GPB>>(grid, dim3(kThreads), smem, st, p);
+    return launch_with_lds<k_moe_up_split<D, BITS, GPB, W>>(grid, dim3(kThreads), smem, st, p);
 }
 // Split gate/up kernel: only the widths whose table exceeds the LDS-resident
 // limit (d2 15-16 bits, d4 14-16, d8 13-16).
 #define VQK_SPLIT_CASE(D, B, G) \
-    if (d == D && bits == B && gpb == G) return go_up_split<D, B, G>(p, grid, smem, st);
-static int launch_moe_up_split(const MoeParams &p, int d, int bits, int gpb, dim3 grid, size_t smem,
-                               hipStream_t st) {
+    if (d == D && bits == B && gpb == G)                                                   \
+        return wide ? go_up_split<D, B, G, true>(p, grid, smem, st)                          \
+                    : go_up_split<D, B, G, false>(p, grid, smem, st);
+static int launch_moe_up_split(const MoeParams &p, int d, int bits, int gpb, bool wide, dim3 grid,
+                               size_t smem, hipStream_t st) {
     VQK_SPLIT_CASE(2, 15, 1) VQK_SPLIT_CASE(2, 16, 1)
     VQK_SPLIT_CASE(4, 14, 2) VQK_SPLIT_CASE(4, 15, 2) VQK_SPLIT_CASE(4, 16, 2)
     VQK_SPLIT_CASE(8, 13, 4) VQK_SPLIT_CASE(8, 14, 4) VQK_SPLIT_CASE(8, 15, 4) VQK_SPLIT_CASE(8, 16, 4)
     return set_error(VQK_ENOTIMPL, "fused layer: no split gate/up kernel for d=%d bits=%d", d, bits);
 }
-template <int D, int BITS, int GPB>
+template <int D, int BITS, int GPB, bool W = false>
 static int go_down(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
-    return launch_with_lds<k_moe_down<D, BITS, GPB>>(grid, dim3(kThreads), smem, st, p);
+    return launch_with_lds<k_moe_down<D, BITS, GPB, W>>(grid, dim3(kThreads), smem, st, p);
+}
+// Down kernel with the larger LDS part: the widths whose table is beyond LDS.
+#define VQK_DNW_CASE(D, B, G) \
+    if (d == D && bits == B && gpb == G) return go_down<D, B, G, true>(p, grid, smem, st);
+static int launch_moe_down_wide(const MoeParams &p, int d, int bits, int gpb, dim3 grid, size_t smem,
+                                hipStream_t st) {
+    VQK_DNW_CASE(2, 15, 1) VQK_DNW_CASE(2, 16, 1)
+    VQK_DNW_CASE(4, 14, 2) VQK_DNW_CASE(4, 15, 2) VQK_DNW_CASE(4, 16, 2)
+    VQK_DNW_CASE(8, 13, 4) VQK_DNW_CASE(8, 14, 4) VQK_DNW_CASE(8, 15, 4) VQK_DNW_CASE(8, 16, 4)
+    return set_error(VQK_ENOTIMPL, "fused layer: no wide down kernel for d=%d bits=%d", d, bits);
 }
 // Instances: every width for d in {2, 4, 8}, scale groups of 64 weights.
 #define VQK_MOE_BITS(X, D, G) \
@@ -1132,9 +1156,10 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, i
         return launch_moe_grouped(m, pl, ws, st);
     }
     if (pl.path == kMoeBig) return launch_moe_big(m, pl, ws, st);
-    rc = split ? launch_moe_up_split(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.grid1, pl.smem1, st)
+    rc = split ? launch_moe_up_split(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.wide1, pl.grid1, pl.smem1, st)
                : launch_moe_up(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.grid1, pl.smem1, st);
     if (rc) return rc;
+    if (pl.wide2) return launch_moe_down_wide(p, pl.g2.D, pl.g2.BITS, pl.g2.gpb, pl.grid2, pl.smem2, st);
     return launch_moe_down(p, pl.g2.D, pl.g2.BITS, pl.g2.gpb, pl.grid2, pl.smem2, st);
 }
 
