@@ -455,7 +455,7 @@ def run_prefill(torch, dev, a, w):
     cpu = None if a.no_cpu else cpu_prefill_baseline(w)
     return {
         "metric": "TFLOP/s (% of fp16 MFMA peak) of the dense VQ prefill GEMMs",
-        "value": round(tfs, 2), "unit": "TFLOP/s", "dtype": "fp16",
+        "value": round(tfs, 2), "unit": "TFLOP/s", "dtype": "bf16",   # bf16 GEMM, fp32 accumulate
         "config": {"workload": w["desc"], "tokens": N, "hidden": H, "ffn": F, "d": d, "K": K,
                    "index_bits": 16, "group": 64, "io_dtype": "bf16"},
         "us_per_step_events": round(ev_ms * 1e3 / a.steps, 2),

@@ -8,9 +8,11 @@
 // on that first call with the caller's own buffers (the heuristic's first
 // pick ran 35 % slower than its second on a config-5 linear); the timing
 // synchronises the stream once per shape, and is skipped (first pick) while
-// the stream is being captured into a graph or with VQK_GEMM_TUNE=0.
+// the stream is being captured into a graph or with VQK_GEMM_TUNE=0
+// (VQK_GEMM_VERBOSE=1 prints each candidate's time to stderr).
 #include <hipblaslt/hipblaslt.h>
 
+#include <stdio.h>
 #include <stdlib.h>
 
 #include <mutex>
@@ -90,15 +92,17 @@ bool make_plan(hipblasLtHandle_t h, LtPlan *p, const LtCall &c) {
     uint64_t wsb = p->ws;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
                                           sizeof wsb);
-    hipblasLtMatmulHeuristicResult_t res[8];
+    hipblasLtMatmulHeuristicResult_t res[16];
     int n = 0;
     const hipblasStatus_t s = hipblasLtMatmulAlgoGetHeuristic(h, p->md, p->lw, p->lx, p->ly, p->ly,
-                                                              pref, 8, res, &n);
+                                                              pref, 16, res, &n);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (s != HIPBLAS_STATUS_SUCCESS) return false;
     const bool tune = tuning_allowed(c.st);
+    const char *vv = getenv("VQK_GEMM_VERBOSE");   // print each candidate's time
+    const bool verbose = vv && vv[0] == '1';
     float best = -1.f;
-    for (int i = 0, tried = 0; i < n && tried < 4; ++i) {   // the heuristic's order
+    for (int i = 0, tried = 0; i < n && tried < 8; ++i) {   // the heuristic's order
         if (res[i].workspaceSize > p->ws) continue;
         if (!tune) {
             p->algo = res[i].algo;
@@ -107,6 +111,10 @@ bool make_plan(hipblasLtHandle_t h, LtPlan *p, const LtCall &c) {
         }
         ++tried;
         const float ms = time_algo(h, *p, res[i].algo, c);
+        if (verbose)
+            fprintf(stderr, "vqk gemm M %lld N %lld K %lld: candidate %d (scratch %zu B) %.4f ms\n",
+                    (long long)p->m, (long long)p->n, (long long)p->k, i,
+                    size_t(res[i].workspaceSize), ms);
         if (ms >= 0.f && (best < 0.f || ms < best)) {
             best = ms;
             p->algo = res[i].algo;
