@@ -182,6 +182,10 @@ def test_grouped_gemm_shapes(shape):
     (24, 6, 20, 4000, 1024, 8, 32768),        # OUT not a multiple of 128
     (32, 8, 24, 2560, 1024, 4, 32768),
     (32, 8, 24, 2048, 512, 2, 65536),
+    # <= 2 pairs per expert on average: d8 tables take 4-row tiles
+    (8, 10, 64, 1024, 4096, 8, 16384),
+    (12, 6, 40, 1000, 512, 8, 32768),
+    (8, 8, 40, 512, 1024, 8, 65536),
 ])
 def test_grouped_gemm_fp32_out_large_tables(shape):
     """fp32 output with a table beyond LDS, against the oracle; the bf16
@@ -278,9 +282,10 @@ def test_grouped_gemm_sort_builds_oracle_tiles():
     wb = work.cpu().numpy()
     al = lambda v: (v + 255) & ~255
     mt = (N + 15) // 16 + min(N, E + 1)                 # tiles of <= 16 rows
+    room = (N + 3) // 4 + min(N, E + 1)                 # record room: 4-row tiles
     order = wb[:4 * N].view(np.int32)
     tm = wb[al(4 * N):al(4 * N) + 12 * mt].view(np.int32).reshape(mt, 3)
-    nt = int(wb[al(4 * N) + al(12 * mt):][:4].view(np.int32)[0])
+    nt = int(wb[al(4 * N) + al(12 * room):][:4].view(np.int32)[0])
     valid = ids < E
     ro, _, _, rs = vo.sort_routing(np.where(valid, ids, E), 1)
     ref_tm = vo.tile_meta(rs[rs < E], E, 16)
@@ -296,6 +301,58 @@ def test_grouped_gemm_sort_builds_oracle_tiles():
     ref = vo.expert_gemv(x.float().cpu().numpy()[valid], ids[valid], m["codes"], m["codebook"],
                          m["scales"], 64)
     assert_close(yn[valid], ref, what="sort case")
+
+
+def test_grouped_gemm_narrow_tiles():
+    """A d8 K16384 routing with <= 2 pairs per expert on average sorts into
+    tiles of <= 4 rows (the oracle's tile_meta at 4), one expert on every
+    token spanning several tiles, a skipzero row table on the same routing;
+    fp32 outputs against the oracle, dead rows exact zeros."""
+    from vqlab_amd import _lib as L, _torch as Tt, vq_switch as VS
+    from vq_cases import skipzero
+    print("grouped gemm narrow tiles", flush=True)
+    rng = np.random.default_rng(41)
+    E, OUT, IN, T, k = 64, 640, 1024, 11, 10              # N = 110 <= 2 E
+    m = make_module(rng, E, OUT, IN, 8, 16384, dead_frac=0.2)
+    codes, cb, sc = to_device(m)
+    ids = _routes(rng, T, k, E)
+    for t in range(T):                                  # expert 5 on every token
+        if 5 not in ids[t]:
+            ids[t, 0] = 5
+    assert all(len(np.unique(r)) == k for r in ids)
+    ids = ids.reshape(-1)
+    assert (ids == 5).sum() == T
+    N = T * k
+    x = _x(rng, T, IN)
+    e = torch.from_numpy(ids.astype(np.int32)).cuda()
+    keep = []
+    w = Tt.weights(codes, cb, sc, 64, m["pack_bits"], IN, keep=keep)
+    ws = ctypes.c_size_t()
+    L.check(L.lib().vqk_grouped_gemm_workspace(ctypes.byref(w), N, ctypes.byref(ws)))
+    work = torch.zeros(ws.value, dtype=torch.uint8, device="cuda")
+    y = torch.empty((N, OUT), dtype=torch.float32, device="cuda")
+    L.check(L.lib().vqk_grouped_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, T, Tt.ptr(e), N, k,
+                                     Tt.ptr(y), L.VQK_F32, Tt.ptr(work), ws.value, Tt.stream()))
+    torch.cuda.synchronize()
+    wb = work.cpu().numpy()
+    al = lambda v: (v + 255) & ~255
+    room = (N + 3) // 4 + min(N, E + 1)
+    _, _, _, rs = vo.sort_routing(ids, 1)
+    ref_tm = vo.tile_meta(rs, E, 4)
+    tm = wb[al(4 * N):al(4 * N) + 12 * len(ref_tm)].view(np.int32).reshape(-1, 3)
+    nt = int(wb[al(4 * N) + al(12 * room):][:4].view(np.int32)[0])
+    assert nt == len(ref_tm) and np.array_equal(tm, ref_tm)
+    assert (ref_tm[ref_tm[:, 0] == 5][:, 2] == [4, 4, 3]).all()
+    ref = vo.expert_gemv(_x16(x), ids, m["codes"], m["codebook"], m["scales"], 64, xkrep=k)
+    assert_close(_np(y), ref, what="narrow tiles")
+    sz, rt = skipzero(m)
+    zc = torch.from_numpy(sz["sz_codes"].view(np.int32)).cuda()
+    zs = torch.from_numpy(sz["sz_scales"]).cuda()
+    yc = VS._gemmseg(x, e, zc, cb, zs, m["pack_bits"], IN, k, torch.from_numpy(rt).cuda(),
+                     out_dtype=torch.float32)
+    dead = rt[ids] < 0
+    assert dead.any() and (_np(yc)[dead] == 0).all()
+    assert torch.equal(yc[torch.from_numpy(~dead).cuda()], y[torch.from_numpy(~dead).cuda()])
 
 
 def test_grouped_gemm_errors():

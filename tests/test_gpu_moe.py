@@ -142,15 +142,17 @@ def test_routing_ties_pick_lower_ids():
     assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("D,K,T,shared", [(8, 16384, 8, True), (8, 16384, 16, False),
-                                          (4, 4096, 12, True), (2, 512, 40, False)])
-def test_moe_layer_batched_grouped_path(D, K, T, shared):
+@pytest.mark.parametrize("D,K,T,shared,E", [(8, 16384, 8, True, 32), (8, 16384, 16, False, 32),
+                                            (4, 4096, 12, True, 32), (2, 512, 40, False, 32),
+                                            (8, 16384, 8, True, 64), (8, 16384, 12, False, 48)])
+def test_moe_layer_batched_grouped_path(D, K, T, shared, E):
     """T * top_k >= 64 pairs: the layer runs as one routing + one sort +
     grouped matrix-core GEMMs (SwiGLU built while down's input is staged) +
-    the weighted combine; same oracle, same bar."""
-    print(f"moe batched grouped D={D} K={K} T={T} shared={shared}", flush=True)
-    rng = np.random.default_rng(20 + T + D)
-    E, H, I, k = 32, 1024, 256, 8
+    the weighted combine; same oracle, same bar. With <= 2 pairs per expert
+    (the last two cases) the d8 tables take 4-row tiles."""
+    print(f"moe batched grouped D={D} K={K} T={T} shared={shared} E={E}", flush=True)
+    rng = np.random.default_rng(20 + T + D + (E if E != 32 else 0))
+    H, I, k = 1024, 256, 8
     blk, projs, sh, shv = _block(rng, E, H, I, D, K, k, shared=shared)
     _check(blk, projs, sh, shv, rng, T, E, H, k)
 

@@ -306,10 +306,10 @@ constexpr int kSegDenseMaxN = 64;               // dense rows up to which the se
 
 static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
-// Tiles of <= kSegTok sorted rows: sum over experts of ceil(count / kSegTok)
-// is at most ceil(N / kSegTok) + (non-empty buckets).
-static int64_t group_max_tiles(int64_t N, int64_t E) {
-    return (N + kSegTok - 1) / kSegTok + (N < E + 1 ? N : E + 1);
+// Tiles of <= tok sorted rows: sum over experts of ceil(count / tok) is at
+// most ceil(N / tok) + (non-empty buckets).
+static int64_t group_max_tiles(int64_t N, int64_t E, int tok) {
+    return (N + tok - 1) / tok + (N < E + 1 ? N : E + 1);
 }
 
 // The register-decode segment kernel covers whole 32-code blocks per row
@@ -393,11 +393,12 @@ static int dense_lt(const vqk_weights *w, const Geom &g, const void *x, int32_t 
     return VQK_OK;
 }
 
-static int launch_seg(const SegParams &p, const Geom &g, dim3 grid, hipStream_t st) {
+// tok: the most rows a tile holds (16, or 4 from a narrow sort).
+static int launch_seg(const SegParams &p, const Geom &g, int tok, dim3 grid, hipStream_t st) {
     switch (g.D) {
         case 2: return launch_seg_d2(p, g.BITS, g.gpb, grid, st);
         case 4: return launch_seg_d4(p, g.BITS, g.gpb, grid, st);
-        default: return launch_seg_d8(p, g.BITS, g.gpb, grid, st);
+        default: return launch_seg_d8(p, g.BITS, g.gpb, tok, grid, st);
     }
 }
 
@@ -452,8 +453,8 @@ static int check_acts(const void *x, int32_t x_type, const void *y, int32_t y_ty
 // ---- pieces of the grouped path for callers that sort one routing and run
 // several projections over it (the batched MoE layer)
 static size_t sort_order_bytes(int64_t N) { return al256(sizeof(int32_t) * size_t(N)); }
-static size_t sort_meta_bytes(int64_t N, int64_t E) {
-    return al256(sizeof(int32_t) * 3 * size_t(group_max_tiles(N, E)));
+static size_t sort_meta_bytes(int64_t N, int64_t E) {     // room for either tile size
+    return al256(sizeof(int32_t) * 3 * size_t(group_max_tiles(N, E, kSegTokNarrow)));
 }
 
 size_t seg_sort_bytes(int64_t N, int64_t E) {
@@ -463,20 +464,28 @@ size_t seg_sort_bytes(int64_t N, int64_t E) {
 bool seg_ok(const vqk_weights *w, int64_t N) {
     Geom g;
     if (make_geom(w, &g)) return false;
-    return seg_fits_geom(g, w) && g.E <= kMaxSortExperts && group_max_tiles(N, g.E) <= 65535 &&
-           N <= INT32_MAX / 2;
+    return seg_fits_geom(g, w) && g.E <= kMaxSortExperts &&
+           group_max_tiles(N, g.E, kSegTokNarrow) <= 65535 && N <= INT32_MAX / 2;
 }
 
-int seg_sort(const uint32_t *eidx, int64_t N, int64_t E, void *ws, hipStream_t st) {
+int seg_tile_rows(const vqk_weights *w, int64_t N, int64_t E) {
+    Geom g;
+    if (make_geom(w, &g)) return kSegTok;
+    return (g.D == 8 && !cb_in_lds(8, g.BITS) && N <= 2 * E) ? kSegTokNarrow : kSegTok;
+}
+
+int seg_sort(const uint32_t *eidx, int64_t N, int64_t E, int tok, void *ws, hipStream_t st) {
     if (N == 0) return VQK_OK;
+    if (tok != kSegTok && tok != kSegTokNarrow)
+        return set_error(VQK_EINVAL, "sort tiles of %d rows (16 or %d)", tok, kSegTokNarrow);
     uint8_t *b = static_cast<uint8_t *>(ws);
-    const int64_t mt = group_max_tiles(N, E);
+    const int64_t mt = group_max_tiles(N, E, tok);
     int32_t *order = reinterpret_cast<int32_t *>(b);
     int32_t *tmeta = reinterpret_cast<int32_t *>(b + sort_order_bytes(N));
     int32_t *ntiles = reinterpret_cast<int32_t *>(b + sort_order_bytes(N) + sort_meta_bytes(N, E));
     const size_t sort_lds = sizeof(int) * (3 * size_t(E + 1) + kSortThreads);
     hipLaunchKernelGGL(k_group_sort, dim3(1), dim3(kSortThreads), sort_lds, st, eidx, int(N), int(E),
-                       kSegTok, int(mt), order, tmeta, ntiles);
+                       tok, int(mt), order, tmeta, ntiles);
     return hip_status(hipGetLastError(), "group sort launch");
 }
 
@@ -496,15 +505,19 @@ int seg_run(const vqk_weights *w, const SegCall &c, const void *sort_ws, hipStre
     sp.y_type = c.y_type;
     sp.N = int32_t(c.N);
     int64_t tiles = (c.N + kSegTok - 1) / kSegTok;
+    int tok = kSegTok;
     if (sort_ws) {
+        tok = c.tok ? c.tok : kSegTok;
+        if (tok != kSegTok && tok != kSegTokNarrow)
+            return set_error(VQK_EINVAL, "sorted tiles of %d rows (16 or %d)", tok, kSegTokNarrow);
         const uint8_t *b = static_cast<const uint8_t *>(sort_ws);
         sp.order = reinterpret_cast<const int32_t *>(b);
         sp.tmeta = reinterpret_cast<const int32_t *>(b + sort_order_bytes(c.N));
         sp.ntiles = reinterpret_cast<const int32_t *>(b + sort_order_bytes(c.N) + sort_meta_bytes(c.N, g.E));
-        tiles = group_max_tiles(c.N, g.E);
+        tiles = group_max_tiles(c.N, g.E, tok);
     }
     const dim3 grid(unsigned((g.OUT + kSegRows - 1) / kSegRows), unsigned(tiles), 1);
-    return launch_seg(sp, g, grid, st);
+    return launch_seg(sp, g, tok, grid, st);
 }
 
 }  // namespace vqk
@@ -552,7 +565,7 @@ int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_t 
         sp.N = int32_t(N);
         const dim3 grid(unsigned((g.OUT + kSegRows - 1) / kSegRows),
                         unsigned((N + kSegTok - 1) / kSegTok), 1);
-        return launch_seg(sp, g, grid, hipStream_t(stream));
+        return launch_seg(sp, g, kSegTok, grid, hipStream_t(stream));
     }
     if (hgemm_fits(g, x, N) && (workspace || ws_bytes)) {
         hipStream_t st = hipStream_t(stream);
@@ -636,16 +649,18 @@ int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_
     if (!workspace || ws_bytes < need)
         return set_error(VQK_ENOSPACE, "workspace %zu B < %zu B", ws_bytes, need);
     if (N == 0) return VQK_OK;
-    const int64_t mt = group_max_tiles(N, g.E);
+    const bool seg = seg_fits(g, w, x);
+    const int tok = seg ? seg_tile_rows(w, N, g.E) : kSegTok;
+    const int64_t mt = group_max_tiles(N, g.E, tok);
     if (mt > 65535) return set_error(VQK_ENOTIMPL, "%lld tiles exceed one launch", (long long)mt);
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     int32_t *order = reinterpret_cast<int32_t *>(ws);
     int32_t *tmeta = reinterpret_cast<int32_t *>(ws + sort_order_bytes(N));
     int32_t *ntiles = reinterpret_cast<int32_t *>(ws + sort_order_bytes(N) + sort_meta_bytes(N, g.E));
     hipStream_t st = hipStream_t(stream);
-    if ((rc = seg_sort(eidx, N, g.E, ws, st))) return rc;
-    if (seg_fits(g, w, x)) {
-        const SegCall c{x, x_type, nullptr, nullptr, xkrep, y, y_type, N};
+    if ((rc = seg_sort(eidx, N, g.E, tok, ws, st))) return rc;
+    if (seg) {
+        const SegCall c{x, x_type, nullptr, nullptr, xkrep, y, y_type, N, tok};
         return seg_run(w, c, ws, st);
     }
     GemmParams p;

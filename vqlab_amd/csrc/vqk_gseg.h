@@ -59,6 +59,10 @@ struct SegParams {
 
 constexpr int kSegRows = 128;      // weight rows per workgroup
 constexpr int kSegTok = 16;        // tokens per tile
+// Tiles of at most kSegTokNarrow tokens, for routings that put a few pairs on
+// each expert (an MTP verify batch: ~1.25 per expert): the smaller x chunk
+// leaves more of the 160 KB to a d8 table too large for LDS.
+constexpr int kSegTokNarrow = 4;
 
 // Entry D halves of a table (LDS or global) as 8 halves: d8 one entry,
 // d4 two, d2 four (the codes of one MFMA step).
@@ -122,30 +126,32 @@ __device__ __forceinline__ h8 step_entries_hyb(const uint32_t (&w)[BITS], int s,
 }
 
 // LDS entries of a table too large for LDS that the kernel stages: what the
-// x chunk (kSegTok x (128 D + 8) halves) leaves of the 160 KB -- 124 KB of a
-// d8 table (7936 of K16384's entries), all of a d4 K16384 table, 144 KB of a
-// d2 one.
-__host__ __device__ constexpr int seg_hyb_entries(int D) {
-    return (D == 8 ? 124 * 1024 : (D == 4 ? 128 * 1024 : 144 * 1024)) / (2 * D);
+// x chunk (TOK x (128 D + 8) halves) leaves of the 160 KB -- 124 KB of a d8
+// table (7936 of K16384's entries; 151 KB, 9664 entries, with 4-token
+// tiles), all of a d4 K16384 table, 144 KB of a d2 one.
+__host__ __device__ constexpr int seg_hyb_entries(int D, int TOK = kSegTok) {
+    return (D == 8 ? (TOK == kSegTokNarrow ? 151 : 124) * 1024
+                   : (D == 4 ? 128 * 1024 : 144 * 1024)) / (2 * D);
 }
 
 
-template <int D, int BITS, int GPB, bool CBL>
+template <int D, int BITS, int GPB, bool CBL, int TOK = kSegTok>
 __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     constexpr int TN = 2;                       // 16-row tiles per wave
     constexpr int SPB = 4 * D;                  // MFMA steps per block (8 weights each)
     constexpr int CC = 128 * D;                 // x columns per superstep
     constexpr int XS = CC + 8;                  // LDS row stride of an x chunk (halves)
-    constexpr int PIECES = kSegTok * CC / 8;    // 16-byte pieces per chunk
+    constexpr int PIECES = TOK * CC / 8;        // 16-byte pieces per chunk
     constexpr int PPT = PIECES / 256;
     static_assert(PIECES % 256 == 0, "chunk must split evenly over 256 threads");
     // LDS table entries: the whole table, or the first seg_hyb_entries of it
-    constexpr int CBN = CBL ? (1 << BITS) : seg_hyb_entries(D);
-    static_assert(kSegTok * XS * 2 + (CBN + 1) * D * 2 <= 160 * 1024, "LDS beyond 160 KB");
+    constexpr int CBN = CBL ? (1 << BITS) : seg_hyb_entries(D, TOK);
+    static_assert(TOK == kSegTok || TOK == kSegTokNarrow, "token tile of 16 or 4 rows");
+    static_assert(TOK * XS * 2 + (CBN + 1) * D * 2 <= 160 * 1024, "LDS beyond 160 KB");
 
     extern __shared__ __align__(16) uint8_t smem[];
-    f16 *xs = reinterpret_cast<f16 *>(smem);    // [kSegTok][XS]
-    f16 *cbl = xs + kSegTok * XS;               // [CBN + 1][D]; entry CBN is zero
+    f16 *xs = reinterpret_cast<f16 *>(smem);    // [TOK][XS]
+    f16 *cbl = xs + TOK * XS;                   // [CBN + 1][D]; entry CBN is zero
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ln = lane & 15, lg = lane >> 4;
@@ -160,8 +166,8 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
         nrows = tm[2];
     } else {
         expert = 0;
-        row0 = int(blockIdx.y) * kSegTok;
-        nrows = min(kSegTok, p.N - row0);
+        row0 = int(blockIdx.y) * TOK;
+        nrows = min(TOK, p.N - row0);
     }
     const int o0 = int(blockIdx.x) * kSegRows + wave * 32;
 
@@ -249,7 +255,9 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
 
     auto compute = [&](const uint32_t (&w)[TN][BITS], const h2 (&s)[TN][GPB],
                        const bool (&live)[TN]) {
-        const f16 *xb = xs + ln * XS + lg * (32 * D);
+        // MFMA column ln is token ln; with TOK < 16 the columns past the tile
+        // repeat its rows and their sums are never stored
+        const f16 *xb = xs + (ln & (TOK - 1)) * XS + lg * (32 * D);
         const f16 *tab[TN];
         uint32_t kl[TN];
 #pragma unroll
@@ -332,16 +340,18 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     }
 }
 
-// LDS bytes of k_seg_mfma<D, BITS, ...>.
-__host__ __device__ constexpr size_t seg_lds(int D, int BITS, bool cbl) {
-    return size_t(kSegTok) * (128 * D + 8) * 2 +
-           (size_t(cbl ? (1 << BITS) : seg_hyb_entries(D)) + 1) * D * 2;
+// LDS bytes of k_seg_mfma<D, BITS, GPB, cbl, tok>.
+__host__ __device__ constexpr size_t seg_lds(int D, int BITS, bool cbl, int tok = kSegTok) {
+    return size_t(tok) * (128 * D + 8) * 2 +
+           (size_t(cbl ? (1 << BITS) : seg_hyb_entries(D, tok)) + 1) * D * 2;
 }
 
 // Launches k_seg_mfma for geometry-dependent template arguments; returns a
 // VQK status (VQK_ENOTIMPL when no instance matches).
 int launch_seg_d2(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st);
 int launch_seg_d4(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st);
-int launch_seg_d8(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st);
+// d8 with tok == kSegTokNarrow (tiles of at most 4 rows) takes the narrow
+// instance where the table is beyond LDS.
+int launch_seg_d8(const SegParams &p, int bits, int gpb, int tok, dim3 grid, hipStream_t st);
 
 }  // namespace vqk

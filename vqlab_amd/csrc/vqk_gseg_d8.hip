@@ -10,9 +10,30 @@ int go(const SegParams &p, dim3 grid, hipStream_t st) {
     constexpr bool CBL = cb_in_lds(8, BITS);
     return launch_with_lds<k_seg_mfma<8, BITS, GPB, CBL>>(grid, dim3(256), seg_lds(8, BITS, CBL), st, p);
 }
+// 4-token tiles: only where the table is beyond LDS (the x chunk's room goes
+// to table entries); other widths run the 16-token kernel on those tiles.
+template <int BITS, int GPB>
+int go_narrow(const SegParams &p, dim3 grid, hipStream_t st) {
+    static_assert(!cb_in_lds(8, BITS), "narrow tiles only pay for tables beyond LDS");
+    return launch_with_lds<k_seg_mfma<8, BITS, GPB, false, kSegTokNarrow>>(
+        grid, dim3(256), seg_lds(8, BITS, false, kSegTokNarrow), st, p);
+}
 }  // namespace
 
-int launch_seg_d8(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st) {
+int launch_seg_d8(const SegParams &p, int bits, int gpb, int tok, dim3 grid, hipStream_t st) {
+    if (tok == kSegTokNarrow) {
+        switch (bits * 16 + gpb) {
+            case 209: return go_narrow<13, 1>(p, grid, st);
+            case 212: return go_narrow<13, 4>(p, grid, st);
+            case 225: return go_narrow<14, 1>(p, grid, st);
+            case 228: return go_narrow<14, 4>(p, grid, st);
+            case 241: return go_narrow<15, 1>(p, grid, st);
+            case 244: return go_narrow<15, 4>(p, grid, st);
+            case 257: return go_narrow<16, 1>(p, grid, st);
+            case 260: return go_narrow<16, 4>(p, grid, st);
+            default: break;
+        }
+    }
     switch (bits * 16 + gpb) {
         case 33: return go<2, 1>(p, grid, st);
         case 36: return go<2, 4>(p, grid, st);

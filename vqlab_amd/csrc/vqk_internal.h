@@ -28,7 +28,13 @@ struct SegCall {
     void *y;                   // y[pair, OUT] in y_type
     int32_t y_type;
     int64_t N;                 // pairs (sorted) or dense rows (sort_ws == NULL)
+    int32_t tok;               // sorted: the sort's tile rows (seg_tile_rows); 0 = 16
 };
+
+// Rows per tile to sort N pairs into for module `w` over E experts: 4 when
+// the routing puts at most ~2 pairs on an expert on average and w's d8 table
+// is beyond LDS (more of it fits beside a 4-row x chunk), else 16.
+int seg_tile_rows(const vqk_weights *w, int64_t N, int64_t E);
 
 // Workspace of seg_sort for N pairs over E experts.
 size_t seg_sort_bytes(int64_t N, int64_t E);
@@ -37,8 +43,9 @@ size_t seg_sort_bytes(int64_t N, int64_t E);
 bool seg_ok(const vqk_weights *w, int64_t N);
 
 // Counting sort of N pair experts (device uint32, out-of-range ids form dead
-// tiles) into `ws`: pair order, tile records and the tile count.
-int seg_sort(const uint32_t *eidx, int64_t N, int64_t E, void *ws, hipStream_t st);
+// tiles) into `ws`: pair order, records of tiles of at most `tok` rows (16
+// or 4) and the tile count.
+int seg_sort(const uint32_t *eidx, int64_t N, int64_t E, int tok, void *ws, hipStream_t st);
 
 // One projection over a routing sorted into `sort_ws` (or over N dense rows
 // of expert 0 when sort_ws is NULL).

@@ -1086,12 +1086,15 @@ static int launch_moe_grouped(const vqk_moe_desc *m, const MoePlan &pl, uint8_t 
     hipLaunchKernelGGL(k_route_tokens, dim3(unsigned(T)), dim3(kWave), 0, st, p);
     int rc = hip_status(hipGetLastError(), "routing launch");
     if (rc) return rc;
-    if ((rc = seg_sort(reinterpret_cast<const uint32_t *>(p.ids), N, p.E, sort, st))) return rc;
-    SegCall c{p.x, p.x_type, nullptr, nullptr, k, g, VQK_F32, N};
+    // one sort for the three routed projections: its tile rows must suit
+    // every kernel run over it (the 16-row kernels take 4-row tiles too)
+    const int tok = seg_tile_rows(m->gate, N, p.E);
+    if ((rc = seg_sort(reinterpret_cast<const uint32_t *>(p.ids), N, p.E, tok, sort, st))) return rc;
+    SegCall c{p.x, p.x_type, nullptr, nullptr, k, g, VQK_F32, N, tok};
     if ((rc = seg_run(m->gate, c, sort, st))) return rc;
     c.y = u;
     if ((rc = seg_run(m->up, c, sort, st))) return rc;
-    SegCall d{nullptr, VQK_F32, g, u, 1, yd, VQK_F32, N};
+    SegCall d{nullptr, VQK_F32, g, u, 1, yd, VQK_F32, N, tok};
     if ((rc = seg_run(m->down, d, sort, st))) return rc;
     if (p.shared) {
         SegCall cs{p.x, p.x_type, nullptr, nullptr, 1, sgg, VQK_F32, T};
