@@ -340,6 +340,249 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     }
 }
 
+// Persistent form of k_seg_mfma for sorted expert tiles over a d8 table
+// beyond LDS (the MTP-verify shape: a few pairs per expert, hundreds of
+// experts). One workgroup per CU stages the table's LDS part once and then
+// walks its items -- (tile, 128-row block) pairs, item i of workgroup b is
+// b + i * gridDim.x -- as one flat sequence of K supersteps. Every step loads
+// the next step's weights and x (of the next item when this one ends) before
+// it multiplies, so neither the table copy nor an item's first memory latency
+// stalls the CU, as they do once per workgroup in k_seg_mfma (for a 1024-wide
+// down projection an item is a single superstep). An item's context -- its
+// weight rows through the skipzero row table, its token rows through the
+// sort order -- is resolved two items ahead and its tile record loaded three
+// ahead; each step issues those loads (discarded unless an item ends) so that
+// every step sends the same loads and the compiler's load-count waits never
+// stall a step on the prefetch issued in it.
+template <int BITS, int GPB, int TOK>
+__global__ void __launch_bounds__(256) k_seg_persist(const SegParams p) {
+    constexpr int D = 8;
+    constexpr int TN = 2;                       // 16-row tiles per wave
+    constexpr int SPB = 4 * D;                  // MFMA steps per block
+    constexpr int CC = 128 * D;                 // x columns per superstep
+    constexpr int XS = CC + 8;                  // LDS row stride of the x chunk (halves)
+    constexpr int PIECES = TOK * CC / 8;        // 16-byte pieces per chunk
+    constexpr int PPT = PIECES / 256;
+    static_assert(PIECES % 256 == 0, "chunk must split evenly over 256 threads");
+    constexpr int CBN = seg_hyb_entries(D, TOK);
+    static_assert(TOK * XS * 2 + (CBN + 1) * D * 2 <= 160 * 1024, "LDS beyond 160 KB");
+
+    extern __shared__ __align__(16) uint8_t smem[];
+    f16 *xs = reinterpret_cast<f16 *>(smem);    // [TOK][XS]
+    f16 *cbl = xs + TOK * XS;                   // [CBN + 1][D]; entry CBN is zero
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ln = lane & 15, lg = lane >> 4;
+    const int nxb = (p.OUT + kSegRows - 1) / kSegRows;
+    const int items = *p.ntiles * nxb;          // uniform
+    const int G = int(gridDim.x), i0 = int(blockIdx.x);
+    if (i0 >= items) return;                    // uniform, before any barrier
+    const int mine = (items - i0 + G - 1) / G;
+    const int NSS = (p.NB + 3) >> 2;
+    const int steps = mine * NSS;
+    const uint32_t kmax = uint32_t(p.K - 1);
+
+    {
+        const int ent = min(p.K, CBN);
+        lds_copy_async(p.codebook, cbl, ent * D * 2, (CBN + 1) * D * 2);
+    }
+
+    struct Meta { int e, row0, nrows, xb; };
+    struct Ctx {
+        int64_t cr[TN];       // this lane's stored weight row per row tile, or -1
+        int64_t xoff[PPT];    // x element offset of each x piece's token row, or -1
+        int64_t yrow;         // output row of token ln, or -1
+        int o0, nrows;
+    };
+    // tile record of this workgroup's item m (none past the last: no rows)
+    auto meta = [&](int m) {
+        Meta r{-1, 0, 0, 0};
+        if (m < mine) {
+            const int it = i0 + m * G;
+            const int32_t *tm = p.tmeta + 3 * (it / nxb);
+            r.e = tm[0];
+            r.row0 = tm[1];
+            r.nrows = tm[2];
+            r.xb = it % nxb;
+        }
+        return r;
+    };
+    auto resolve = [&](const Meta &m) {
+        Ctx c;
+        c.o0 = m.xb * kSegRows + wave * 32;
+        c.nrows = m.nrows;
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+            const int o = c.o0 + 16 * tn + ln;
+            int64_t f = -1;
+            if (m.e >= 0 && m.e < p.E && o < p.OUT) {
+                f = int64_t(m.e) * p.OUT + o;
+                if (p.row_table) f = p.row_table[f];
+                if (f < 0 || f >= p.stored_rows) f = -1;
+            }
+            c.cr[tn] = f;
+        }
+#pragma unroll
+        for (int r = 0; r < PPT; ++r) {
+            const int t = (tid + 256 * r) / (CC / 8);
+            c.xoff[r] = t < m.nrows ? int64_t(p.order[m.row0 + t] / p.xkrep) * p.IN : int64_t(-1);
+        }
+        c.yrow = ln < m.nrows ? int64_t(p.order[m.row0 + ln]) : int64_t(-1);
+        return c;
+    };
+
+    auto load_x = [&](const Ctx &c, int sb, u32x4 (&v)[PPT]) {
+#pragma unroll
+        for (int r = 0; r < PPT; ++r) {
+            const int col = sb * CC + ((tid + 256 * r) % (CC / 8)) * 8;
+            const bool ok = c.xoff[r] >= 0 && col < p.IN;
+            if (p.xg) {
+                v[r] = ok ? swiglu8(p.xg + c.xoff[r] + col, p.xu + c.xoff[r] + col) : u32x4{0, 0, 0, 0};
+            } else {
+                v[r] = ok ? load8_act(p.x, p.x_type, c.xoff[r] + col) : u32x4{0, 0, 0, 0};
+            }
+        }
+    };
+    auto store_x = [&](const u32x4 (&v)[PPT]) {
+#pragma unroll
+        for (int r = 0; r < PPT; ++r) {
+            const int pc = tid + 256 * r;
+            *reinterpret_cast<u32x4 *>(xs + (pc / (CC / 8)) * XS + (pc % (CC / 8)) * 8) = v[r];
+        }
+    };
+    auto load_w = [&](const Ctx &c, int sb, uint32_t (&w)[TN][BITS], h2 (&s)[TN][GPB],
+                      bool (&live)[TN]) {
+        const int b = 4 * sb + lg;
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+            live[tn] = c.cr[tn] >= 0 && b < p.NB;
+            if (live[tn]) {
+                const uint32_t *src = p.codes + c.cr[tn] * p.row_words + int64_t(b) * BITS;
+#pragma unroll
+                for (int i = 0; i < BITS; ++i) w[tn][i] = __builtin_nontemporal_load(src + i);
+                const uint16_t *sr = p.scales + c.cr[tn] * p.ngrp + (GPB == 1 ? b / p.bpg : b * GPB);
+#pragma unroll
+                for (int g = 0; g < GPB; ++g) {
+                    const f16 v = __builtin_bit_cast(f16, __builtin_nontemporal_load(sr + g));
+                    s[tn][g] = h2{v, v};
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < BITS; ++i) w[tn][i] = 0u;
+#pragma unroll
+                for (int g = 0; g < GPB; ++g) s[tn][g] = h2{0, 0};
+            }
+        }
+    };
+
+    f32x4 acc[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) acc[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const uint32_t (&w)[TN][BITS], const h2 (&s)[TN][GPB],
+                       const bool (&live)[TN]) {
+        // MFMA column ln is token ln; with TOK < 16 the columns past the tile
+        // repeat its rows and their sums are never stored
+        const f16 *xb = xs + (ln & (TOK - 1)) * XS + lg * (32 * D);
+        const f16 *tab[TN];
+        uint32_t kl[TN];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+            tab[tn] = live[tn] ? cbl : cbl + CBN * D;        // dead lanes: code 0 -> zero entry
+            kl[tn] = live[tn] ? uint32_t(min(p.K, CBN)) : 1u;
+        }
+        const f16 *tg = reinterpret_cast<const f16 *>(p.codebook);
+#pragma unroll
+        for (int st = 0; st < SPB; ++st) {
+            const h8 xf = *reinterpret_cast<const h8 *>(xb + 8 * st);
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const int q = (st * GPB) / (4 * D);
+                const h8 e = step_entries_hyb<D, BITS>(w[tn], st, tab[tn], tg, kl[tn], kmax);
+                const h2 sc = s[tn][q];
+                const h8 wv = e * h8{sc[0], sc[0], sc[0], sc[0], sc[0], sc[0], sc[0], sc[0]};
+                acc[tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv, xf, acc[tn], 0, 0, 0);
+            }
+        }
+    };
+    // lane holds rows 16*tn + 4*lg + i of token ln
+    auto epilogue = [&](const Ctx &c) {
+        uint64_t alive[TN];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) alive[tn] = __ballot(c.cr[tn] >= 0);
+        if (ln < c.nrows) {
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 16 * tn + 4 * lg + i;
+                    const int o = c.o0 + r;
+                    if (o < p.OUT) {
+                        const float v = ((alive[tn] >> (r - 16 * tn)) & 1) ? acc[tn][i] : 0.f;
+                        store_act(p.y, p.y_type, c.yrow * p.OUT + o, v);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) acc[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    // context pipeline: c0 = item m, c1 = item m + 1 (resolved), m2 = item m + 2
+    int m = 0, sb = 0;
+    Ctx c0 = resolve(meta(0));
+    Ctx c1 = resolve(meta(1));
+    Meta m2 = meta(2);
+
+    uint32_t w0[TN][BITS], w1[TN][BITS];
+    h2 s0[TN][GPB], s1[TN][GPB];
+    bool l0[TN], l1[TN];
+    u32x4 xr[PPT];
+
+    load_x(c0, 0, xr);
+    load_w(c0, 0, w0, s0, l0);
+    store_x(xr);
+    wait_vmem();                                // table part and the first chunk
+    __syncthreads();
+
+    // one step on buffers (wc, sc, lc), prefetching into (wn, sn, lnx);
+    // false after the last step
+    auto step = [&](int j, const uint32_t (&wc)[TN][BITS], const h2 (&sc)[TN][GPB],
+                    const bool (&lc)[TN], uint32_t (&wn)[TN][BITS], h2 (&sn)[TN][GPB],
+                    bool (&lnx)[TN]) {
+        const bool last = sb + 1 == NSS;        // this item's last superstep
+        const bool more = j + 1 < steps;
+        Ctx c2 = c1;
+        Meta m3 = m2;
+        if (more) {
+            c2 = resolve(m2);                   // kept only if this item ends
+            m3 = meta(m + 3);
+            load_x(last ? c1 : c0, last ? 0 : sb + 1, xr);
+            load_w(last ? c1 : c0, last ? 0 : sb + 1, wn, sn, lnx);
+        }
+        compute(wc, sc, lc);
+        if (last) {
+            epilogue(c0);
+            c0 = c1;
+            c1 = c2;
+            m2 = m3;
+            ++m;
+            sb = 0;
+        } else {
+            ++sb;
+        }
+        if (!more) return false;
+        __syncthreads();                        // every wave is done with this chunk
+        store_x(xr);
+        __syncthreads();                        // the next chunk is in place
+        return true;
+    };
+    for (int j = 0;; j += 2) {
+        if (!step(j, w0, s0, l0, w1, s1, l1)) break;
+        if (!step(j + 1, w1, s1, l1, w0, s0, l0)) break;
+    }
+}
+
 // LDS bytes of k_seg_mfma<D, BITS, GPB, cbl, tok>.
 __host__ __device__ constexpr size_t seg_lds(int D, int BITS, bool cbl, int tok = kSegTok) {
     return size_t(tok) * (128 * D + 8) * 2 +
@@ -353,5 +596,7 @@ int launch_seg_d4(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t 
 // d8 with tok == kSegTokNarrow (tiles of at most 4 rows) takes the narrow
 // instance where the table is beyond LDS.
 int launch_seg_d8(const SegParams &p, int bits, int gpb, int tok, dim3 grid, hipStream_t st);
+// k_seg_persist (sorted 4-row tiles, d8 tables beyond LDS) on `grid` workgroups.
+int launch_seg_persist_d8(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st);
 
 }  // namespace vqk

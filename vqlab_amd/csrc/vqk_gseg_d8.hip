@@ -18,7 +18,28 @@ int go_narrow(const SegParams &p, dim3 grid, hipStream_t st) {
     return launch_with_lds<k_seg_mfma<8, BITS, GPB, false, kSegTokNarrow>>(
         grid, dim3(256), seg_lds(8, BITS, false, kSegTokNarrow), st, p);
 }
+template <int BITS, int GPB>
+int go_persist(const SegParams &p, dim3 grid, hipStream_t st) {
+    return launch_with_lds<k_seg_persist<BITS, GPB, kSegTokNarrow>>(
+        grid, dim3(256), seg_lds(8, BITS, false, kSegTokNarrow), st, p);
+}
 }  // namespace
+
+int launch_seg_persist_d8(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st) {
+    switch (bits * 16 + gpb) {
+        case 209: return go_persist<13, 1>(p, grid, st);
+        case 212: return go_persist<13, 4>(p, grid, st);
+        case 225: return go_persist<14, 1>(p, grid, st);
+        case 228: return go_persist<14, 4>(p, grid, st);
+        case 241: return go_persist<15, 1>(p, grid, st);
+        case 244: return go_persist<15, 4>(p, grid, st);
+        case 257: return go_persist<16, 1>(p, grid, st);
+        case 260: return go_persist<16, 4>(p, grid, st);
+        default:
+            return set_error(VQK_ENOTIMPL, "no persistent segment kernel for d=8 bits=%d gpb=%d",
+                             bits, gpb);
+    }
+}
 
 int launch_seg_d8(const SegParams &p, int bits, int gpb, int tok, dim3 grid, hipStream_t st) {
     if (tok == kSegTokNarrow) {

@@ -18,6 +18,10 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
                 const uint32_t *eidx, int64_t N, int64_t xkrep, void *y, int32_t y_type,
                 hipStream_t st);
 
+// min(items, the current device's CU count): the grid of a kernel that
+// keeps one workgroup per CU (vqk_big.hip).
+int big_grid(int64_t items);
+
 // ---- grouped expert GEMM pieces (vqk_gemm.hip): sort one routing, then run
 // several projections over it with the register-decode segment kernel.
 struct SegCall {
