@@ -224,7 +224,9 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
         }
     };
     // words and scales of block 4*sb + lg of each row; lanes without one get
-    // zero words, zero scales and the zero entry
+    // zero words, zero scales and the zero entry. Plain (cached) loads: a
+    // superstep takes 4 blocks of a row (224 bytes at 14 bits), so lines
+    // straddle supersteps and a streaming load would fetch them twice.
     auto load_w = [&](int sb, uint32_t (&w)[TN][BITS], h2 (&s)[TN][GPB], bool (&live)[TN]) {
         const int b = 4 * sb + lg;
 #pragma unroll
@@ -233,11 +235,11 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
             if (live[tn]) {
                 const uint32_t *src = p.codes + cr[tn] * p.row_words + int64_t(b) * BITS;
 #pragma unroll
-                for (int i = 0; i < BITS; ++i) w[tn][i] = __builtin_nontemporal_load(src + i);
+                for (int i = 0; i < BITS; ++i) w[tn][i] = src[i];
                 const uint16_t *sr = p.scales + cr[tn] * p.ngrp + (GPB == 1 ? b / p.bpg : b * GPB);
 #pragma unroll
                 for (int g = 0; g < GPB; ++g) {
-                    const f16 v = __builtin_bit_cast(f16, __builtin_nontemporal_load(sr + g));
+                    const f16 v = __builtin_bit_cast(f16, sr[g]);
                     s[tn][g] = h2{v, v};
                 }
             } else {
@@ -459,11 +461,11 @@ __global__ void __launch_bounds__(256) k_seg_persist(const SegParams p) {
             if (live[tn]) {
                 const uint32_t *src = p.codes + c.cr[tn] * p.row_words + int64_t(b) * BITS;
 #pragma unroll
-                for (int i = 0; i < BITS; ++i) w[tn][i] = __builtin_nontemporal_load(src + i);
+                for (int i = 0; i < BITS; ++i) w[tn][i] = src[i];
                 const uint16_t *sr = p.scales + c.cr[tn] * p.ngrp + (GPB == 1 ? b / p.bpg : b * GPB);
 #pragma unroll
                 for (int g = 0; g < GPB; ++g) {
-                    const f16 v = __builtin_bit_cast(f16, __builtin_nontemporal_load(sr + g));
+                    const f16 v = __builtin_bit_cast(f16, sr[g]);
                     s[tn][g] = h2{v, v};
                 }
             } else {
