@@ -296,7 +296,7 @@ def run_mtp(torch, dev, a, w):
                      "traffic": (measured_traffic(f"mtp_verify_{a.workload}_traffic.md")
                                  if a.mtp_path == "fused" else None),
                      "traffic_source": "profiles/mtp_verify_<workload>_traffic.md",
-                     "kernel": "k_seg_mfma (grouped gate/up/down) + routing / sort / combine",
+                     "kernel": "k_seg_persist (routed gate/up/down) + k_seg_mfma (shared expert) + routing / sort / combine",
                      "path": a.mtp_path,
                      "alg_bytes_per_call": int(alg_per_call),
                      "us_per_call_events": round(us_call, 3)},

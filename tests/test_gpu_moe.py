@@ -157,14 +157,17 @@ def test_moe_layer_batched_grouped_path(D, K, T, shared, E):
     _check(blk, projs, sh, shv, rng, T, E, H, k)
 
 
-def test_moe_layer_batched_skipzero():
+@pytest.mark.parametrize("E,T", [(32, 16), (64, 8)])
+def test_moe_layer_batched_skipzero(E, T):
     """The grouped layer over compact skipzero experts (20% dead rows): dead
-    rows contribute exact zeros, as in the expanded oracle."""
+    rows contribute exact zeros, as in the expanded oracle. E=64, T=8: one
+    pair per expert on average, the config-4 path (4-row tiles, persistent
+    segment kernel)."""
     from vq_cases import skipzero
     from vqlab_amd.vq_switch import VQSwitchLinear
-    print("moe batched skipzero", flush=True)
-    rng = np.random.default_rng(31)
-    E, H, I, k, T = 32, 1024, 256, 8, 16
+    print(f"moe batched skipzero E={E} T={T}", flush=True)
+    rng = np.random.default_rng(31 + E)
+    H, I, k = 1024, 256, 8
     blk, projs, _, _ = _block(rng, E, H, I, 8, 16384, k)
     for name, (o, i) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
         m = make_module(rng, E, o, i, 8, 16384, dead_frac=0.2)
