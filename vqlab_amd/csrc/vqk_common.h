@@ -71,6 +71,15 @@ __device__ __forceinline__ uint16_t f32_to_h(float f) {
     return __builtin_bit_cast(uint16_t, f16(f));
 }
 
+// Element i of a table in global memory, read through the global address
+// space: a global_load waits on the vector-memory counter only, where the
+// flat_load a generic pointer (e.g. one taken from a parameter struct) gets
+// also counts as an LDS access, so every LDS wait after it waits for it.
+template <typename T>
+__device__ __forceinline__ T load_global(const T *p, int64_t i) {
+    return ((const __attribute__((address_space(1))) T *)p)[i];
+}
+
 __device__ __forceinline__ float load_act(const void *p, int32_t type, int64_t i) {
     if (type == VQK_F32) return static_cast<const float *>(p)[i];
     uint16_t v = static_cast<const uint16_t *>(p)[i];

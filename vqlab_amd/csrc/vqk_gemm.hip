@@ -517,11 +517,12 @@ int seg_run(const vqk_weights *w, const SegCall &c, const void *sort_ws, hipStre
         tiles = group_max_tiles(c.N, g.E, tok);
     }
     const int64_t nxb = (g.OUT + kSegRows - 1) / kSegRows;
+    const int64_t nxp = (g.OUT + kPersistWaves * 32 - 1) / (kPersistWaves * 32);
     if (sort_ws && tok == kSegTokNarrow && g.D == 8 && !cb_in_lds(8, g.BITS) &&
-        nxb * tiles <= INT32_MAX) {
+        nxp * tiles <= INT32_MAX) {
         // one workgroup per CU walking (tile, row block) items: the table
         // part is staged once per CU, not once per item
-        const dim3 grid(unsigned(big_grid(nxb * tiles)), 1, 1);
+        const dim3 grid(unsigned(big_grid(nxp * tiles)), 1, 1);
         return launch_seg_persist_d8(sp, g.BITS, g.gpb, grid, st);
     }
     const dim3 grid(unsigned(nxb), unsigned(tiles), 1);

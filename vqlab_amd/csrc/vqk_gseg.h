@@ -63,6 +63,10 @@ constexpr int kSegTok = 16;        // tokens per tile
 // each expert (an MTP verify batch: ~1.25 per expert): the smaller x chunk
 // leaves more of the 160 KB to a d8 table too large for LDS.
 constexpr int kSegTokNarrow = 4;
+// Waves of the persistent kernel's workgroup (one per CU): two per SIMD, so
+// one wave's table reads are in flight while the other decodes; an item is
+// 32 rows per wave.
+constexpr int kPersistWaves = 8;
 
 // Entry D halves of a table (LDS or global) as 8 halves: d8 one entry,
 // d4 two, d2 four (the codes of one MFMA step).
@@ -102,8 +106,13 @@ __device__ __forceinline__ typename EntryT<D>::type hyb_entry(uint32_t c, const 
                                                               uint32_t kl, uint32_t kmax) {
     typedef typename EntryT<D>::type E;
     E e;
-    if (c < kl) e = reinterpret_cast<const E *>(tl)[c];
-    else e = reinterpret_cast<const E *>(tg)[min(c, kmax)];
+    // branch-free: both reads for every lane (the other one of entry 0: a
+    // broadcast in LDS, one coalesced line in L2), so the unrolled steps'
+    // reads are not split into exec-masked blocks and can overlap
+    const bool inl = c < kl;
+    const E el = reinterpret_cast<const E *>(tl)[inl ? c : 0u];
+    const E eg = load_global(reinterpret_cast<const E *>(tg), inl ? 0u : min(c, kmax));
+    e = inl ? el : eg;
     return e;
 }
 
@@ -356,16 +365,18 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
 // ahead; each step issues those loads (discarded unless an item ends) so that
 // every step sends the same loads and the compiler's load-count waits never
 // stall a step on the prefetch issued in it.
-template <int BITS, int GPB, int TOK>
-__global__ void __launch_bounds__(256) k_seg_persist(const SegParams p) {
+template <int BITS, int GPB, int TOK, int NW = kPersistWaves>
+__global__ void __launch_bounds__(NW * 64) k_seg_persist(const SegParams p) {
     constexpr int D = 8;
+    constexpr int NT = NW * 64;                 // threads
+    constexpr int ROWS = NW * 32;               // weight rows per item
     constexpr int TN = 2;                       // 16-row tiles per wave
     constexpr int SPB = 4 * D;                  // MFMA steps per block
     constexpr int CC = 128 * D;                 // x columns per superstep
     constexpr int XS = CC + 8;                  // LDS row stride of the x chunk (halves)
     constexpr int PIECES = TOK * CC / 8;        // 16-byte pieces per chunk
-    constexpr int PPT = PIECES / 256;
-    static_assert(PIECES % 256 == 0, "chunk must split evenly over 256 threads");
+    constexpr int PPT = PIECES / NT;
+    static_assert(PIECES % NT == 0, "chunk must split evenly over the threads");
     constexpr int CBN = seg_hyb_entries(D, TOK);
     static_assert(TOK * XS * 2 + (CBN + 1) * D * 2 <= 160 * 1024, "LDS beyond 160 KB");
 
@@ -375,7 +386,7 @@ __global__ void __launch_bounds__(256) k_seg_persist(const SegParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ln = lane & 15, lg = lane >> 4;
-    const int nxb = (p.OUT + kSegRows - 1) / kSegRows;
+    const int nxb = (p.OUT + ROWS - 1) / ROWS;
     const int items = *p.ntiles * nxb;          // uniform
     const int G = int(gridDim.x), i0 = int(blockIdx.x);
     if (i0 >= items) return;                    // uniform, before any barrier
@@ -411,7 +422,7 @@ __global__ void __launch_bounds__(256) k_seg_persist(const SegParams p) {
     };
     auto resolve = [&](const Meta &m) {
         Ctx c;
-        c.o0 = m.xb * kSegRows + wave * 32;
+        c.o0 = m.xb * ROWS + wave * 32;
         c.nrows = m.nrows;
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) {
@@ -426,7 +437,7 @@ __global__ void __launch_bounds__(256) k_seg_persist(const SegParams p) {
         }
 #pragma unroll
         for (int r = 0; r < PPT; ++r) {
-            const int t = (tid + 256 * r) / (CC / 8);
+            const int t = (tid + NT * r) / (CC / 8);
             c.xoff[r] = t < m.nrows ? int64_t(p.order[m.row0 + t] / p.xkrep) * p.IN : int64_t(-1);
         }
         c.yrow = ln < m.nrows ? int64_t(p.order[m.row0 + ln]) : int64_t(-1);
@@ -436,7 +447,7 @@ __global__ void __launch_bounds__(256) k_seg_persist(const SegParams p) {
     auto load_x = [&](const Ctx &c, int sb, u32x4 (&v)[PPT]) {
 #pragma unroll
         for (int r = 0; r < PPT; ++r) {
-            const int col = sb * CC + ((tid + 256 * r) % (CC / 8)) * 8;
+            const int col = sb * CC + ((tid + NT * r) % (CC / 8)) * 8;
             const bool ok = c.xoff[r] >= 0 && col < p.IN;
             if (p.xg) {
                 v[r] = ok ? swiglu8(p.xg + c.xoff[r] + col, p.xu + c.xoff[r] + col) : u32x4{0, 0, 0, 0};
@@ -448,7 +459,7 @@ __global__ void __launch_bounds__(256) k_seg_persist(const SegParams p) {
     auto store_x = [&](const u32x4 (&v)[PPT]) {
 #pragma unroll
         for (int r = 0; r < PPT; ++r) {
-            const int pc = tid + 256 * r;
+            const int pc = tid + NT * r;
             *reinterpret_cast<u32x4 *>(xs + (pc / (CC / 8)) * XS + (pc % (CC / 8)) * 8) = v[r];
         }
     };

@@ -21,7 +21,7 @@ int go_narrow(const SegParams &p, dim3 grid, hipStream_t st) {
 template <int BITS, int GPB>
 int go_persist(const SegParams &p, dim3 grid, hipStream_t st) {
     return launch_with_lds<k_seg_persist<BITS, GPB, kSegTokNarrow>>(
-        grid, dim3(256), seg_lds(8, BITS, false, kSegTokNarrow), st, p);
+        grid, dim3(kPersistWaves * 64), seg_lds(8, BITS, false, kSegTokNarrow), st, p);
 }
 }  // namespace
 
