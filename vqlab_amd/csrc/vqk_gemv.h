@@ -158,6 +158,38 @@ __device__ __forceinline__ float block_dot_hyb(const uint32_t (&w)[BITS], const 
     return acc;
 }
 
+// block_dot_hyb with the block's 32·D activations read from LDS (`xl`) per
+// code instead of held in 16·D registers: the registers that frees let two
+// waves share a SIMD, each hiding the other's table-read latency.
+template <int D, int BITS, int GPB>
+__device__ __forceinline__ float block_dot_hyb_lx(const uint32_t (&w)[BITS], const f16 *xl,
+                                                  const float (&s)[GPB], const h2 *cbl,
+                                                  const h2 *cbg, uint32_t kl, uint32_t kmax) {
+    typedef typename EntryT<D>::type E;
+    constexpr int CPG = kBlock / GPB;
+    const E *xv = reinterpret_cast<const E *>(__builtin_assume_aligned(xl, 16));
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < GPB; ++g) {
+        float ga = 0.f;
+#pragma unroll
+        for (int q = 0; q < CPG; ++q) {
+            const int i = g * CPG + q;
+            const uint32_t c = block_field<BITS>(w, i);
+            E e;
+            if (c < kl) e = reinterpret_cast<const E *>(cbl)[c];
+            else e = reinterpret_cast<const E *>(cbg)[min(c, kmax)];
+            const E x = xv[i];
+            h2 xh[D / 2];
+#pragma unroll
+            for (int k = 0; k < D / 2; ++k) xh[k] = h2{x[2 * k], x[2 * k + 1]};
+            ga = dot_vec<D>(e, xh, ga);
+        }
+        acc = fmaf(s[g], ga, acc);
+    }
+    return acc;
+}
+
 template <int BITS, int GPB>
 __device__ __forceinline__ void load_block(const GemvParams &p, int64_t cr, int blk, int sidx,
                                            uint32_t (&w)[BITS], uint32_t (&s)[GPB]) {

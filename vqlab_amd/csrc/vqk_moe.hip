@@ -267,6 +267,14 @@ constexpr int kHybDownBytes = 112 * 1024;
 // Larger LDS parts when the workgroup's activations leave room (the host
 // checks): every entry moved into LDS is an L2 request per code saved.
 constexpr int kHybDownWideBytes = 136 * 1024;
+// Waves of the workgroups with the larger LDS parts (one workgroup per CU),
+// which read x from LDS: two per SIMD, so one wave decodes while the other
+// waits on its table reads (12 for gate / up measured no faster).
+constexpr int kWideWavesUp = 8, kWideWavesDown = 8;
+__host__ __device__ constexpr int moe_waves_up(bool wide) { return wide ? kWideWavesUp : kThreads / kWave; }
+__host__ __device__ constexpr int moe_waves_down(bool wide) {
+    return wide ? kWideWavesDown : kThreads / kWave;
+}
 
 // Entries of one gate/up table held in LDS, and of the routed down table.
 template <int D, int BITS>
@@ -438,8 +446,9 @@ constexpr int kHybSplitBytes = 128 * 1024;
 constexpr int kHybSplitWideBytes = 150 * 1024;   // when x leaves room (the host checks)
 
 template <int D, int BITS, int GPB, bool W = false>
-__global__ void __launch_bounds__(kThreads) k_moe_up_split(const MoeParams p) {
+__global__ void __launch_bounds__(moe_waves_up(W) * kWave) k_moe_up_split(const MoeParams p) {
     constexpr int CBN = (W ? kHybSplitWideBytes : kHybSplitBytes) / (2 * D);
+    constexpr int NWV = moe_waves_up(W);
     constexpr int XH = kBlock * D, XS = XH + 8;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ RouteLds rl;
@@ -465,7 +474,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_up_split(const MoeParams p) {
         if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
         if (lane == 0) rl.route = e_pair;
     } else {
-        constexpr int NT = kThreads - kWave;
+        constexpr int NT = NWV * kWave - kWave;
         stage_codebook_fixed<D, CBN, NT, 1>(w.codebook, w.K, cb_lds);
         stage_x<XH, XS>(p.x, p.x_type, int64_t(t) * p.H, p.H, p.NB1, xs, kWave, NT);
     }
@@ -488,7 +497,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_up_split(const MoeParams p) {
     const int64_t e = is_shared ? 0 : ((e_pair >= 0 && e_pair < p.E) ? e_pair : -1);
     const int sidx = GPB == 1 ? blk / p.bpg1 : blk * GPB;
     const int r_wg = bx * p.rows_per_wg1;
-    auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * rpw + sub; };
+    auto row_at = [&](int st) { return r_wg + (st * NWV + wave) * rpw + sub; };
     auto code_row = [&](int st) -> int64_t {
         const int r = row_at(st);
         return (on && e >= 0 && r < p.I) ? moe_row(w, e, p.I, r) : -1;
@@ -498,8 +507,10 @@ __global__ void __launch_bounds__(kThreads) k_moe_up_split(const MoeParams p) {
     uint32_t sc[GPB];
     int64_t cr = code_row(0);
     moe_load<BITS, GPB>(w, cr, blk, sidx, p.ngrp1, a, sc);
-    h2 xr[16 * D];
-    load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
+    // 8-wave (wide) instances read x from LDS per code; the others hold it
+    h2 xr[W ? 1 : 16 * D];
+    const f16 *xl = xs + (on ? blk : 0) * XS;
+    if constexpr (!W) load_xregs<D>(xl, xr);
     const h2 *cbg = reinterpret_cast<const h2 *>(w.codebook);
     const uint32_t kl = uint32_t(min(w.K, CBN));
     float *out = (proj == 0 ? p.gbuf : p.ubuf) + (int64_t(t) * p.P + j) * p.I;
@@ -510,7 +521,11 @@ __global__ void __launch_bounds__(kThreads) k_moe_up_split(const MoeParams p) {
         moe_load<BITS, GPB>(w, crn, blk, sidx, p.ngrp1, n, ns);
         float v = 0.f;
         const ScalesF32<GPB> fs(sc);
-        if (cr >= 0) v = block_dot_hyb<D, BITS, GPB>(a, xr, fs.v, cb_lds, cbg, kl, uint32_t(w.K - 1));
+        if constexpr (W) {
+            if (cr >= 0) v = block_dot_hyb_lx<D, BITS, GPB>(a, xl, fs.v, cb_lds, cbg, kl, uint32_t(w.K - 1));
+        } else {
+            if (cr >= 0) v = block_dot_hyb<D, BITS, GPB>(a, xr, fs.v, cb_lds, cbg, kl, uint32_t(w.K - 1));
+        }
         v = group_sum(v, lpr);
         const int r = row_at(st);
         if (blk == lpr - 1 && r < p.I) out[r] = v;
@@ -567,12 +582,12 @@ __device__ __forceinline__ void down_prep(const MoeParams &p, int bx, int t, con
 // Routed down table (all of it, or its first CBN entries) and, when the
 // whole table fits, the shared expert's; a partly staged routed table leaves
 // the shared expert's to L2.
-template <int D, int CBN, bool CBL>
+template <int D, int CBN, bool CBL, int NTH = kThreads>
 __device__ __forceinline__ void down_stage_cb(const MoeParams &p, uint8_t *smem) {
-    stage_codebook_fixed<D, CBN, kThreads>(p.down.codebook, p.down.K, reinterpret_cast<h2 *>(smem));
+    stage_codebook_fixed<D, CBN, NTH>(p.down.codebook, p.down.K, reinterpret_cast<h2 *>(smem));
     if (CBL && p.shared)
-        stage_codebook_fixed<D, CBN, kThreads>(p.sdown.codebook, p.sdown.K,
-                                               reinterpret_cast<h2 *>(smem + CBN * D * 2));
+        stage_codebook_fixed<D, CBN, NTH>(p.sdown.codebook, p.sdown.K,
+                                          reinterpret_cast<h2 *>(smem + CBN * D * 2));
 }
 
 // The token's P SwiGLU rows (fp16) -> LDS at the padded block stride, then
@@ -621,15 +636,16 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
     wait_vmem();
     __syncthreads();
 
-    h2 xr[16 * D];
-    load_xregs<D>(xs + (dl.on ? dl.j * p.NB2 + dl.blk : 0) * XS, xr);
+    h2 xr[W ? 1 : 16 * D];                  // wide (8-wave) instances read x from LDS
+    const f16 *xl = xs + (dl.on ? dl.j * p.NB2 + dl.blk : 0) * XS;
+    if constexpr (!W) load_xregs<D>(xl, xr);
     const h2 *cb = CBL ? (dl.is_shared ? cbs_lds : cbd_lds)
                        : reinterpret_cast<const h2 *>(wd.codebook);
     const uint32_t kmax = uint32_t(wd.K - 1);
     const uint32_t kl = dl.is_shared ? 0u : uint32_t(min(wd.K, CBN));     // partly staged: routed only
     const int sidx = GPB == 1 ? dl.blk / p.bpg2 : dl.blk * GPB;
     const int r_wg = bx * p.rows_per_wg2;
-    auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * dl.rpw + dl.sub; };
+    auto row_at = [&](int st) { return r_wg + (st * moe_waves_down(W) + wave) * dl.rpw + dl.sub; };
     auto code_row = [&](int st) -> int64_t {
         const int r = row_at(st);
         return (ds.e >= 0 && r < p.H) ? moe_row(wd, ds.e, p.H, r) : -1;
@@ -644,6 +660,8 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
         const ScalesF32<GPB> fs(ds.s);
         if constexpr (CBL) {
             if (ds.cr >= 0) acc = ds.wj * block_dot<D, BITS, GPB, true>(ds.a, xr, fs.v, cb, kmax);
+        } else if constexpr (W) {
+            if (ds.cr >= 0) acc = ds.wj * block_dot_hyb_lx<D, BITS, GPB>(ds.a, xl, fs.v, cbd_lds, cb, kl, kmax);
         } else {
             if (ds.cr >= 0) acc = ds.wj * block_dot_hyb<D, BITS, GPB>(ds.a, xr, fs.v, cbd_lds, cb, kl, kmax);
         }
@@ -659,7 +677,7 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
 }
 
 template <int D, int BITS, int GPB, bool W = false>
-__global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
+__global__ void __launch_bounds__(moe_waves_down(W) * kWave) k_moe_down(const MoeParams p) {
     constexpr int CBN = down_cbn<D, BITS, W>();
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = int(blockIdx.y);
@@ -677,7 +695,7 @@ __global__ void __launch_bounds__(kThreads) k_moe_down(const MoeParams p) {
     DownState<BITS, GPB> ds;
     down_prep<BITS, GPB>(p, int(blockIdx.x), t, dl, [&](int) { return id; },
                          [&](int) { return wt; }, ds);
-    down_stage_cb<D, CBN, cb_in_lds(D, BITS)>(p, smem);
+    down_stage_cb<D, CBN, cb_in_lds(D, BITS), moe_waves_down(W) * kWave>(p, smem);
     down_run<D, BITS, GPB, W>(p, int(blockIdx.x), t, smem, dl, ds);
 }
 
@@ -884,25 +902,29 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     // enough steps that the grid fits the CUs in one round (each round would
     // repeat the routing, the table copy and the first weight latency).
     const int64_t target = 2048, ncu = big_grid(int64_t(1) << 30);
-    auto plan_steps = [&](int64_t row_steps, int64_t cols, size_t smem, int32_t *steps) {
+    auto plan_steps = [&](int64_t row_steps, int64_t cols, size_t smem, int nw, int32_t *steps) {
         int64_t st = (row_steps * cols + target - 1) / target;
         st = st < 1 ? 1 : (st > 16 ? 16 : st);
-        if (smem > 80 * 1024)
-            while (st < 16 && ((row_steps + 4 * st - 1) / (4 * st)) * cols > ncu) ++st;
+        if (smem > 80 * 1024) {     // one workgroup per CU: the fewest steps that fit one round
+            st = 1;
+            while (st < 16 && ((row_steps + nw * st - 1) / (nw * st)) * cols > ncu) ++st;
+        }
         *steps = int32_t(st);
     };
     {   // K1: T*P pairs x I rows (x 2 projections when split)
         const int rpw = kWave >> p.lpr1_log2;
         const int nz = pl->split ? 2 : 1;
-        plan_steps((gg.OUT + rpw - 1) / rpw, T * P * nz, pl->smem1, &p.steps1);
-        p.rows_per_wg1 = int32_t(4 * rpw * p.steps1);
+        const int nw = moe_waves_up(pl->wide1);
+        plan_steps((gg.OUT + rpw - 1) / rpw, T * P * nz, pl->smem1, nw, &p.steps1);
+        p.rows_per_wg1 = int32_t(nw * rpw * p.steps1);
         pl->grid1 = dim3(unsigned((gg.OUT + p.rows_per_wg1 - 1) / p.rows_per_wg1), unsigned(T * P),
                          unsigned(nz));
     }
     {   // K2: T tokens x H rows
         const int rpw = kWave >> p.lpr2_log2;
-        plan_steps((gd.OUT + rpw - 1) / rpw, T, pl->smem2, &p.steps2);
-        p.rows_per_wg2 = int32_t(4 * rpw * p.steps2);
+        const int nw = moe_waves_down(pl->wide2);
+        plan_steps((gd.OUT + rpw - 1) / rpw, T, pl->smem2, nw, &p.steps2);
+        p.rows_per_wg2 = int32_t(nw * rpw * p.steps2);
         pl->grid2 = dim3(unsigned((gd.OUT + p.rows_per_wg2 - 1) / p.rows_per_wg2), unsigned(T), 1);
     }
     // Many pairs: sort once and run each projection as a grouped matrix-core
@@ -939,7 +961,8 @@ static int go_up(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
 }
 template <int D, int BITS, int GPB, bool W>
 static int go_up_split(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
-    return launch_with_lds<k_moe_up_split<D, BITS, GPB, W>>(grid, dim3(kThreads), smem, st, p);
+    return launch_with_lds<k_moe_up_split<D, BITS, GPB, W>>(grid, dim3(moe_waves_up(W) * kWave), smem,
+                                                            st, p);
 }
 // Split gate/up kernel: only the widths whose table exceeds the LDS-resident
 // limit (d2 15-16 bits, d4 14-16, d8 13-16).
@@ -956,7 +979,7 @@ static int launch_moe_up_split(const MoeParams &p, int d, int bits, int gpb, boo
 }
 template <int D, int BITS, int GPB, bool W = false>
 static int go_down(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
-    return launch_with_lds<k_moe_down<D, BITS, GPB, W>>(grid, dim3(kThreads), smem, st, p);
+    return launch_with_lds<k_moe_down<D, BITS, GPB, W>>(grid, dim3(moe_waves_down(W) * kWave), smem, st, p);
 }
 // Down kernel with the larger LDS part: the widths whose table is beyond LDS.
 #define VQK_DNW_CASE(D, B, G) \
