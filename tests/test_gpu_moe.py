@@ -144,12 +144,14 @@ def test_routing_ties_pick_lower_ids():
 
 @pytest.mark.parametrize("D,K,T,shared,E", [(8, 16384, 8, True, 32), (8, 16384, 16, False, 32),
                                             (4, 4096, 12, True, 32), (2, 512, 40, False, 32),
-                                            (8, 16384, 8, True, 64), (8, 16384, 12, False, 48)])
+                                            (8, 16384, 8, True, 64), (8, 16384, 12, False, 48),
+                                            (8, 16384, 8, False, 96)])
 def test_moe_layer_batched_grouped_path(D, K, T, shared, E):
     """T * top_k >= 64 pairs: the layer runs as one routing + one sort +
     grouped matrix-core GEMMs (SwiGLU built while down's input is staged) +
     the weighted combine; same oracle, same bar. With <= 2 pairs per expert
-    (the last two cases) the d8 tables take 4-row tiles."""
+    (the last three cases) the d8 tables take 4-row tiles; the last has fewer
+    pairs than experts (64 over 96), grouped only because of that path."""
     print(f"moe batched grouped D={D} K={K} T={T} shared={shared} E={E}", flush=True)
     rng = np.random.default_rng(20 + T + D + (E if E != 32 else 0))
     H, I, k = 1024, 256, 8

@@ -932,8 +932,10 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     // Batch >= 2 with tables beyond LDS: the sliced-codebook GEMV composition.
     // Otherwise the two fused kernels (partly LDS-staged tables).
     const int64_t N = T * k;
-    bool grouped = N >= kMoeGroupedMinPairs && N >= E && seg_ok(m->gate, N) && seg_ok(m->up, N) &&
-                   seg_ok(m->down, N);
+    // grouped: at least one pair per expert on average, or the sparser
+    // routings whose d8 tables take the persistent 4-row-tile path
+    bool grouped = N >= kMoeGroupedMinPairs && (N >= E || seg_tile_rows(m->gate, N, E) < 16) &&
+                   seg_ok(m->gate, N) && seg_ok(m->up, N) && seg_ok(m->down, N);
     if (grouped && shared)
         grouped = seg_ok(m->sh_gate, T) && seg_ok(m->sh_up, T) && seg_ok(m->sh_down, T);
     bool big = T >= 2 && big_fits(gg, m->gate) && big_fits(gu, m->up) && big_fits(gd, m->down);
