@@ -144,15 +144,20 @@ __host__ __device__ constexpr int seg_hyb_entries(int D, int TOK = kSegTok) {
 }
 
 
+// Waves of k_seg_mfma: 8 x one 16-row tile (two waves per SIMD, so one
+// decodes while the other waits on its loads), 128 weight rows per workgroup.
+constexpr int kSegWaves = 8;
+
 template <int D, int BITS, int GPB, bool CBL, int TOK = kSegTok>
-__global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
-    constexpr int TN = 2;                       // 16-row tiles per wave
+__global__ void __launch_bounds__(kSegWaves * 64) k_seg_mfma(const SegParams p) {
+    constexpr int NT = kSegWaves * 64;          // threads
+    constexpr int TN = kSegRows / (16 * kSegWaves);   // 16-row tiles per wave
     constexpr int SPB = 4 * D;                  // MFMA steps per block (8 weights each)
     constexpr int CC = 128 * D;                 // x columns per superstep
     constexpr int XS = CC + 8;                  // LDS row stride of an x chunk (halves)
     constexpr int PIECES = TOK * CC / 8;        // 16-byte pieces per chunk
-    constexpr int PPT = PIECES / 256;
-    static_assert(PIECES % 256 == 0, "chunk must split evenly over 256 threads");
+    constexpr int PPT = PIECES / NT;
+    static_assert(PIECES % NT == 0, "chunk must split evenly over the threads");
     // LDS table entries: the whole table, or the first seg_hyb_entries of it
     constexpr int CBN = CBL ? (1 << BITS) : seg_hyb_entries(D, TOK);
     static_assert(TOK == kSegTok || TOK == kSegTokNarrow, "token tile of 16 or 4 rows");
@@ -178,7 +183,7 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
         row0 = int(blockIdx.y) * TOK;
         nrows = min(TOK, p.N - row0);
     }
-    const int o0 = int(blockIdx.x) * kSegRows + wave * 32;
+    const int o0 = int(blockIdx.x) * kSegRows + wave * 16 * TN;
 
     {
         const int ent = min(p.K, CBN);
@@ -201,7 +206,7 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     int64_t xoff[PPT];
 #pragma unroll
     for (int r = 0; r < PPT; ++r) {
-        const int t = (tid + 256 * r) / (CC / 8);
+        const int t = (tid + NT * r) / (CC / 8);
         int64_t off = -1;
         if (t < nrows) {
             const int64_t row = grouped ? int64_t(p.order[row0 + t] / p.xkrep) : int64_t(row0 + t);
@@ -216,7 +221,7 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     auto load_x = [&](int sb, u32x4 (&v)[PPT]) {
 #pragma unroll
         for (int r = 0; r < PPT; ++r) {
-            const int col = sb * CC + ((tid + 256 * r) % (CC / 8)) * 8;
+            const int col = sb * CC + ((tid + NT * r) % (CC / 8)) * 8;
             const bool ok = xoff[r] >= 0 && col < p.IN;
             if (p.xg) {
                 v[r] = ok ? swiglu8(p.xg + xoff[r] + col, p.xu + xoff[r] + col) : u32x4{0, 0, 0, 0};
@@ -228,7 +233,7 @@ __global__ void __launch_bounds__(256) k_seg_mfma(const SegParams p) {
     auto store_x = [&](const u32x4 (&v)[PPT]) {
 #pragma unroll
         for (int r = 0; r < PPT; ++r) {
-            const int pc = tid + 256 * r;
+            const int pc = tid + NT * r;
             *reinterpret_cast<u32x4 *>(xs + (pc / (CC / 8)) * XS + (pc % (CC / 8)) * 8) = v[r];
         }
     };

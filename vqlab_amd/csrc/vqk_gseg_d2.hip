@@ -8,7 +8,7 @@ namespace {
 template <int BITS, int GPB>
 int go(const SegParams &p, dim3 grid, hipStream_t st) {
     constexpr bool CBL = cb_in_lds(2, BITS);
-    return launch_with_lds<k_seg_mfma<2, BITS, GPB, CBL>>(grid, dim3(256), seg_lds(2, BITS, CBL), st, p);
+    return launch_with_lds<k_seg_mfma<2, BITS, GPB, CBL>>(grid, dim3(kSegWaves * 64), seg_lds(2, BITS, CBL), st, p);
 }
 }  // namespace
 

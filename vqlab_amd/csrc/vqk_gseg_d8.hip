@@ -8,7 +8,7 @@ namespace {
 template <int BITS, int GPB>
 int go(const SegParams &p, dim3 grid, hipStream_t st) {
     constexpr bool CBL = cb_in_lds(8, BITS);
-    return launch_with_lds<k_seg_mfma<8, BITS, GPB, CBL>>(grid, dim3(256), seg_lds(8, BITS, CBL), st, p);
+    return launch_with_lds<k_seg_mfma<8, BITS, GPB, CBL>>(grid, dim3(kSegWaves * 64), seg_lds(8, BITS, CBL), st, p);
 }
 // 4-token tiles: only where the table is beyond LDS (the x chunk's room goes
 // to table entries); other widths run the 16-token kernel on those tiles.
@@ -16,7 +16,7 @@ template <int BITS, int GPB>
 int go_narrow(const SegParams &p, dim3 grid, hipStream_t st) {
     static_assert(!cb_in_lds(8, BITS), "narrow tiles only pay for tables beyond LDS");
     return launch_with_lds<k_seg_mfma<8, BITS, GPB, false, kSegTokNarrow>>(
-        grid, dim3(256), seg_lds(8, BITS, false, kSegTokNarrow), st, p);
+        grid, dim3(kSegWaves * 64), seg_lds(8, BITS, false, kSegTokNarrow), st, p);
 }
 template <int BITS, int GPB>
 int go_persist(const SegParams &p, dim3 grid, hipStream_t st) {
