@@ -159,6 +159,17 @@ def test_moe_layer_batched_grouped_path(D, K, T, shared, E):
     _check(blk, projs, sh, shv, rng, T, E, H, k)
 
 
+def test_moe_layer_batched_shared_ksplit():
+    """Batched grouped layer whose shared expert's gate / up split K (H=2048:
+    two supersteps, so two fp32 partials that the shared down adds while it
+    stages silu(g) * u); same oracle, same bar."""
+    print("moe batched shared K split", flush=True)
+    rng = np.random.default_rng(47)
+    E, H, I, k, T = 64, 2048, 256, 8, 8
+    blk, projs, sh, shv = _block(rng, E, H, I, 8, 16384, k, shared=True)
+    _check(blk, projs, sh, shv, rng, T, E, H, k)
+
+
 @pytest.mark.parametrize("E,T", [(32, 16), (64, 8)])
 def test_moe_layer_batched_skipzero(E, T):
     """The grouped layer over compact skipzero experts (20% dead rows): dead

@@ -468,6 +468,16 @@ bool seg_ok(const vqk_weights *w, int64_t N) {
            group_max_tiles(N, g.E, kSegTokNarrow) <= 65535 && N <= INT32_MAX / 2;
 }
 
+int seg_ksplit(const vqk_weights *w, int64_t N) {
+    Geom g;
+    if (make_geom(w, &g)) return 1;
+    const int64_t nss = (g.NB + 3) / 4;
+    const int64_t wgs = ((g.OUT + kSegRows - 1) / kSegRows) * ((N + kSegTok - 1) / kSegTok);
+    int64_t ks = wgs > 0 ? big_grid(int64_t(1) << 30) / wgs : 1;
+    ks = ks < 1 ? 1 : (ks > nss ? nss : ks);
+    return int(ks > 4 ? 4 : ks);
+}
+
 int seg_tile_rows(const vqk_weights *w, int64_t N, int64_t E) {
     Geom g;
     if (make_geom(w, &g)) return kSegTok;
@@ -504,6 +514,18 @@ int seg_run(const vqk_weights *w, const SegCall &c, const void *sort_ws, hipStre
     sp.y = c.y;
     sp.y_type = c.y_type;
     sp.N = int32_t(c.N);
+    if (c.xparts > 1) {
+        if (!c.xg) return set_error(VQK_EINVAL, "x partials need fp32 gate / up rows");
+        sp.xparts = c.xparts;
+        sp.xpstride = c.N * g.IN;
+    }
+    const int ks = c.ksplit > 1 ? c.ksplit : 1;
+    if (ks > 1) {
+        if (sort_ws || c.y_type != VQK_F32 || ks > 64)
+            return set_error(VQK_EINVAL, "K split needs dense rows, fp32 output, <= 64 slices");
+        sp.ksplit = ks;
+        sp.ypart = c.N * g.OUT;
+    }
     int64_t tiles = (c.N + kSegTok - 1) / kSegTok;
     int tok = kSegTok;
     if (sort_ws) {
@@ -525,7 +547,7 @@ int seg_run(const vqk_weights *w, const SegCall &c, const void *sort_ws, hipStre
         const dim3 grid(unsigned(big_grid(nxp * tiles)), 1, 1);
         return launch_seg_persist_d8(sp, g.BITS, g.gpb, grid, st);
     }
-    const dim3 grid(unsigned(nxb), unsigned(tiles), 1);
+    const dim3 grid{unsigned(nxb), unsigned(tiles), unsigned(ks)};
     return launch_seg(sp, g, tok, grid, st);
 }
 

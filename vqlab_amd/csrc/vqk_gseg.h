@@ -55,7 +55,34 @@ struct SegParams {
     const int32_t *tmeta;      // grouped: (expert or -1, row_start, nrows) per tile
     const int32_t *ntiles;     // grouped: tiles built by the sort
     const int32_t *order;      // grouped: sorted position -> pair
+    int32_t ksplit;            // K slices (blockIdx.z): slice z writes fp32 partials at y + z * ypart
+    int64_t ypart;
+    int32_t xparts;            // xg / xu given as xparts partial rows, xpstride elements apart
+    int64_t xpstride;
 };
+
+// Eight fp16 values fp16(silu(g) * u) where g and u are the fixed-order sums
+// of `np` fp32 partial rows `stride` elements apart (K-split producers).
+__device__ __forceinline__ u32x4 swiglu8_parts(const float *g, const float *u, int np,
+                                               int64_t stride) {
+    float gv[8], uv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { gv[i] = 0.f; uv[i] = 0.f; }
+    for (int q = 0; q < np; ++q) {
+        const f32x4 *gq = reinterpret_cast<const f32x4 *>(g + q * stride);
+        const f32x4 *uq = reinterpret_cast<const f32x4 *>(u + q * stride);
+        const f32x4 g0 = gq[0], g1 = gq[1], u0 = uq[0], u1 = uq[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            gv[i] += g0[i]; gv[4 + i] += g1[i];
+            uv[i] += u0[i]; uv[4 + i] += u1[i];
+        }
+    }
+    uint32_t h[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = f32_to_h(gv[i] / (1.f + __expf(-gv[i])) * uv[i]);
+    return u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+}
 
 constexpr int kSegRows = 128;      // weight rows per workgroup
 constexpr int kSegTok = 16;        // tokens per tile
@@ -216,6 +243,9 @@ __global__ void __launch_bounds__(kSegWaves * 64) k_seg_mfma(const SegParams p) 
     }
 
     const int NSS = (p.NB + 3) >> 2;
+    // K slice of this workgroup: supersteps [sb0, sb1) (all of them unless split)
+    const int ks = p.ksplit > 1 ? p.ksplit : 1, per = (NSS + ks - 1) / ks;
+    const int sb0 = min(NSS, int(blockIdx.z) * per), sb1 = min(NSS, sb0 + per);
     const uint32_t kmax = uint32_t(p.K - 1);
 
     auto load_x = [&](int sb, u32x4 (&v)[PPT]) {
@@ -224,7 +254,10 @@ __global__ void __launch_bounds__(kSegWaves * 64) k_seg_mfma(const SegParams p) 
             const int col = sb * CC + ((tid + NT * r) % (CC / 8)) * 8;
             const bool ok = xoff[r] >= 0 && col < p.IN;
             if (p.xg) {
-                v[r] = ok ? swiglu8(p.xg + xoff[r] + col, p.xu + xoff[r] + col) : u32x4{0, 0, 0, 0};
+                v[r] = !ok ? u32x4{0, 0, 0, 0}
+                     : p.xparts > 1 ? swiglu8_parts(p.xg + xoff[r] + col, p.xu + xoff[r] + col,
+                                                    p.xparts, p.xpstride)
+                                    : swiglu8(p.xg + xoff[r] + col, p.xu + xoff[r] + col);
             } else {
                 v[r] = ok ? load8_act(p.x, p.x_type, xoff[r] + col) : u32x4{0, 0, 0, 0};
             }
@@ -307,13 +340,15 @@ __global__ void __launch_bounds__(kSegWaves * 64) k_seg_mfma(const SegParams p) 
     // entries instead): the next superstep's x and weights are loaded into
     // registers before the current one multiplies, so their latency stays
     // hidden; the chunk is overwritten between two barriers.
-    load_x(0, xr);
-    load_w(0, w0, s0, l0);
-    store_x(xr);
+    if (sb0 < sb1) {
+        load_x(sb0, xr);
+        load_w(sb0, w0, s0, l0);
+        store_x(xr);
+    }
     wait_vmem();
     __syncthreads();
-    for (int sb = 0; sb < NSS; sb += 2) {
-        const bool more1 = sb + 1 < NSS;
+    for (int sb = sb0; sb < sb1; sb += 2) {
+        const bool more1 = sb + 1 < sb1;
         if (more1) {
             load_x(sb + 1, xr);
             load_w(sb + 1, w1, s1, l1);
@@ -323,7 +358,7 @@ __global__ void __launch_bounds__(kSegWaves * 64) k_seg_mfma(const SegParams p) 
         __syncthreads();                        // every wave is done with chunk sb
         store_x(xr);
         __syncthreads();                        // chunk sb + 1 is in place
-        const bool more2 = sb + 2 < NSS;
+        const bool more2 = sb + 2 < sb1;
         if (more2) {
             load_x(sb + 2, xr);
             load_w(sb + 2, w0, s0, l0);
@@ -339,6 +374,7 @@ __global__ void __launch_bounds__(kSegWaves * 64) k_seg_mfma(const SegParams p) 
     uint64_t alive[TN];
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) alive[tn] = __ballot(cr[tn] >= 0);
+    const int64_t yoff = ks > 1 ? int64_t(blockIdx.z) * p.ypart : 0;   // K slice's partial
     if (ln < nrows) {
         const int64_t yr = grouped ? int64_t(p.order[row0 + ln]) : int64_t(row0 + ln);
 #pragma unroll
@@ -349,7 +385,7 @@ __global__ void __launch_bounds__(kSegWaves * 64) k_seg_mfma(const SegParams p) 
                 const int o = o0 + r;
                 if (o < p.OUT) {
                     const float v = ((alive[tn] >> (r - 16 * tn)) & 1) ? acc[tn][i] : 0.f;
-                    store_act(p.y, p.y_type, yr * p.OUT + o, v);
+                    store_act(p.y, p.y_type, yoff + yr * p.OUT + o, v);
                 }
             }
         }

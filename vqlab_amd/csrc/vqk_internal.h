@@ -33,12 +33,19 @@ struct SegCall {
     int32_t y_type;
     int64_t N;                 // pairs (sorted) or dense rows (sort_ws == NULL)
     int32_t tok;               // sorted: the sort's tile rows (seg_tile_rows); 0 = 16
+    int32_t ksplit;            // dense rows only: K slices, y holds ksplit fp32 partials
+                               //   [ksplit][N][OUT] (0 or 1: no split)
+    int32_t xparts;            // xg / xu hold xparts partial rows [xparts][N][IN] to add
 };
 
 // Rows per tile to sort N pairs into for module `w` over E experts: 4 when
 // the routing puts at most ~2 pairs on an expert on average and w's d8 table
 // is beyond LDS (more of it fits beside a 4-row x chunk), else 16.
 int seg_tile_rows(const vqk_weights *w, int64_t N, int64_t E);
+
+// K slices for the segment kernel over N dense rows of `w`: enough that the
+// launch fills the CUs once (at most 4 and the module's supersteps).
+int seg_ksplit(const vqk_weights *w, int64_t N);
 
 // Workspace of seg_sort for N pairs over E experts.
 size_t seg_sort_bytes(int64_t N, int64_t E);

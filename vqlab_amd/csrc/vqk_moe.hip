@@ -766,11 +766,13 @@ static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I, int64_t H, int p
         L.total = align_up(L.us + 4 * size_t(T) * P * I);
     }
     if (path != kMoeFused) {
+        // grouped: the shared gate / up rows as up to 4 K-slice partials
+        const size_t nsh = path == kMoeGrouped ? 4 : 1;
         L.g = L.total;
         L.u = align_up(L.g + 4 * size_t(T) * k * I);
         L.sgg = align_up(L.u + 4 * size_t(T) * k * I);
-        L.sgu = align_up(L.sgg + 4 * size_t(T) * I);
-        L.yd = align_up(L.sgu + 4 * size_t(T) * I);
+        L.sgu = align_up(L.sgg + 4 * nsh * size_t(T) * I);
+        L.yd = align_up(L.sgu + 4 * nsh * size_t(T) * I);
         L.ysh = align_up(L.yd + 4 * size_t(T) * k * H);
         L.total = align_up(L.ysh + 4 * size_t(T) * H);
     }
@@ -1122,11 +1124,15 @@ static int launch_moe_grouped(const vqk_moe_desc *m, const MoePlan &pl, uint8_t 
     SegCall d{nullptr, VQK_F32, g, u, 1, yd, VQK_F32, N, tok};
     if ((rc = seg_run(m->down, d, sort, st))) return rc;
     if (p.shared) {
-        SegCall cs{p.x, p.x_type, nullptr, nullptr, 1, sgg, VQK_F32, T};
+        // the shared expert is one expert over T rows: its gate / up launches
+        // alone would fill few CUs, so they split K (fp32 partials that the
+        // down launch adds in a fixed order as it stages its input)
+        const int ks = seg_ksplit(m->sh_gate, T);
+        SegCall cs{p.x, p.x_type, nullptr, nullptr, 1, sgg, VQK_F32, T, 0, ks};
         if ((rc = seg_run(m->sh_gate, cs, nullptr, st))) return rc;
         cs.y = sgu;
         if ((rc = seg_run(m->sh_up, cs, nullptr, st))) return rc;
-        SegCall ds{nullptr, VQK_F32, sgg, sgu, 1, ysh, VQK_F32, T};
+        SegCall ds{nullptr, VQK_F32, sgg, sgu, 1, ysh, VQK_F32, T, 0, 0, ks};
         if ((rc = seg_run(m->sh_down, ds, nullptr, st))) return rc;
     }
     hipLaunchKernelGGL(k_moe_combine, dim3(unsigned((p.H + 255) / 256), unsigned(T)), dim3(256), 0, st,
