@@ -114,7 +114,16 @@ __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
             // the entry as ONE vector load (D * 2 bytes): a gather per half
             // would multiply the L2 requests that bound this kernel
             uint16_t e[D];
-            __builtin_memcpy(e, a.codebook + int64_t(c) * D, sizeof e);
+            if constexpr (D == 8) {                  // through the global address space
+                const u32x4 ev = load_global(reinterpret_cast<const u32x4 *>(a.codebook), int64_t(c));
+                __builtin_memcpy(e, &ev, sizeof e);
+            } else if constexpr (D == 4) {
+                const u32x2 ev = load_global(reinterpret_cast<const u32x2 *>(a.codebook), int64_t(c));
+                __builtin_memcpy(e, &ev, sizeof e);
+            } else {
+                const uint32_t ev = load_global(reinterpret_cast<const uint32_t *>(a.codebook), int64_t(c));
+                __builtin_memcpy(e, &ev, sizeof e);
+            }
 #pragma unroll
             for (int u = 0; u < D; ++u) {
                 // a group boundary can fall inside a subvector only if G % D != 0,
@@ -143,9 +152,13 @@ __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
     }
 }
 
-static dim3 rows_grid(int64_t cols, int64_t rows) {
+// Threads stride over the rows (`rpt` rows each where rows allow): fewer,
+// longer-lived waves than one row per thread, whose tiny workgroups cost
+// more to dispatch than their single gather.
+static dim3 rows_grid(int64_t cols, int64_t rows, int64_t rpt = 1) {
     const int64_t gx = (cols + 255) / 256;
-    const int64_t gy = rows < 65535 ? (rows > 0 ? rows : 1) : 65535;
+    int64_t gy = (rows + rpt - 1) / rpt;
+    gy = gy < 1 ? 1 : (gy > 65535 ? 65535 : gy);
     return dim3(unsigned(gx), unsigned(gy), 1);
 }
 
@@ -170,7 +183,7 @@ static int launch_dequant(const vqk_weights *w, const Geom &g, const uint32_t *e
     a.r0 = r0; a.rows = rows;
     a.out = out;
     if (rows == 0) return VQK_OK;
-    const dim3 grid = rows_grid(g.NSUB, rows);
+    const dim3 grid = rows_grid(g.NSUB, rows, 4);
     switch (g.D) {
         case 2: hipLaunchKernelGGL(k_dequant<2>, grid, dim3(256), 0, st, a); break;
         case 4: hipLaunchKernelGGL(k_dequant<4>, grid, dim3(256), 0, st, a); break;
