@@ -135,6 +135,22 @@ def _w(L, **kw):
     return w
 
 
+@pytest.mark.parametrize("N,E", [(640, 512), (64, 96), (700, 40), (1, 1)])
+def test_grouped_workspace_layout(L, N, E):
+    """vqk_grouped_gemm_workspace (host only): the pair order, room for the
+    tile records of the smallest tiles the sort builds (4 rows: the sparse
+    routings over d8 tables beyond LDS; ceil(N/4) + min(N, E + 1) records of
+    3 int32), the tile count -- each 256-byte aligned, as the GPU tests read
+    the sort's output back."""
+    w = _w(L, D=8, K=16384, pack_bits=14, E=E, OUT=1024, IN=4096,
+           code_cols=vo.words_per_row(512, 14))
+    ws = ctypes.c_size_t()
+    assert L.lib().vqk_grouped_gemm_workspace(ctypes.byref(w), N, ctypes.byref(ws)) == L.VQK_OK
+    al = lambda v: (v + 255) & ~255
+    room = (N + 3) // 4 + min(N, E + 1)
+    assert ws.value == al(4 * N) + al(12 * room) + 256
+
+
 @pytest.mark.parametrize("kw,rc", [
     ({"D": 3}, 1),                          # NotImplementedError: no kernel for d=3
     ({"code_cols": 5}, 2),                  # ValueError: WPR mismatch
