@@ -21,8 +21,8 @@
 // past the staged part: lanes without a block (dead skipzero row, past the
 // row's end) decode code 0 from it with scale 0, i.e. weights +0.
 //
-// Workgroup = 4 waves x 2 row tiles of 16 = 128 weight rows; one token tile
-// of <= 16 rows (grouped: one tile of an expert segment from the device
+// Workgroup = 8 waves x one row tile of 16 = 128 weight rows (two waves per
+// SIMD); one token tile of <= 16 rows (grouped: one tile of an expert segment from the device
 // sort, vq_switch.py:4590-4610; dense: 16 consecutive rows of x). The K loop
 // walks supersteps of 4 blocks per row (128 * D columns); the x columns of
 // the next superstep and the next blocks' words are loaded while the
