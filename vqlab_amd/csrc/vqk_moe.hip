@@ -269,7 +269,8 @@ constexpr int kHybDownBytes = 112 * 1024;
 constexpr int kHybDownWideBytes = 136 * 1024;
 // Waves of the workgroups with the larger LDS parts (one workgroup per CU),
 // which read x from LDS: two per SIMD, so one wave decodes while the other
-// waits on its table reads (12 for gate / up measured no faster).
+// waits on its table reads (12 for gate / up measured no faster, 16 for down
+// slower: it spills).
 constexpr int kWideWavesUp = 8, kWideWavesDown = 8;
 __host__ __device__ constexpr int moe_waves_up(bool wide) { return wide ? kWideWavesUp : kThreads / kWave; }
 __host__ __device__ constexpr int moe_waves_down(bool wide) {
