@@ -34,7 +34,13 @@ Pinning (what checks each function; see tests/test_oracle.py):
                    (one-hot codebook, constant scales).
   route            brute-force sort; weights sum to one; softmax invariance.
   moe_layer        identical-expert invariant (combine of equal experts ==
-                   one expert), per-pair loop restatement.
+                   one expert), per-pair loop restatement; the shared-expert
+                   term by closed forms (shared expert == the only routed
+                   expert: a zero gate vector gives exactly 1.5x the routed
+                   output, gate logits of +-1000 give 2x and 1x) in both
+                   rounding modes.
+  bf16_round,      torch's own float32 -> bfloat16 / float16 conversions
+  fp16_round       over 200k random bit patterns, bf16 ties and specials.
   skipzero         reference golden sha256 prefixes (sz_codes, sz_scales,
                    sz_rowmask, sz_shape) + cumsum brute force for the table.
   tile_meta        the reference test's double loop, restated.
@@ -158,8 +164,14 @@ def dequant(codes: np.ndarray, codebook: np.ndarray, scales: np.ndarray,
     d = cb.shape[1]
     lead, nsub = codes.shape[:-1], codes.shape[-1]
     w = cb[codes].reshape(lead + (nsub * d,))
-    sx = np.repeat(s, group, axis=-1)[..., : nsub * d]
+    ngrp = s.shape[-1]
     with np.errstate(invalid="ignore", over="ignore"):
+        if ngrp * group == nsub * d:
+            # whole groups: broadcast each scale over its group (same products,
+            # no repeated scale array)
+            prod = w.reshape(lead + (ngrp, group)) * s[..., None]
+            return prod.astype(np.float16).reshape(lead + (nsub * d,))
+        sx = np.repeat(s, group, axis=-1)[..., : nsub * d]
         return (w * sx).astype(np.float16)
 
 
@@ -231,9 +243,27 @@ def sigmoid(v):
     return 1.0 / (1.0 + np.exp(-v))
 
 
+def bf16_round(v) -> np.ndarray:
+    """Values -> the float64 values of their bfloat16 roundings: one RNE of
+    the float32 value to 8 significand bits (what `.astype(bfloat16)` does to
+    an fp32 array); NaN stays NaN."""
+    u = np.asarray(v, np.float64).astype(np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, (u >> 16) | 0x40, r)
+    return (r.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def fp16_round(v) -> np.ndarray:
+    """float64 -> float32 -> fp16 (RNE) -> float64: a kernel's fp32
+    accumulator stored as an fp16 output."""
+    with np.errstate(over="ignore"):
+        return np.asarray(v, np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
+
+
 def moe_layer(x, logits, gate, up, down, top_k, norm=True, shared=None,
-              shared_gate=None, h_round=None):
-    """Qwen-style SparseMoeBlock over VQ experts, float64 throughout.
+              shared_gate=None, h_round=None, rounding=None):
+    """Qwen-style SparseMoeBlock over VQ experts.
 
     y[t] = sum_j w[t,j] * down_e(silu(gate_e(x_t)) * up_e(x_t))
            + sigmoid(shared_gate . x_t) * shared(x_t)
@@ -241,9 +271,23 @@ def moe_layer(x, logits, gate, up, down, top_k, norm=True, shared=None,
 
     gate/up/down are dicts {codes (unpacked [E,OUT,NSUB]), codebook, scales,
     group}; shared, if given, is a dict of three such (E=1) and shared_gate a
-    float vector [H]. h_round: None, or a numpy float dtype the SwiGLU
-    intermediate is rounded to before down_proj (the kernels hand down_proj an
-    fp16 activation, like the reference's fp16 x cast, vq_switch.py:5306-5308).
+    float vector [H].
+
+    Rounding of the intermediates (the dot products are float64 over the
+    exact fp16 weights either way):
+      rounding=None      float64 throughout; h_round, if given, is a numpy
+                         float dtype the SwiGLU intermediate is rounded to
+                         before down_proj (the fused kernels hand down_proj an
+                         fp16 activation).
+      rounding="reference"  the rounding points of the reference's bf16
+                         decode path: each VQSwitchLinear's fp32 accumulator
+                         leaves its kernel as fp16 and is cast back to x's
+                         dtype, bf16 (vq_switch.py:5306-5308, 5423); SwiGLU
+                         runs in bf16 (silu = g * sigmoid(g), each op rounded);
+                         down_proj's bf16 input is cast to fp16 again; the
+                         shared gate linear and its sigmoid give bf16
+                         (decode_ladder.py:117-125); the weighted sum over
+                         experts is float (scores are fp32 router outputs).
     Returns (y [T, H] float64, ids, weights).
     """
     x = np.asarray(x, np.float32).astype(np.float64)
@@ -252,6 +296,9 @@ def moe_layer(x, logits, gate, up, down, top_k, norm=True, shared=None,
     H = down["codes"].shape[1]
     y = np.zeros((T, H), np.float64)
     wcache = {}
+    ref = rounding == "reference"
+    if rounding not in (None, "reference"):
+        raise ValueError(f"unknown rounding {rounding!r}")
 
     def W(p, e):
         key = (id(p), e)
@@ -260,18 +307,28 @@ def moe_layer(x, logits, gate, up, down, top_k, norm=True, shared=None,
                                   p["group"]).astype(np.float64)
         return wcache[key]
 
+    def lin(p, e, v):
+        out = W(p, e) @ v
+        return bf16_round(fp16_round(out)) if ref else out
+
     def mlp(xt, g, u, dn, e):
-        h = silu(W(g, e) @ xt) * (W(u, e) @ xt)
-        if h_round is not None:
-            h = h.astype(h_round).astype(np.float64)
-        return W(dn, e) @ h
+        gv, uv = lin(g, e, xt), lin(u, e, xt)
+        if ref:
+            h = bf16_round(bf16_round(gv * bf16_round(sigmoid(gv))) * uv)
+            h = fp16_round(h)
+        else:
+            h = silu(gv) * uv
+            if h_round is not None:
+                h = h.astype(h_round).astype(np.float64)
+        return lin(dn, e, h)
 
     for t in range(T):
         for j in range(top_k):
             e = int(ids[t, j])
             y[t] += w[t, j] * mlp(x[t], gate, up, down, e)
         if shared is not None:
-            sg = sigmoid(float(np.asarray(shared_gate, np.float64) @ x[t]))
+            z = float(np.asarray(shared_gate, np.float64) @ x[t])
+            sg = float(bf16_round(sigmoid(bf16_round(z)))) if ref else sigmoid(z)
             y[t] += sg * mlp(x[t], shared["gate"], shared["up"], shared["down"], 0)
     return y, ids, w
 
