@@ -5,8 +5,8 @@
  * Every entry point validates its arguments on the host and returns a status
  * before anything is launched; no entry point allocates device memory --
  * callers that need scratch pass a workspace sized by the matching
- * *_workspace query. Kernels are re-entrant; the library keeps no mutable
- * global state besides a per-thread error message.
+ * *_workspace query (the one exception, vqk_moe_decode_layer_noalloc, uses
+ * a library-owned device array instead). Kernels are re-entrant.
  *
  * Each entry point cites the reference interface it replaces (paths are
  * relative to the reference checkout; vq_switch.py, vq_dense.py and vq_pack.py
@@ -192,6 +192,23 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type,
                          int64_t T, const float *logits, void *y,
                          int32_t y_type, int32_t *topk_ids, float *topk_w,
                          void *workspace, size_t ws_bytes, void *stream);
+
+/* ---- no-allocation variant of vqk_moe_decode_layer ------------------------
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments, results and errors as
+ * vqk_moe_decode_layer, without the workspace: the layer's scratch is a
+ * library-owned device array of VQK_NOALLOC_SCRATCH_BYTES per GPU, taken when
+ * the library is loaded on that GPU and held until the process ends. A call
+ * whose workspace (vqk_moe_decode_layer_workspace) exceeds it returns
+ * VQK_ENOSPACE before any launch (config 4 at T = 64 needs about 19 MB).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (two streams, two threads) race and must be serialised by the caller.
+ * The stream must belong to the current device (else VQK_EINVAL). */
+#define VQK_NOALLOC_SCRATCH_BYTES (32u << 20)
+int vqk_moe_decode_layer_noalloc(const vqk_moe_desc *m, const void *x, int32_t x_type,
+                                 int64_t T, const float *logits, void *y, int32_t y_type,
+                                 int32_t *topk_ids, float *topk_w, void *stream);
 
 /* ---- gather-only embeddings: VQEmbedding.__call__ (vq_dense.py:444-502) and
  * VQPLEEmbedding.__call__ (vq_switch.py:5426-5495) ------------------------------

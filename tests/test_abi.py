@@ -266,3 +266,11 @@ def test_codebook_staging_stays_in_its_table(D, BITS, NT):
         for K in {1 << BITS, (1 << BITS) - 8, 8}:
             got, pieces, valid = _staged_pieces(K, D, CBN, NT)
             assert got == set(range(valid)) and max(got, default=0) < pieces
+
+
+def test_noalloc_scratch_size_matches_header(L):
+    """The Python mirror of VQK_NOALLOC_SCRATCH_BYTES is the header's value."""
+    txt = (ROOT / "include" / "vqk.h").read_text()
+    m = re.search(r"#define\s+VQK_NOALLOC_SCRATCH_BYTES\s+\((\d+)u\s*<<\s*(\d+)\)", txt)
+    assert m, "VQK_NOALLOC_SCRATCH_BYTES not found"
+    assert int(m.group(1)) << int(m.group(2)) == L.VQK_NOALLOC_SCRATCH_BYTES

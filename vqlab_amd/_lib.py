@@ -16,6 +16,7 @@ LIB_PATH = pathlib.Path(os.environ.get("VQK_LIBRARY") or
 
 VQK_OK, VQK_ENOTIMPL, VQK_EINVAL, VQK_ESHARDED, VQK_EDEVICE, VQK_ENOSPACE = range(6)
 VQK_F16, VQK_BF16, VQK_F32, VQK_U8, VQK_U16, VQK_U32, VQK_I32, VQK_I64 = range(8)
+VQK_NOALLOC_SCRATCH_BYTES = 32 << 20     # include/vqk.h
 
 c_i32, c_i64, c_p, c_sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
 
@@ -63,6 +64,8 @@ SIGNATURES = {
                                                ctypes.POINTER(c_sz)]),
     "vqk_moe_decode_layer": (c_i32, [ctypes.POINTER(VQKMoeDesc), c_p, c_i32, c_i64, c_p, c_p,
                                      c_i32, c_p, c_p, c_p, c_sz, c_p]),
+    "vqk_moe_decode_layer_noalloc": (c_i32, [ctypes.POINTER(VQKMoeDesc), c_p, c_i32, c_i64, c_p,
+                                             c_p, c_i32, c_p, c_p, c_p]),
     "vqk_embed_gather": (c_i32, [ctypes.POINTER(VQKWeights), c_p, c_i32, c_i64, c_p, c_i32,
                                  c_p]),
     "vqk_dense_fits": (c_i32, [c_i64, c_i64, c_i32, c_i32]),

@@ -16,6 +16,8 @@
 //               token's experts; each lane scales its partial by the router
 //               weight and the butterfly reduction IS the combine -- no
 //               atomics, deterministic.
+#include <mutex>
+
 #include "vqk_gemv.h"
 #include "vqk_internal.h"
 #include "vqk_big.h"
@@ -1141,6 +1143,47 @@ static int launch_moe_grouped(const vqk_moe_desc *m, const MoePlan &pl, uint8_t 
     return hip_status(hipGetLastError(), "combine launch");
 }
 
+// ------------------------------------------------ no-allocation scratch
+// The workspace of vqk_moe_decode_layer_noalloc: a fixed device array, one
+// copy per GPU, held until the process ends. Host code never uses the
+// array's name as an address (in host code it names a host-side stand-in);
+// the device address comes from hipGetSymbolAddress, once per device, with
+// that device current.
+static __device__ __align__(256) uint8_t scratch[VQK_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of the current device's scratch array; `stream` (NULL or a
+// stream of the current device) is checked against that device.
+static int scratch_of_current_device(void *stream, void **out) {
+    int dev = -1;
+    int rc = hip_status(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return set_error(VQK_EDEVICE, "device %d outside the scratch table (%d devices)", dev,
+                         kMaxScratchDevices);
+    if (stream) {
+        int sdev = -1;
+        if ((rc = hip_status(hipStreamGetDevice(hipStream_t(stream), &sdev), "hipStreamGetDevice")))
+            return rc;
+        if (sdev != dev)
+            return set_error(VQK_EINVAL, "stream belongs to device %d, the current device is %d",
+                             sdev, dev);
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if ((rc = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress")))
+            return rc;
+        if (!p) return set_error(VQK_EDEVICE, "scratch array has no device address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return VQK_OK;
+}
+
 }  // namespace vqk
 
 using namespace vqk;
@@ -1196,6 +1239,23 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, i
     if (rc) return rc;
     if (pl.wide2) return launch_moe_down_wide(p, pl.g2.D, pl.g2.BITS, pl.g2.gpb, pl.grid2, pl.smem2, st);
     return launch_moe_down(p, pl.g2.D, pl.g2.BITS, pl.g2.gpb, pl.grid2, pl.smem2, st);
+}
+
+int vqk_moe_decode_layer_noalloc(const vqk_moe_desc *m, const void *x, int32_t x_type, int64_t T,
+                                 const float *logits, void *y, int32_t y_type, int32_t *topk_ids,
+                                 float *topk_w, void *stream) {
+    MoePlan pl;
+    int rc = moe_plan(m, T, &pl);
+    if (rc) return rc;
+    if (pl.lay.total > size_t(VQK_NOALLOC_SCRATCH_BYTES))
+        return set_error(VQK_ENOSPACE,
+                         "layer call needs %zu B of scratch; the no-allocation entry point has %zu B "
+                         "(use vqk_moe_decode_layer with a workspace)",
+                         pl.lay.total, size_t(VQK_NOALLOC_SCRATCH_BYTES));
+    void *ws = nullptr;
+    if ((rc = scratch_of_current_device(stream, &ws))) return rc;
+    return vqk_moe_decode_layer(m, x, x_type, T, logits, y, y_type, topk_ids, topk_w, ws,
+                                size_t(VQK_NOALLOC_SCRATCH_BYTES), stream);
 }
 
 }  // extern "C"
