@@ -168,3 +168,46 @@ def test_loaded_modules_match_oracle_on_gpu(tmp_path, form):
             ref = vo.f16_to_bf16(vo.embed_rows(ids, src["_codes"], src["codebook"],
                                                src["vq_scales"], G))
             assert np.array_equal(got.cpu().view(torch.int16).numpy().view(np.uint16), ref), p
+
+
+def test_skipzero_weights_converts_state_dicts(tmp_path):
+    """vq_switch.skipzero_weights (vq_switch.py:4988-5013) over the reference
+    golden's skipzero tensors: {p}.sz_* become compact codes / scales + the
+    row table, other tensors pass through, a list stays a list, the module
+    entry is found under the other module-tree spelling, weights without sz_
+    tensors come back unchanged, and incomplete or inconsistent tensors are
+    refused."""
+    from safetensors.numpy import load_file
+    from vqlab_amd.vq_switch import skipzero_weights
+    cfg, mods = af.write(tmp_path, "sz_pack")
+    flat = {}
+    for f in sorted(tmp_path.glob("*.safetensors")):
+        flat.update({k: torch.from_numpy(v) for k, v in load_file(str(f)).items()})
+    szmods = cfg["vq_skipzero"]["modules"]
+    out = skipzero_weights(flat, szmods)
+    assert isinstance(out, dict) and not any(".sz_" in k for k in out)
+    for p, spec in szmods.items():
+        c = vo.skipzero_compact(mods[p]["codes"], mods[p]["vq_scales"])
+        assert np.array_equal(_np(out[p + ".codes"]), c["sz_codes"])
+        assert np.array_equal(_np(out[p + ".vq_scales"]), c["sz_scales"])
+        assert np.array_equal(out[p + ".row_table"].numpy(),
+                              vo.skipzero_row_table(c["sz_rowmask"], spec["experts"], spec["out"]))
+    passthru = [k for k in flat if ".sz_" not in k]
+    assert all(out[k] is flat[k] for k in passthru)
+    # list in, list out; module entries spelled in the other layout
+    other = {k.replace("model.language_model.", "language_model.model."): v
+             for k, v in szmods.items()}
+    lst = skipzero_weights(list(flat.items()), other)
+    assert isinstance(lst, list) and dict(lst).keys() == out.keys()
+    # nothing to convert: the same object back
+    plain = {k: flat[k] for k in passthru}
+    assert skipzero_weights(plain, szmods) is plain
+    # a missing mask, and a compact row count the mask disagrees with
+    p = next(iter(szmods))
+    broken = {k: v for k, v in flat.items() if k != p + ".sz_rowmask"}
+    with pytest.raises(KeyError, match="missing"):
+        skipzero_weights(broken, szmods)
+    bad = dict(flat)
+    bad[p + ".sz_codes"] = flat[p + ".sz_codes"][1:]
+    with pytest.raises(ValueError, match="live rows"):
+        skipzero_weights(bad, szmods)

@@ -151,6 +151,76 @@ class _Reader:
         self._open.clear()
 
 
+# ------------------------------------------------------------- skipzero
+# On-disk tensors of one skipzero module (docs/SKIPZERO.md in the reference):
+# live rows of codes / scales, the [E, ceil(OUT/8)] live-row bit mask and the
+# [E, OUT, W, NGRP] shape record.
+SZ_SUFFIXES = (".sz_codes", ".sz_scales", ".sz_rowmask", ".sz_shape")
+
+
+def skipzero_module(q, parts, E, OUT):
+    """One module's skipzero tensors (`parts`: suffix -> tensor) -> (compact
+    codes, compact scales, row table [E, OUT] int32) after checking the mask
+    against (E, OUT), the shape record against the mask, and the compact
+    row counts against the mask's live rows."""
+    missing = [suf for suf in (".sz_codes", ".sz_scales", ".sz_rowmask") if suf not in parts]
+    if missing:
+        raise KeyError(f"{q}: skipzero tensors incomplete, missing {missing}")
+    mask = parts[".sz_rowmask"]
+    _expect(q + ".sz_rowmask", mask, (E, (OUT + 7) // 8), (torch.uint8,))
+    if ".sz_shape" in parts:
+        shp = [int(v) for v in torch.as_tensor(parts[".sz_shape"]).reshape(-1).tolist()]
+        if shp[:2] != [E, OUT]:
+            raise ValueError(f"{q}.sz_shape {shp} disagrees with (experts, out) = ({E}, {OUT})")
+    table = skipzero_row_table(mask, E, OUT)
+    n_live = int((table >= 0).sum())
+    codes, sc = parts[".sz_codes"], parts[".sz_scales"]
+    for suf, t in ((".sz_codes", codes), (".sz_scales", sc)):
+        if t.ndim != 2 or t.shape[0] != n_live:
+            raise ValueError(f"{q}{suf}: {tuple(t.shape)} rows, the mask has {n_live} live rows")
+    return codes, sc, table
+
+
+def _layout_match(modules, prefix):
+    """The vq_skipzero entry of a tensor prefix: exact, else the one entry
+    that names the same module in the other module-tree spelling."""
+    if prefix in modules:
+        return modules[prefix]
+    want = _strip(prefix)
+    hits = [v for k, v in modules.items() if _strip(k) == want]
+    if len(hits) != 1:
+        raise KeyError(f"skipzero tensors for {prefix!r} match {len(hits)} vq_skipzero entries")
+    return hits[0]
+
+
+def convert_skipzero(weights, modules):
+    """On-disk skipzero tensors -> what VQSwitchLinear(row_table=...) loads
+    (the reference's skipzero_weights, vq_switch.py:4988-5013): each module's
+    {p}.sz_* tensors become {p}.codes / {p}.vq_scales (compact rows) and
+    {p}.row_table; every other tensor passes through unchanged, and weights
+    without skipzero tensors come back as given. `weights` is a dict or a
+    list of (key, tensor) pairs (the same kind is returned); `modules` maps
+    module prefixes to their vq_skipzero entries (experts, out)."""
+    pairs = list(weights.items()) if isinstance(weights, dict) else list(weights)
+    groups, kept = {}, []
+    for key, val in pairs:
+        suf = next((s for s in SZ_SUFFIXES if key.endswith(s)), None)
+        if suf is None:
+            kept.append((key, val))
+        else:
+            groups.setdefault(key[: -len(suf)], {})[suf] = val
+    if not groups:
+        return weights
+    for prefix, parts in groups.items():
+        entry = _layout_match(modules, prefix)
+        codes, sc, table = skipzero_module(prefix, parts, int(entry["experts"]),
+                                           int(entry["out"]))
+        dev = codes.device if isinstance(codes, torch.Tensor) else None
+        kept += [(prefix + ".codes", codes), (prefix + ".vq_scales", sc),
+                 (prefix + ".row_table", table.to(dev) if dev is not None else table)]
+    return dict(kept) if isinstance(weights, dict) else kept
+
+
 def _build(path, kind, spec, rd, sz_mods, device, out_dtype):
     q = _tensor_prefix(path, rd.smap)
     g = int(spec["group"])
@@ -176,21 +246,13 @@ def _build(path, kind, spec, rd, sz_mods, device, out_dtype):
     infeat = IN if pb else None
     if kind == "switch" and q + ".sz_rowmask" in rd:
         # skipzero: compact live rows + [E, OUT] row table (vq_switch.py:4988-5013)
-        E, OUT = int(spec["experts"]), int(spec["out"])
         szm = sz_mods.get(path, {})
-        E, OUT = int(szm.get("experts", E)), int(szm.get("out", OUT))
-        mask = rd.get(q + ".sz_rowmask")
-        _expect(q + ".sz_rowmask", mask, (E, (OUT + 7) // 8), (torch.uint8,))
-        if q + ".sz_shape" in rd:
-            shp = [int(v) for v in rd.get(q + ".sz_shape").tolist()]
-            if shp[:2] != [E, OUT]:
-                raise ValueError(f"{q}.sz_shape {shp} disagrees with the config's "
-                                 f"(experts, out) = ({E}, {OUT})")
-        table = skipzero_row_table(mask, E, OUT)
-        n_live = int((table >= 0).sum())
-        codes, sc = rd.get(q + ".sz_codes"), rd.get(q + ".sz_scales")
-        _expect(q + ".sz_codes", codes, (n_live, cols), cdt)
-        _expect(q + ".sz_scales", sc, (n_live, IN // g), (torch.float16,))
+        E = int(szm.get("experts", spec["experts"]))
+        OUT = int(szm.get("out", spec["out"]))
+        parts = {suf: rd.get(q + suf) for suf in SZ_SUFFIXES if q + suf in rd}
+        codes, sc, table = skipzero_module(q, parts, E, OUT)
+        _expect(q + ".sz_codes", codes, (codes.shape[0], cols), cdt)
+        _expect(q + ".sz_scales", sc, (codes.shape[0], IN // g), (torch.float16,))
         return VQSwitchLinear(_as_kernel_codes(codes).to(device), cb, sc.to(device),
                               group_size=g, pack_bits=pb, in_features=infeat,
                               row_table=table.to(device))

@@ -174,23 +174,10 @@ def skipzero_row_table(rowmask, E, OUT):
 
 def skipzero_weights(weights, modules):
     """On-disk skipzero tensors -> what VQSwitchLinear(row_table=...) loads
-    (vq_switch.py:4988-5013): {p}.sz_codes / sz_scales / sz_rowmask become
-    {p}.codes / vq_scales (compact) and {p}.row_table. `modules` maps the
-    prefix to its vq_skipzero entry (experts, out)."""
-    as_list = not isinstance(weights, dict)
-    d = dict(weights)
-    pre = [k[: -len(".sz_rowmask")] for k in d if k.endswith(".sz_rowmask")]
-    if not pre:
-        return weights
-    out = {k: v for k, v in d.items() if ".sz_" not in k}
-    for p in pre:
-        m = modules[p] if p in modules else next(
-            v for k, v in modules.items() if k.endswith(p.split("layers.", 1)[-1]))
-        out[p + ".codes"] = d[p + ".sz_codes"]
-        out[p + ".vq_scales"] = d[p + ".sz_scales"]
-        out[p + ".row_table"] = skipzero_row_table(d[p + ".sz_rowmask"], int(m["experts"]),
-                                                   int(m["out"]))
-    return list(out.items()) if as_list else out
+    (vq_switch.py:4988-5013); the conversion lives with the artifact loader
+    (artifact.convert_skipzero), which applies the same per-module checks."""
+    from .artifact import convert_skipzero
+    return convert_skipzero(weights, modules)
 
 
 # ---------------------------------------------------------------- module
