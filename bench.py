@@ -19,8 +19,9 @@ value = packed-weight GB/s: bytes of the codes and scales of the experts the
 router touched (SURVEY 8(d) first term), summed over every layer call, over
 the timed wall time. roofline uses the layer call's total algorithmic bytes
 (codes + scales + codebooks + activations) over its event-timed duration.
-cpu_baseline: the repository's numpy oracle of the same layer (unpack ->
-fp16 dequant -> float64 matmuls), single-threaded, on a bounded sample.
+cpu_baseline: the reference's decode-then-matmul of the same layer on the
+host cores (unpack -> fp16 dequant -> fp32 matvecs, numpy), timed on one
+thread and on every usable core, on a bounded sample.
 
 --workload c4 / c4t16: an MTP verify batch of T tokens
 through the config-3 layer with 20% of the routed experts' rows dead and
@@ -32,8 +33,8 @@ value = packed GB/s of the live rows of the touched experts.
 --workload c1 (the reference's CPU-runnable case): one
 dense VQ GEMV per call (W 4096x4096, d=2, K=256, uint8 codes, x [1, 4096]
 bf16) over 48 distinct weights (403 MB) so each call streams from HBM; value
-= packed GB/s of codes + scales; cpu_baseline: the numpy oracle of the same
-GEMV, single-threaded.
+= packed GB/s of codes + scales; cpu_baseline: the same GEMV as fp16 dequant +
+fp32 matvec on the host, one thread and all cores.
 
 --workload c5: dense VQ prefill, x [2048, 5120]
 through VQLinear 5120->17408 then 17408->5120 (d8, K=65536 uint16 codes);
@@ -130,12 +131,83 @@ def expert_bytes(w):
     return 2 * gu + dn
 
 
-def cpu_baseline(w, budget_s=12.0):
-    """Numpy oracle of one token-layer (decode-then-matmul), single thread."""
+# ------------------------------------------------------------ CPU baseline
+def _cpu_env():
+    """Host facts the CPU baseline is quoted with: usable cores, CPU model,
+    numpy's BLAS (vendor, version, default threads)."""
+    cores = len(os.sched_getaffinity(0))
+    model = None
     try:
-        from threadpoolctl import threadpool_limits
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    blas = None
+    try:
+        from threadpoolctl import threadpool_info
+        np.ones((64, 64)) @ np.ones((64, 64))            # loads the BLAS
+        for i in threadpool_info():
+            if i.get("user_api") == "blas":
+                blas = {"vendor": i.get("internal_api"), "version": i.get("version"),
+                        "threads": i.get("num_threads")}
+                break
     except ImportError:
-        threadpool_limits = None
+        pass
+    return cores, model, blas
+
+
+def _cpu_time(units, budget_s, workers):
+    """Mean seconds per unit: units(i) -> list of independent zero-argument
+    tasks (plus a finishing callable of their results). BLAS runs one thread;
+    `workers` > 1 spreads each unit's tasks over a thread pool (numpy's
+    gathers, conversions and matmuls release the GIL)."""
+    import concurrent.futures as cf
+    from threadpoolctl import threadpool_limits
+    pool = cf.ThreadPoolExecutor(workers) if workers > 1 else None
+    n, t0 = 0, time.perf_counter()
+    try:
+        with threadpool_limits(1):
+            while n < 2 or (time.perf_counter() - t0 < budget_s and n < 4096):
+                tasks, finish = units(n)
+                res = list(pool.map(lambda f: f(), tasks)) if pool else [f() for f in tasks]
+                finish(res)
+                n += 1
+    finally:
+        if pool:
+            pool.shutdown()
+    return (time.perf_counter() - t0) / n, n
+
+
+def _cpu_report(units, budget_s, per_unit, unit, what, sample):
+    """Times `units` on one thread and on every usable core; the all-core run
+    is the reported value, the one-thread run rides along."""
+    cores, model, blas = _cpu_env()
+    t1, n1 = _cpu_time(units, budget_s / 2, 1)
+    tn, nn = _cpu_time(units, budget_s / 2, cores) if cores > 1 else (t1, n1)
+    return {"value": round(per_unit / tn, 6), "unit": unit, "cores": cores, "kind": "port",
+            "sample": f"{sample}; {nn} units on {cores} threads, {n1} on 1",
+            "one_thread": {"value": round(per_unit / t1, 6), "cores": 1,
+                           "us_per_unit": round(t1 * 1e6, 1)},
+            "us_per_unit": round(tn * 1e6, 1), "what": what,
+            "host": {"cpu_model": model, "usable_cores": cores, "numpy": np.__version__,
+                     "blas": blas, "blas_threads_used": 1}}
+
+
+def _f32_linear(codes, cb, sc, x32):
+    """The reference's decode-then-matmul on the CPU (vq_dense.py:132-137,
+    288-294): W = fp16(cb[codes] * s), cast to fp32, x @ W.T in fp32."""
+    from oracle import vq_oracle as vo
+    return x32 @ vo.dequant(codes, cb, sc, 64).astype(np.float32).T
+
+
+def cpu_baseline(w, budget_s=16.0):
+    """The MoE decode layer on the host: per token, softmax/top-k routing,
+    then per routed expert unpack + fp16 dequant + fp32 matvecs of gate, up
+    and down with SwiGLU between, and the weighted combine; the experts are
+    the parallel tasks."""
     sys.path.insert(0, ROOT)
     from oracle import vq_oracle as vo
     H, I, d, K, bits, k = w["H"], w["I"], w["d"], w["K"], w["bits"], w["k"]
@@ -144,42 +216,79 @@ def cpu_baseline(w, budget_s=12.0):
     projs = {}
     for name, (o, i) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
         codes = rng.integers(0, K, (pool, o, i // d)).astype(np.uint16)
-        projs[name] = {"packed": vo.pack(codes, bits), "codebook":
-                       (rng.standard_normal((K, d)) * 0.02).astype(np.float16),
-                       "scales": rng.uniform(0.5, 1.5, (pool, o, i // 64)).astype(np.float16),
-                       "group": 64, "nsub": i // d}
+        projs[name] = {"packed": vo.pack(codes, bits), "nsub": i // d,
+                       "codebook": (rng.standard_normal((K, d)) * 0.02).astype(np.float16),
+                       "scales": rng.uniform(0.5, 1.5, (pool, o, i // 64)).astype(np.float16)}
     xs = rng.standard_normal((64, H)).astype(np.float32)
     lgs = rng.standard_normal((64, pool)).astype(np.float32)
 
-    def token_layer(x, lg):
-        spec = {}
-        ids, _ = vo.route(lg[None], k)
-        for name, p in projs.items():
-            codes = np.zeros(p["scales"].shape[:2] + (p["nsub"],), np.uint16)
-            for e in ids[0]:                      # unpack only the touched experts
-                codes[e] = vo.unpack(p["packed"][e:e + 1], p["nsub"], bits)[0]
-            spec[name] = {"codes": codes, "codebook": p["codebook"], "scales": p["scales"],
-                          "group": 64}
-        return vo.moe_layer(x[None], lg[None], spec["gate"], spec["up"], spec["down"], k)[0]
+    def lin(name, e, v):
+        p = projs[name]
+        codes = vo.unpack(p["packed"][e], p["nsub"], bits)
+        return _f32_linear(codes, p["codebook"], p["scales"][e], v[None])[0]
 
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    n, t0 = 0, time.perf_counter()
-    try:
-        if ctx:
-            ctx.__enter__()
-        while n < 64 and (n < 3 or time.perf_counter() - t0 < budget_s):
-            token_layer(xs[n], lgs[n])
-            n += 1
-    finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
-    dt = (time.perf_counter() - t0) / n
-    gbs = k * expert_bytes(w) / dt / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "us_per_token_layer": round(dt * 1e6, 1),
-            "sample": f"{n} token-layers of the same shape (numpy oracle: unpack + fp16 dequant "
-                      f"of the {k} routed experts + float64 matmuls, 1 thread; expert pool "
-                      f"{pool} since per-token work does not depend on E)"}
+    def expert(e, x):
+        g, u = lin("gate", e, x), lin("up", e, x)
+        return lin("down", e, (g / (1 + np.exp(-g)) * u).astype(np.float32))
+
+    def units(n):
+        x, lg = xs[n % 64], lgs[n % 64]
+        ids, wt = vo.route(lg[None], k)
+        tasks = [lambda e=int(e): expert(e, x) for e in ids[0]]
+        return tasks, lambda ys: sum(float(a) * y for a, y in zip(wt[0], ys))
+
+    return _cpu_report(units, budget_s, k * expert_bytes(w) / 1e9, "GB/s",
+                       "MoE decode token-layer: routing + unpack, fp16 dequant and fp32 matvecs "
+                       "of the routed experts (the reference's decode-then-matmul)",
+                       f"token-layers of the benchmark's shape (H {H}, I {I}, top-{k}, d{d} "
+                       f"K{K} {bits}-bit; an expert pool of {pool}, since per-token work does "
+                       f"not depend on E)")
+
+
+def cpu_prefill_baseline(w, budget_s=16.0):
+    """Dense prefill on the host: fp16 dequant of weight rows + fp32 GEMM
+    with a block of tokens; row blocks are the parallel tasks."""
+    from oracle import vq_oracle as vo
+    rng = np.random.default_rng(7)
+    H, d, K = w["H"], w["d"], w["K"]
+    rows, ntok, nblk = 64, 256, 8
+    codes = rng.integers(0, K, (nblk, rows, H // d)).astype(np.uint16)
+    cb = (rng.standard_normal((K, d)) * 0.02).astype(np.float16)
+    sc = rng.uniform(0.5, 1.5, (nblk, rows, H // 64)).astype(np.float16)
+    x = rng.standard_normal((ntok, H)).astype(np.float32)
+
+    def units(n):
+        return [lambda b=b: _f32_linear(codes[b], cb, sc[b], x) for b in range(nblk)], \
+            lambda ys: None
+
+    return _cpu_report(units, budget_s, 2.0 * nblk * rows * H * ntok / 1e12, "TFLOP/s",
+                       "dense VQ prefill: fp16 dequant + fp32 GEMM (the reference's "
+                       "decode-then-matmul)",
+                       f"{nblk} x {rows} weight rows of the {H}-wide linear (d{d} K{K}) "
+                       f"against {ntok} tokens per unit")
+
+
+def cpu_gemv_baseline(w, budget_s=16.0):
+    """Dense VQ GEMV on the host: fp16 dequant + fp32 matvec of the whole
+    4096 x 4096 weight; 8 row blocks are the parallel tasks."""
+    from oracle import vq_oracle as vo
+    rng = np.random.default_rng(11)
+    OUT, IN, d, K, G = w["OUT"], w["IN"], w["d"], w["K"], w["G"]
+    codes = rng.integers(0, K, (OUT, IN // d)).astype(np.uint8)
+    cb = (rng.standard_normal((K, d)) * 0.02).astype(np.float16)
+    sc = rng.uniform(0.5, 1.5, (OUT, IN // G)).astype(np.float16)
+    x = rng.standard_normal((1, IN)).astype(np.float32)
+    blk = OUT // 8
+
+    def units(n):
+        return [lambda b=b: _f32_linear(codes[b * blk:(b + 1) * blk], cb,
+                                        sc[b * blk:(b + 1) * blk], x) for b in range(8)], \
+            lambda ys: None
+
+    packed = OUT * (IN // d) + OUT * (IN // G) * 2
+    return _cpu_report(units, budget_s, packed / 1e9, "GB/s",
+                       "dense VQ GEMV: fp16 dequant + fp32 matvec",
+                       f"calls of the full {OUT}x{IN} GEMV (d{d} K{K} uint8 codes)")
 
 
 def _graph_time(torch, step, warmup, steps, dev):
@@ -302,72 +411,6 @@ def run_mtp(torch, dev, a, w):
                      "us_per_call_events": round(us_call, 3)},
         "cpu_baseline": cpu,
     }, wall, calls
-
-
-def cpu_prefill_baseline(w, budget_s=10.0):
-    """Numpy oracle of the dense prefill GEMM on a bounded sample of rows."""
-    try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:
-        threadpool_limits = None
-    from oracle import vq_oracle as vo
-    rng = np.random.default_rng(7)
-    H, d, K = w["H"], w["d"], w["K"]
-    rows, ntok = 64, 256
-    codes = rng.integers(0, K, (rows, H // d)).astype(np.uint16)
-    cb = (rng.standard_normal((K, d)) * 0.02).astype(np.float16)
-    sc = rng.uniform(0.5, 1.5, (rows, H // 64)).astype(np.float16)
-    x = rng.standard_normal((ntok, H)).astype(np.float32)
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    n, t0 = 0, time.perf_counter()
-    try:
-        if ctx:
-            ctx.__enter__()
-        while n < 2 or (time.perf_counter() - t0 < budget_s and n < 2000):
-            wd = vo.dequant(codes, cb, sc, 64)
-            vo.decode_matmul(x, wd)
-            n += 1
-    finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
-    dt = (time.perf_counter() - t0) / n
-    tfs = 2.0 * rows * H * ntok / dt / 1e12
-    return {"value": round(tfs, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"{n} x (dequant {rows}x{H} rows + float64 matmul with {ntok} tokens), "
-                      f"numpy oracle, 1 thread"}
-
-
-def cpu_gemv_baseline(w, budget_s=10.0):
-    """Numpy oracle of the dense GEMV (fp16 dequant + float64 matvec) on the
-    full 4096 x 4096 weight, single-threaded, repeated for ~budget_s."""
-    try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:
-        threadpool_limits = None
-    from oracle import vq_oracle as vo
-    rng = np.random.default_rng(11)
-    OUT, IN, d, K, G = w["OUT"], w["IN"], w["d"], w["K"], w["G"]
-    codes = rng.integers(0, K, (OUT, IN // d)).astype(np.uint8)
-    cb = (rng.standard_normal((K, d)) * 0.02).astype(np.float16)
-    sc = rng.uniform(0.5, 1.5, (OUT, IN // G)).astype(np.float16)
-    x = rng.standard_normal((1, IN)).astype(np.float32)
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    n, t0 = 0, time.perf_counter()
-    try:
-        if ctx:
-            ctx.__enter__()
-        while n < 2 or (time.perf_counter() - t0 < budget_s and n < 200):
-            vo.decode_matmul(x, vo.dequant(codes, cb, sc, G))
-            n += 1
-    finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
-    dt = (time.perf_counter() - t0) / n
-    packed = OUT * (IN // d) + OUT * (IN // G) * 2
-    return {"value": round(packed / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "us_per_call": round(dt * 1e6, 1),
-            "sample": f"{n} calls of the full 4096x4096 GEMV (numpy oracle: fp16 dequant + "
-                      f"float64 matvec), 1 thread"}
 
 
 def run_dense_gemv(torch, dev, a, w):
