@@ -174,10 +174,14 @@ def test_c3_layer_full_shape(c3_layer, T):
     _check_layer(c3_layer, T, 3000 + T)
 
 
-@pytest.mark.parametrize("E,k", [(512, 10), (1024, 8)])
+@pytest.mark.parametrize("E,k", [(512, 10), (1024, 8), (256, 16), (256, 20), (100, 8), (64, 9)])
 def test_routing_many_experts_ties(E, k):
     """Routing with 8 (E=512) and 16 (E=1024) logits per lane: tied logits go
-    to the lower expert id, -inf logits are chosen last, -0 and +0 tie."""
+    to the lower expert id, -inf logits are chosen last, -0 and +0 tie. The
+    threshold-and-rank top-k takes k <= 16 (16 its largest, 8-lane groups up
+    to k = 8 and 4-lane groups above); k = 20 and the rows where more than 64
+    keys reach the threshold (all tied) take the sequential selection; E = 100
+    leaves padding slots in the lanes."""
     from vqlab_amd.moe import VQSparseMoeBlock, VQSwitchGLU
     print(f"routing E={E} k={k}", flush=True)
     g = torch.Generator(device="cuda")

@@ -94,18 +94,84 @@ __device__ __forceinline__ void sort_keys_desc(uint32_t (&key)[NS], uint32_t (&i
                     }
 }
 
+// LDS of one routing wave: the candidates' 64-bit ranking keys and the
+// selections in order.
+constexpr int kFastTopK = 16;            // largest k of the threshold-and-rank top-k
+struct RouteScratch {
+    uint64_t cand[kWave];
+    uint32_t sel_idx[kFastTopK];
+    uint32_t sel_key[kFastTopK];
+};
+
+// Threshold-and-rank top-k (k <= 16) of a wave whose lanes hold NS keys each,
+// sorted descending. The lanes form G >= k groups (8 lanes for k <= 8, else
+// 4); the smallest group maximum tau is at most the k-th largest key (the G
+// group maxima are G distinct keys >= tau), so every selection is among the
+// keys >= tau -- about 20 of 256 for random logits. Those candidates are
+// compacted into LDS as (key << 32 | ~index), which orders them exactly as
+// the selection does (larger key first, lower index on ties), and each takes
+// its rank by counting the candidates above it; ranks below k are the
+// selections, written in order. Returns false (nothing written) when tau is
+// the key of a NaN or padding slot, or more than 64 keys are >= tau; the
+// caller then takes the sequential selection.
+template <int NS>
+__device__ __forceinline__ bool topk_rank(const uint32_t (&key)[NS], const uint32_t (&idx)[NS], int k,
+                                          RouteScratch *rs) {
+    const int lane = threadIdx.x & (kWave - 1);
+    uint32_t gm = key[0];
+    gm = max(gm, dpp_u<kDppQuadXor1>(gm));
+    gm = max(gm, dpp_u<kDppQuadXor2>(gm));
+    if (k <= 8) gm = max(gm, dpp_u<kDppRowHalfMirror>(gm));
+    const uint32_t tau = wave_min_u32(gm);
+    if (tau == 0u) return false;
+    int c = 0;                                          // candidates so far (wave-uniform)
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const bool in = key[s] >= tau;
+        const uint64_t b = __ballot(in);
+        const int below = int(__builtin_amdgcn_mbcnt_hi(uint32_t(b >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(uint32_t(b), 0u)));
+        if (in && c + below < kWave)
+            rs->cand[c + below] = (uint64_t(key[s]) << 32) | uint64_t(~idx[s]);
+        c += __popcll(b);
+    }
+    if (c > kWave) return false;
+    // zero the slots up to the next multiple of 8 so the rank loop reads whole groups
+    if (lane >= c && lane < ((c + 7) & ~7)) rs->cand[lane] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const uint64_t mine = lane < c ? rs->cand[lane] : 0;
+    int rank = 0;
+    for (int j0 = 0; j0 < c; j0 += 8) {
+        uint64_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = rs->cand[j0 + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) rank += v[u] > mine ? 1 : 0;
+    }
+    if (lane < c && rank < k) {
+        rs->sel_idx[rank] = ~uint32_t(mine);
+        rs->sel_key[rank] = uint32_t(mine >> 32);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    return true;
+}
+
 // Wave-level softmax + top-k of one token's logits (fp32, like the
 // reference's precise softmax), NS logits per lane (NS * 64 >= E). Every lane
 // returns the expert of pair `want` (or -1) in *e_want; lane r < k holds
 // selection r in (*my_idx, *my_w). Argmax is exact: logits become
-// order-preserving integer keys, each lane sorts its own keys once, and each
-// selection is a DPP max over the lanes' head keys; the lane holding it (on a
-// tie between lanes, the one whose head has the lowest index) pops its head,
-// so ties go to the lower expert id (stable descending order). NaN logits sort
-// below -inf and are never chosen while k <= number of finite logits.
+// order-preserving integer keys and each lane sorts its own keys once. The
+// selections come from topk_rank, or (k > 16, NaN-heavy or degenerate
+// logits) from k sequential selections, each a DPP max over the lanes' head
+// keys; the lane holding it (on a tie between lanes, the one whose head has
+// the lowest index) pops its head. Either way ties go to the lower expert id
+// (stable descending order); NaN logits sort below -inf and are never chosen
+// while k <= number of finite logits.
 template <int NS>
 __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int norm, int want,
-                                           int *e_want, int *my_idx, float *my_w) {
+                                           RouteScratch *rs, int *e_want, int *my_idx, float *my_w) {
     const int lane = threadIdx.x & (kWave - 1);
     uint32_t key[NS], idx[NS];
     float raw[NS];
@@ -131,10 +197,18 @@ __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int no
             if (key[s]) lsum += __expf(key_f32(key[s]) - m);
         den = wave_sum(lsum);
     }
-    // k sequential selections; lane r keeps selection r, probabilities after
     int e_w = -1, midx = -1;
     uint32_t mykey = 0;
-    for (int r = 0; r < k; ++r) {
+    const bool ranked = k <= kFastTopK && topk_rank<NS>(key, idx, k, rs);
+    if (ranked) {
+        if (want >= 0 && want < k) e_w = int(rs->sel_idx[want]);
+        if (lane < k) {
+            midx = int(rs->sel_idx[lane]);
+            mykey = rs->sel_key[lane];
+        }
+    }
+    // otherwise k sequential selections; lane r keeps selection r
+    for (int r = 0; r < (ranked ? 0 : k); ++r) {
         const uint32_t best = wave_max_u32(key[0]);
         int bi = -1;
         if (best) {
@@ -173,13 +247,13 @@ __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int no
 }
 
 __device__ __forceinline__ void route(const float *lg, int E, int k, int norm, int want,
-                                      int *e_want, int *my_idx, float *my_w) {
+                                      RouteScratch *rs, int *e_want, int *my_idx, float *my_w) {
     const int ns = (E + kWave - 1) / kWave;              // wave-uniform
-    if (ns <= 1) route_wave<1>(lg, E, k, norm, want, e_want, my_idx, my_w);
-    else if (ns <= 2) route_wave<2>(lg, E, k, norm, want, e_want, my_idx, my_w);
-    else if (ns <= 4) route_wave<4>(lg, E, k, norm, want, e_want, my_idx, my_w);
-    else if (ns <= 8) route_wave<8>(lg, E, k, norm, want, e_want, my_idx, my_w);
-    else route_wave<16>(lg, E, k, norm, want, e_want, my_idx, my_w);
+    if (ns <= 1) route_wave<1>(lg, E, k, norm, want, rs, e_want, my_idx, my_w);
+    else if (ns <= 2) route_wave<2>(lg, E, k, norm, want, rs, e_want, my_idx, my_w);
+    else if (ns <= 4) route_wave<4>(lg, E, k, norm, want, rs, e_want, my_idx, my_w);
+    else if (ns <= 8) route_wave<8>(lg, E, k, norm, want, rs, e_want, my_idx, my_w);
+    else route_wave<16>(lg, E, k, norm, want, rs, e_want, my_idx, my_w);
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.f + __expf(-g)); }
@@ -291,6 +365,7 @@ __host__ __device__ constexpr int down_cbn() {
 
 // Routing of the workgroup's token as wave 0 computed it (LDS).
 struct RouteLds {
+    RouteScratch rs;           // the routing wave's scratch
     int route;                 // expert of this workgroup's pair
     int ids[kMaxTopK];
     float wts[kMaxTopK];
@@ -339,7 +414,7 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
     float my_w = 0.f;
     if (wave == 0) {
         int e_pair;
-        route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &e_pair, &my_idx, &my_w);
+        route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &rl.rs, &e_pair, &my_idx, &my_w);
         if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
         if (lane == 0) rl.route = e_pair;
         if (lane < p.top_k) {
@@ -473,7 +548,7 @@ __global__ void __launch_bounds__(moe_waves_up(W) * kWave) k_moe_up_split(const 
     float my_w = 0.f;
     if (wave == 0) {
         int e_pair;
-        route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &e_pair, &my_idx, &my_w);
+        route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &rl.rs, &e_pair, &my_idx, &my_w);
         if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
         if (lane == 0) rl.route = e_pair;
     } else {
@@ -593,12 +668,34 @@ __device__ __forceinline__ void down_stage_cb(const MoeParams &p, uint8_t *smem)
                                           reinterpret_cast<h2 *>(smem + CBN * D * 2));
 }
 
+// First round of the token's SwiGLU rows in registers: kHFirst 16-byte
+// chunks per thread, loaded with clamped indices and no branch, so a wait for
+// a load issued before them counts exactly these. With fp32 gate / up rows
+// (split phase) the loads read the start of those rows and go unused.
+constexpr int kHFirst = 4;
+struct HFirst {
+    u32x4 v[kHFirst];
+};
+
+__device__ __forceinline__ void h_first_load(const MoeParams &p, int t, HFirst &hf) {
+    const int ng = p.P * (p.I / 8);
+    const uint16_t *src = p.gbuf ? reinterpret_cast<const uint16_t *>(p.gbuf) + int64_t(t) * p.P * p.I * 2
+                                 : p.h + int64_t(t) * p.P * p.I;
+#pragma unroll
+    for (int u = 0; u < kHFirst; ++u) {
+        const int g = min(int(threadIdx.x) + u * int(blockDim.x), ng - 1);
+        hf.v[u] = *reinterpret_cast<const u32x4 *>(src + int64_t(g) * 8);
+    }
+}
+
 // The token's P SwiGLU rows (fp16) -> LDS at the padded block stride, then
 // the down projection of the workgroup's rows, scaled per pair by its router
-// weight and combined over the wave (the DPP row reduction is the sum).
+// weight and combined over the wave (the DPP row reduction is the sum). The
+// first kHFirst chunks per thread of fp16 rows come from `hf`.
 template <int D, int BITS, int GPB, bool W = false>
 __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint8_t *smem,
-                                         const DownLane &dl, DownState<BITS, GPB> &ds) {
+                                         const DownLane &dl, DownState<BITS, GPB> &ds,
+                                         const HFirst &hf) {
     constexpr bool CBL = cb_in_lds(D, BITS);
     constexpr int CBN = down_cbn<D, BITS, W>();
     constexpr int XH = kBlock * D, XS = XH + 8;
@@ -613,7 +710,20 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
         const int gpr = p.I / 8;                     // 8-value groups per row
         const int ng = p.P * gpr;
         constexpr int U = 8;
-        for (int g0 = tid; g0 < ng; g0 += U * blockDim.x) {
+        int gs = tid;
+        if (!p.gbuf) {
+#pragma unroll
+            for (int u = 0; u < kHFirst; ++u) {
+                const int g = tid + u * int(blockDim.x);
+                if (g < ng) {
+                    const int jj = g / gpr, col = (g % gpr) * 8;
+                    const int b = jj * p.NB2 + col / XH;
+                    *reinterpret_cast<u32x4 *>(xs + b * XS + col % XH) = hf.v[u];
+                }
+            }
+            gs = tid + kHFirst * int(blockDim.x);
+        }
+        for (int g0 = gs; g0 < ng; g0 += U * blockDim.x) {
             u32x4 hv[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -685,21 +795,26 @@ __global__ void __launch_bounds__(moe_waves_down(W) * kWave) k_moe_down(const Mo
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = int(blockIdx.y);
     const DownLane dl(p);
-    // The routing is read first: the weight addresses wait on it, and a
-    // wave's vector-memory loads complete in issue order, so it must not
-    // queue behind the table copy (which only the decode needs).
-    int id = -1;
-    float wt = 0.f;
-    if (dl.on && !dl.is_shared) {
-        id = p.ids[t * p.top_k + dl.j];
-        wt = p.wts[t * p.top_k + dl.j];
+    // Load order (a wave's vector-memory loads complete in issue order): the
+    // routing first, since the weight addresses wait on it; then the first
+    // round of the SwiGLU rows, which waits on nothing; then, once the
+    // routing is in, the weights and the table copy. The routing loads take a
+    // clamped pair index and the h loads no branch, so the wait before the
+    // weight loads holds only for the routing.
+    const int jc = min(dl.j, p.top_k - 1);
+    int id = p.ids[t * p.top_k + jc];
+    float wt = p.wts[t * p.top_k + jc];
+    HFirst hf;
+    h_first_load(p, t, hf);
+    if (!dl.on || dl.is_shared) {
+        id = -1;
+        wt = 0.f;
     }
-    wait_vmem();
     DownState<BITS, GPB> ds;
     down_prep<BITS, GPB>(p, int(blockIdx.x), t, dl, [&](int) { return id; },
                          [&](int) { return wt; }, ds);
     down_stage_cb<D, CBN, cb_in_lds(D, BITS), moe_waves_down(W) * kWave>(p, smem);
-    down_run<D, BITS, GPB, W>(p, int(blockIdx.x), t, smem, dl, ds);
+    down_run<D, BITS, GPB, W>(p, int(blockIdx.x), t, smem, dl, ds, hf);
 }
 
 // ------------------------------------------------ codebooks beyond LDS
@@ -709,10 +824,11 @@ __global__ void __launch_bounds__(moe_waves_down(W) * kWave) k_moe_down(const Mo
 // over routed + shared down with silu(g) * u built as its input, and the
 // weighted combine.
 __global__ void __launch_bounds__(kWave) k_route_tokens(const MoeParams p) {
+    __shared__ RouteScratch rs;
     const int t = int(blockIdx.x), lane = int(threadIdx.x);
     int e_pair, my_idx = -1;
     float my_w = 0.f;
-    route(p.logits + int64_t(t) * p.E, p.E, p.top_k, p.norm, -1, &e_pair, &my_idx, &my_w);
+    route(p.logits + int64_t(t) * p.E, p.E, p.top_k, p.norm, -1, &rs, &e_pair, &my_idx, &my_w);
     if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
     if (lane < p.top_k) {
         p.ids[t * p.top_k + lane] = my_idx;
