@@ -149,14 +149,19 @@ int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type,
 
 /* ---- a11: dense large-N path, _decode_matmul (vq_dense.py:262-312) ---------
  * y[N, OUT] = x[N, IN] . W^T for E == 1. Up to 64 rows: W is decoded straight
- * into matrix-core operands (no workspace). Above: the reference's
- * decode-then-matmul -- W is dequantised bit-exactly into the workspace panel
- * by panel and multiplied by an LDS-tiled fp16 matrix-core GEMM (x narrowed
- * to fp16 in the workspace first). vqk_dense_gemm_workspace gives the size of
- * a single whole-weight panel; any workspace holding fp16 x plus 128 weight
- * rows works (smaller panels, more passes), less is VQK_ENOSPACE. With no
- * workspace (NULL, 0), and for IN % 64 != 0, a tile kernel that decodes W
- * into LDS per output tile runs instead. */
+ * into matrix-core operands (no workspace, x rounded to fp16 as the fused
+ * kernels take it). Above (and for shapes that path refuses): the reference's
+ * decode-then-matmul, `xf @ w.T.astype(xf.dtype)` -- W is dequantised into the
+ * workspace panel by panel in x's arithmetic type and multiplied by libvqk's
+ * matrix-core GEMM with fp32 accumulation: fp16 x against the bit-exact fp16
+ * W, bf16 x against W rounded once to bf16, fp32 x through split bf16
+ * operands (x to 16 significant bits, W exactly; three products per term).
+ * x is staged into the workspace when it is fp32, not 16-byte aligned or IN
+ * is not a multiple of 64 (rows zero-padded). vqk_dense_gemm_workspace gives a
+ * size that holds the whole weight as one panel for any activation type; a
+ * smaller workspace that still holds the staged x plus 128 weight rows runs
+ * in more panels, less (or none) is VQK_ENOSPACE. No host synchronisation,
+ * no allocation, no state kept between calls. */
 int vqk_dense_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes);
 int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type,
                    int64_t N, void *y, int32_t y_type, void *workspace,

@@ -2,12 +2,14 @@
 
 vqk_dense_gemm (_decode_matmul, vq_dense.py:262-312) and vqk_grouped_gemm
 (_gemmseg_prefill, vq_switch.py:4569-4722): outputs within rtol 2e-2 /
-atol 1e-3 of the float64 decode-then-matmul oracle with x rounded to fp16
-(the operand the matrix cores take). With bf16 x and y, N > 64 and
-IN % 64 == 0 the dense GEMM is the reference's own arithmetic -- W cast to bf16, one bf16
-GEMM (vq_dense.py:288, 294) -- and the oracle rounds W the same way. The
-device-side sort must build the oracle's tile metadata (tile_meta,
-vq_switch.py:4590-4610) exactly.
+atol 1e-3 of the float64 decode-then-matmul oracle. The register-decode
+segment kernels (dense N <= 64, grouped) take x rounded to fp16. Above 64
+rows (or when the segment kernel refuses the shape) the dense GEMM is the
+reference's own arithmetic, `xf @ w.T.astype(xf.dtype)` (vq_dense.py:288,
+294): bf16 x against W cast to bf16, fp16 x against the fp16 W, fp32 x
+against the fp16 W through the split bf16 form -- and the oracle rounds W
+the same way. The device-side sort must build the oracle's tile metadata
+(tile_meta, vq_switch.py:4590-4610) exactly.
 """
 import ctypes
 
@@ -56,9 +58,9 @@ def test_dense_gemm(case):
     y = VD._decode_matmul(x, codes[0], cb, sc[0], G, OUT, IN, m["pack_bits"])
     assert y.shape == (N, OUT) and y.dtype == x.dtype
     w = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], G)
-    if N > 64 and IN % 64 == 0:     # decode-then-GEMM: the reference's bf16 operands
+    if N > 64 or (IN // D) % 32:    # decode-then-GEMM: the reference's bf16 operands
         ref = vo.decode_matmul(_np(x), vo.bf16_values(w))
-    else:                           # register-decode / LDS tile kernels: fp16 operands
+    else:                           # register-decode segment kernel: fp16 operands
         ref = vo.decode_matmul(_x16(x), w)
     assert_close(_np(y), ref, what=f"dense gemm {case}")
 
@@ -66,7 +68,8 @@ def test_dense_gemm(case):
 @pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
 def test_dense_gemm_dtypes_and_linear(xdt):
     """VQLinear routes N > the GEMV cutoff to the GEMM; both agree with the
-    oracle on the same module, in fp16 and fp32 activations."""
+    oracle on the same module, in fp16 and fp32 activations (the GEMM keeps
+    fp32 x to 16 significant bits, the GEMV narrows it to fp16)."""
     from vqlab_amd import vq_dense as VD
     rng = np.random.default_rng(21)
     m = make_module(rng, 1, 512, 2048, 4, 4096)
@@ -76,10 +79,10 @@ def test_dense_gemm_dtypes_and_linear(xdt):
     y = lin(x[None])
     assert y.shape == (1, 200, 512) and y.dtype == xdt
     w = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], 64)
-    ref = vo.decode_matmul(_x16(x), w)
+    ref = vo.decode_matmul(_np(x), w)
     assert_close(_np(y[0]), ref, what=f"VQLinear {xdt}")
     y8 = lin(x[:8])                                   # the GEMV side of the cutoff
-    assert_close(_np(y8), ref[:8], what="VQLinear gemv side")
+    assert_close(_np(y8), vo.decode_matmul(_x16(x[:8]), w), what="VQLinear gemv side")
 
 
 def test_dense_gemm_empty_and_refusals():
@@ -97,21 +100,24 @@ def test_dense_gemm_empty_and_refusals():
     w1 = Tt.weights(codes[0], cb, sc[0], 64, 8, 256, keep=keep)
     assert L.lib().vqk_dense_gemm(ctypes.byref(w1), Tt.ptr(x), L.VQK_BF16, 0, Tt.ptr(y),
                                   L.VQK_BF16, None, 0, Tt.stream()) == L.VQK_OK
-    # above 64 rows the decode-then-GEMM path wants fp16 x + >= 128 weight rows
+    # above 64 rows the decode-then-GEMM path wants the staged x (up to
+    # fp32's split rows) + >= 128 weight rows; none at all is refused too
     xb = torch.zeros((100, 256), dtype=torch.bfloat16, device="cuda")
     yb = torch.empty((100, 128), dtype=torch.bfloat16, device="cuda")
     ws = ctypes.c_size_t()
     L.check(L.lib().vqk_dense_gemm_workspace(ctypes.byref(w1), 100, ctypes.byref(ws)))
-    assert ws.value >= 100 * 256 * 2 + 128 * 256 * 2
+    assert ws.value >= 100 * 3 * 256 * 2 + 128 * 3 * 256 * 2
     small = torch.empty(1024, dtype=torch.uint8, device="cuda")
     assert L.lib().vqk_dense_gemm(ctypes.byref(w1), Tt.ptr(xb), L.VQK_BF16, 100, Tt.ptr(yb),
                                   L.VQK_BF16, Tt.ptr(small), 1024, Tt.stream()) == L.VQK_ENOSPACE
+    assert L.lib().vqk_dense_gemm(ctypes.byref(w1), Tt.ptr(xb), L.VQK_BF16, 100, Tt.ptr(yb),
+                                  L.VQK_BF16, None, 0, Tt.stream()) == L.VQK_ENOSPACE
 
 
-@pytest.mark.parametrize("panel_rows", [128, 256, None])
-def test_dense_gemm_panels_and_tile_fallback(panel_rows):
-    """Workspaces smaller than the whole weight decode it in panels; with no
-    workspace the LDS tile kernel runs. All agree with the oracle."""
+@pytest.mark.parametrize("panel_rows", [128, 256, 1024])
+def test_dense_gemm_panels(panel_rows):
+    """Workspaces smaller than the whole weight decode it in panels of whole
+    128-row multiples; every panel size agrees with the oracle."""
     from vqlab_amd import _lib as L, _torch as Tt
     print(f"dense gemm panels {panel_rows}", flush=True)
     rng = np.random.default_rng(27)
@@ -122,16 +128,87 @@ def test_dense_gemm_panels_and_tile_fallback(panel_rows):
     w = Tt.weights(codes[0], cb, sc[0], 64, 12, IN, keep=keep)
     x = _x(rng, N, IN)
     y = torch.empty((N, OUT), dtype=torch.float32, device="cuda")
-    if panel_rows is None:
-        work, nb = None, 0
-    else:
-        nb = N * IN * 2 + 512 + panel_rows * IN * 2
-        work = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    nb = panel_rows * IN * 2
+    work = torch.empty(nb, dtype=torch.uint8, device="cuda")
     L.check(L.lib().vqk_dense_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, N, Tt.ptr(y),
-                                   L.VQK_F32, Tt.ptr(work) if work is not None else None, nb,
-                                   Tt.stream()))
+                                   L.VQK_F32, Tt.ptr(work), nb, Tt.stream()))
     wd = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], 64)
-    assert_close(_np(y), vo.decode_matmul(_x16(x), wd), what=f"panels {panel_rows}")
+    assert_close(_np(y), vo.decode_matmul(_np(x), vo.bf16_values(wd)), what=f"panels {panel_rows}")
+
+
+@pytest.mark.parametrize("xdt,IN,offset", [
+    (torch.float32, 1000, 0),      # split bf16 operands, rows padded to the k step
+    (torch.bfloat16, 1000, 0),     # bf16 rows padded (x staged)
+    (torch.float16, 1024, 1),      # x misaligned by one element (x staged)
+    (torch.float32, 1024, 3),      # misaligned fp32 x through the split form
+])
+def test_dense_gemm_staged_x(xdt, IN, offset):
+    """x that the GEMM cannot read in place (fp32, IN not a multiple of 64,
+    misaligned) is staged into the workspace: same arithmetic, same bar."""
+    from vqlab_amd import _lib as L, _torch as Tt
+    print(f"dense gemm staged x {xdt} IN {IN} offset {offset}", flush=True)
+    rng = np.random.default_rng(31 + IN + offset)
+    N, OUT = 200, 384
+    G = 64 if IN % 64 == 0 else 40
+    m = make_module(rng, 1, OUT, IN, 4, 4096, G=G, packed=False)
+    codes, cb, sc = to_device(m)
+    keep = []
+    w = Tt.weights(codes[0], cb, sc[0], G, 0, IN, keep=keep)
+    base = _x(rng, N * IN + offset, 1, xdt).reshape(-1)
+    x = base[offset:].reshape(N, IN)
+    y = torch.empty((N, OUT), dtype=torch.float32, device="cuda")
+    ws = ctypes.c_size_t()
+    L.check(L.lib().vqk_dense_gemm_workspace(ctypes.byref(w), N, ctypes.byref(ws)))
+    work = torch.empty(ws.value, dtype=torch.uint8, device="cuda")
+    L.check(L.lib().vqk_dense_gemm(ctypes.byref(w), Tt.ptr(x), Tt.ACT_TYPES[xdt], N, Tt.ptr(y),
+                                   L.VQK_F32, Tt.ptr(work), ws.value, Tt.stream()))
+    wd = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], G)
+    wr = vo.bf16_values(wd) if xdt == torch.bfloat16 else wd
+    assert_close(_np(y), vo.decode_matmul(_np(x), wr), what=f"staged x {xdt} {IN} {offset}")
+
+
+def test_dense_gemm_split_k_tail():
+    """257 output tiles of 256 x 256 on 256 CUs: one whole round, then the
+    last tile's K split 8 ways into fp32 partials summed in a fixed order.
+    Sampled columns (first, last, across the tail tile) against the oracle,
+    and a second call gives the same bits (the sum order is fixed)."""
+    from vqlab_amd import vq_dense as VD
+    print("dense gemm split-K tail", flush=True)
+    rng = np.random.default_rng(35)
+    N, OUT, IN, K = 256, 257 * 256, 1024, 4096
+    g = torch.Generator(device="cuda")
+    g.manual_seed(35)
+    codes = torch.randint(0, K, (OUT, IN // 4), dtype=torch.int32, device="cuda",
+                          generator=g).to(torch.int16)
+    cb = (torch.randn((K, 4), device="cuda", generator=g) * 0.02).to(torch.float16)
+    sc = (torch.rand((OUT, IN // 64), device="cuda", generator=g) + 0.5).to(torch.float16)
+    x = _x(rng, N, IN)
+    y = VD._decode_matmul(x, codes, cb, sc, 64, OUT, IN, 0)
+    y2 = VD._decode_matmul(x, codes, cb, sc, 64, OUT, IN, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    cols = np.unique(np.concatenate([rng.choice(OUT, 48, replace=False), [0, OUT - 1],
+                                     np.arange(OUT - 256, OUT, 9)]))
+    ci = torch.from_numpy(cols).cuda()
+    w = vo.dequant(codes.index_select(0, ci).cpu().numpy().view(np.uint16), cb.cpu().numpy(),
+                   sc.index_select(0, ci).cpu().numpy(), 64)
+    ref = vo.decode_matmul(_np(x), vo.bf16_values(w))
+    assert_close(_np(y)[:, cols], ref, what="split-K tail")
+
+
+def test_dense_gemm_bf16_beyond_fp16_range():
+    """bf16 activations beyond fp16's range stay finite: the GEMM takes bf16
+    operands, never a narrowing of x to fp16 (vq_dense.py:294)."""
+    from vqlab_amd import vq_dense as VD
+    rng = np.random.default_rng(33)
+    N, OUT, IN = 96, 256, 512
+    m = make_module(rng, 1, OUT, IN, 4, 4096)
+    codes, cb, sc = to_device(m)
+    x = _x(rng, N, IN) * 1e6                         # |x| far above 65504
+    y = VD._decode_matmul(x, codes[0], cb, sc[0], 64, OUT, IN, m["pack_bits"])
+    assert torch.isfinite(y).all()
+    w = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], 64)
+    assert_close(_np(y), vo.decode_matmul(_np(x), vo.bf16_values(w)), what="bf16 beyond fp16 range")
 
 
 # ------------------------------------------------------------ grouped GEMM

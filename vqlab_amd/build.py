@@ -53,10 +53,7 @@ def build(jobs: int | None = None, verbose: bool = True) -> pathlib.Path:
     with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, 16))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB.with_suffix(".so.tmp")
-    # hipBLASLt: the plain GEMM after the dense path's weight decode (in a
-    # torch process its SONAME resolves to the copy torch already loaded)
-    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp),
-           *map(str, objs), "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{r.stdout}\n{r.stderr}")

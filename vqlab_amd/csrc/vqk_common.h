@@ -23,6 +23,29 @@ constexpr int kThreads = 256;        // threads per workgroup of the GEMV kernel
 constexpr int kCbLdsMax = 64 * 1024; // largest codebook table staged in LDS (bytes)
 constexpr int kGemvHybBytes = 128 * 1024;  // part of a larger table the GEMV keeps in LDS
 
+// Output forms of the weight dequant: fp16 (the bit-exact weight), bf16 (one
+// RNE of it) or rows [W_hi | W_lo | W_hi] of 3 * IN bf16 with W_hi + W_lo = W.
+enum : int { kDqF16 = 0, kDqBF16 = 1, kDqSplit = 2 };
+
+// Operand types of the matrix-core GEMM of the dense prefill path.
+enum : int { kOpF16 = 0, kOpBF16 = 1 };
+
+// A GEMM launch plan: tile shape (index into the launcher's table), whole
+// tiles before the split-K tail, K slices per tail tile (0: no tail) and the
+// fp32 partials the tail needs.
+struct GemmPlan {
+    int shape;
+    int32_t full, splits;
+    size_t part_bytes;
+};
+
+// Plan of y = A . B^T with A [M, K], B [Nc, K] on the current device, using
+// at most part_room bytes of split-K partials (vqk_hgemm.hip).
+GemmPlan plan_gemm(int64_t M, int64_t Nc, int64_t K, size_t part_room);
+int launch_hgemm(int op, const GemmPlan &plan, const uint16_t *A, const uint16_t *B, void *y,
+                 int32_t y_type, int64_t ldy, int64_t ycol0, int64_t M, int64_t Nc, int64_t K,
+                 float *part, hipStream_t st);
+
 // A codebook table of 2^BITS entries of D halves is staged in LDS when it
 // fits kCbLdsMax; larger tables are gathered from L2 / MALL.
 __host__ __device__ constexpr bool cb_in_lds(int D, int BITS) {

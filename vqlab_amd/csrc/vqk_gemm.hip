@@ -300,7 +300,6 @@ __global__ void __launch_bounds__(kSortThreads) k_group_sort(const uint32_t *eid
 
 // ---------------------------------------------------------------- host
 constexpr int kGroupBM = 32, kGroupBN = 128;   // fallback tile kernel (tiles hold <= kSegTok rows)
-constexpr int kDenseBM = 128, kDenseBN = 128;
 constexpr int kMaxSortExperts = 4096;
 constexpr int kSegDenseMaxN = 64;               // dense rows up to which the segment kernel runs
 
@@ -344,51 +343,74 @@ static void fill_seg(const vqk_weights *w, const Geom &g, SegParams *p) {
     p->NB = int32_t(g.NB);
 }
 
-// Dense large-N path: W dequantised panel by panel into the workspace, then the
-// fp16 GEMM (vqk_hgemm.hip).
-int launch_hgemm(const uint16_t *A, const uint16_t *B, void *y, int32_t y_type, int64_t ldy,
-                 int64_t ycol0, int64_t M, int64_t Nc, int64_t K, hipStream_t st);
-int launch_x_to_f16(const void *x, int32_t type, int64_t n, uint16_t *out, hipStream_t st);
-int lt_gemm_nt(int32_t type, const void *W, int64_t ldw, const void *X, int64_t ldx, void *Y,
-               int64_t ldy, int64_t M, int64_t N, int64_t K, void *ws, size_t ws_bytes,
-               hipStream_t st);
-int dequant_rows_bf16(const vqk_weights *w, int64_t r0, int64_t rows, uint16_t *out, hipStream_t st);
-constexpr int64_t kPanelMin = 128;              // weight rows of the smallest panel
-constexpr size_t kLtScratch = size_t(64) << 20;  // hipBLASLt scratch in the workspace
+// Dense large-N path (vqk_hgemm.hip): W dequantised panel by panel into the
+// workspace in the GEMM's operand type, then the matrix-core GEMM.
+int launch_x_stage(const void *x, int32_t x_type, int64_t N, int64_t IN, int64_t ld, uint16_t *out,
+                   hipStream_t st);
+int dequant_rows(const vqk_weights *w, int64_t r0, int64_t rows, uint16_t *out, int mode, int64_t ld,
+                 hipStream_t st);
+constexpr int64_t kPanelMin = 128;   // weight rows of the smallest panel
+constexpr int64_t kGemmK = 64;       // the GEMM's k step: operand rows are padded to a multiple
 
-static bool hgemm_fits(const Geom &g, const void *x, int64_t N) {
-    return g.IN % 64 == 0 && g.IN <= INT32_MAX && g.OUT <= INT32_MAX && N <= INT32_MAX &&
-           (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+static int64_t pad_k(const Geom &g) { return (g.IN + kGemmK - 1) / kGemmK * kGemmK; }
+
+// Workspace of the decode-then-GEMM path for N rows: the larger of
+//   fp16 / bf16 x: the whole weight as one panel of padded rows, plus a copy
+//                  of x when IN is not a multiple of the k step, plus the
+//                  split-K partials of the whole-weight GEMM's plan;
+//   fp32 x:        x split into bf16 rows [x_hi | x_hi | x_lo], plus the
+//                  smallest panel of split weight rows.
+// A smaller workspace (>= the copy of x + 128 weight rows) runs in panels.
+static size_t dense_ws_bytes(const Geom &g, int64_t N) {
+    const size_t kp = size_t(pad_k(g));
+    const size_t xcopy = g.IN % kGemmK ? al256(size_t(N) * kp * 2) : 0;
+    const size_t half = xcopy + al256(size_t(g.OUT) * kp * 2) +
+                        al256(plan_gemm(N, g.OUT, int64_t(kp), SIZE_MAX).part_bytes);
+    const size_t f32 = al256(size_t(N) * 3 * kp * 2) + size_t(kPanelMin) * 3 * kp * 2;
+    return half > f32 ? half : f32;
 }
 
-static size_t x16_bytes(const Geom &g, int64_t N) { return al256(size_t(N) * size_t(g.IN) * 2); }
-
-// fp16 or bf16 x and y of one type: the weight decoded panel by panel in that
-// type (bf16 = one RNE of the fp16 value, the reference's cast), each panel's
-// GEMM on hipBLASLt with the rest of the workspace as its scratch.
-// VQK_ENOTIMPL before any launch when the library has no algorithm.
-static int dense_lt(const vqk_weights *w, const Geom &g, const void *x, int32_t type, int64_t N,
-                    void *y, void *workspace, size_t ws_bytes, hipStream_t st) {
-    const size_t row_b = size_t(g.IN) * 2;
-    if (ws_bytes < kPanelMin * row_b)
-        return set_error(VQK_ENOSPACE, "dense GEMM workspace %zu B < %lld weight rows", ws_bytes,
+// The reference's `xf @ w.T.astype(xf.dtype)` (vq_dense.py:288, 294): fp16 x
+// multiplies the bit-exact fp16 weight, bf16 x its bf16 rounding (one RNE),
+// each in its own type with fp32 accumulation; fp32 x goes through the split
+// form (k_x_stage). Operand rows are padded with zeros to the GEMM's k step;
+// x is staged into the workspace when it is fp32, misaligned or padded.
+// Panels of whole 128-row multiples when the workspace is smaller than the
+// weight.
+static int dense_decode_gemm(const vqk_weights *w, const Geom &g, const void *x, int32_t x_type,
+                             int64_t N, void *y, int32_t y_type, void *workspace, size_t ws_bytes,
+                             hipStream_t st) {
+    const int64_t kp = pad_k(g);
+    const int parts = x_type == VQK_F32 ? 3 : 1;
+    const size_t row_b = size_t(parts * kp) * 2;
+    const bool stage = x_type == VQK_F32 || kp != g.IN || (reinterpret_cast<uintptr_t>(x) & 15);
+    const size_t xb = stage ? al256(size_t(N) * row_b) : 0;
+    if (!workspace || ws_bytes < xb + kPanelMin * row_b)
+        return set_error(VQK_ENOSPACE, "dense GEMM workspace %zu B < %zu B (%s%lld weight rows)",
+                         ws_bytes, xb + kPanelMin * row_b, stage ? "staged x + " : "",
                          (long long)kPanelMin);
-    int64_t prow = int64_t(ws_bytes / row_b);
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    const uint16_t *a = static_cast<const uint16_t *>(x);
+    int rc;
+    if (stage) {
+        uint16_t *xs = reinterpret_cast<uint16_t *>(ws);
+        if ((rc = launch_x_stage(x, x_type, N, g.IN, kp, xs, st))) return rc;
+        a = xs;
+    }
+    const int op = x_type == VQK_F16 ? kOpF16 : kOpBF16;
+    const int mode = x_type == VQK_F16 ? kDqF16 : (x_type == VQK_BF16 ? kDqBF16 : kDqSplit);
+    uint16_t *panel = reinterpret_cast<uint16_t *>(ws + xb);
+    int64_t prow = int64_t((ws_bytes - xb) / row_b);
     prow = prow >= g.OUT ? g.OUT : prow / kPanelMin * kPanelMin;
-    uint16_t *panel = static_cast<uint16_t *>(workspace);
-    const size_t used = al256(size_t(prow) * row_b);
-    uint8_t *lws = used < ws_bytes ? static_cast<uint8_t *>(workspace) + used : nullptr;
-    const size_t lwb = used < ws_bytes ? ws_bytes - used : 0;
     for (int64_t r0 = 0; r0 < g.OUT; r0 += prow) {
         const int64_t rows = g.OUT - r0 < prow ? g.OUT - r0 : prow;
-        int rc = type == VQK_BF16 ? dequant_rows_bf16(w, r0, rows, panel, st)
-                                  : vqk_dequant(w, r0, rows, panel, st);
-        if (rc) return rc;
-        rc = lt_gemm_nt(type, panel, g.IN, x, g.IN, static_cast<uint16_t *>(y) + r0, g.OUT, rows, N,
-                        g.IN, lws, lwb, st);
-        if (rc == VQK_ENOTIMPL && r0 > 0)
-            return set_error(VQK_EINVAL, "library GEMM refused a later panel");
-        if (rc) return rc;
+        // split-K partials go in whatever the panel leaves of the workspace
+        const size_t used = xb + al256(size_t(rows) * row_b);
+        const GemmPlan plan = plan_gemm(N, rows, parts * kp, used < ws_bytes ? ws_bytes - used : 0);
+        float *part = plan.splits ? reinterpret_cast<float *>(ws + used) : nullptr;
+        if ((rc = dequant_rows(w, r0, rows, panel, mode, kp, st))) return rc;
+        if ((rc = launch_hgemm(op, plan, a, panel, y, y_type, g.OUT, r0, N, rows, parts * kp, part, st)))
+            return rc;
     }
     return VQK_OK;
 }
@@ -567,11 +589,9 @@ int vqk_dense_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes) {
     int rc = make_geom(w, &g);
     if (rc) return rc;
     if (!bytes || N < 0) return set_error(VQK_EINVAL, "bad arguments");
-    // the decode-then-GEMM path: fp16 x plus the whole fp16 weight (one panel),
-    // plus the library GEMM's scratch (fp16 / bf16 activations)
+    // up to 64 rows the segment kernel decodes in registers and needs none
     const bool seg = N <= kSegDenseMaxN && seg_fits_geom(g, w);
-    *bytes = (!seg && N > 0 && g.IN % 64 == 0)
-                 ? x16_bytes(g, N) + al256(size_t(g.OUT) * size_t(g.IN) * 2) + kLtScratch : 0;
+    *bytes = (!seg && N > 0) ? dense_ws_bytes(g, N) : 0;
     return VQK_OK;
 }
 
@@ -598,58 +618,10 @@ int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_t 
                         unsigned((N + kSegTok - 1) / kSegTok), 1);
         return launch_seg(sp, g, kSegTok, grid, hipStream_t(stream));
     }
-    if (hgemm_fits(g, x, N) && (workspace || ws_bytes)) {
-        hipStream_t st = hipStream_t(stream);
-        if (x_type == y_type && (x_type == VQK_F16 || x_type == VQK_BF16) &&
-            (reinterpret_cast<uintptr_t>(y) & 15) == 0 && workspace) {
-            rc = dense_lt(w, g, x, x_type, N, y, workspace, ws_bytes, st);
-            if (rc != VQK_ENOTIMPL) return rc;
-        }
-        const bool cvt = x_type != VQK_F16;
-        const size_t xb = cvt ? x16_bytes(g, N) : 0;
-        const size_t row_b = size_t(g.IN) * 2;
-        if (!workspace || ws_bytes < xb + kPanelMin * row_b)
-            return set_error(VQK_ENOSPACE, "dense GEMM workspace %zu B < %zu B (fp16 x + %lld "
-                             "weight rows)", ws_bytes, xb + kPanelMin * row_b, (long long)kPanelMin);
-        uint8_t *ws = static_cast<uint8_t *>(workspace);
-        const uint16_t *a16 = static_cast<const uint16_t *>(x);
-        if (cvt) {
-            if ((rc = launch_x_to_f16(x, x_type, N * g.IN, reinterpret_cast<uint16_t *>(ws), st)))
-                return rc;
-            a16 = reinterpret_cast<const uint16_t *>(ws);
-        }
-        uint16_t *panel = reinterpret_cast<uint16_t *>(ws + xb);
-        int64_t prow = int64_t((ws_bytes - xb) / row_b);
-        prow = prow >= g.OUT ? g.OUT : prow / kPanelMin * kPanelMin;
-        for (int64_t r0 = 0; r0 < g.OUT; r0 += prow) {
-            const int64_t rows = g.OUT - r0 < prow ? g.OUT - r0 : prow;
-            if ((rc = vqk_dequant(w, r0, rows, panel, stream))) return rc;
-            if ((rc = launch_hgemm(a16, panel, y, y_type, g.OUT, r0, N, rows, g.IN, st))) return rc;
-        }
-        return VQK_OK;
-    }
-    GemmParams p;
-    if ((rc = fill_gemm(w, g, &p))) return rc;
-    p.x = x;
-    p.x_type = x_type;
-    p.xkrep = 1;
-    p.y = y;
-    p.y_type = y_type;
-    p.N = int32_t(N);
-    const int64_t gy = (N + kDenseBM - 1) / kDenseBM;
-    const dim3 grid(unsigned((g.OUT + kDenseBN - 1) / kDenseBN), 1, 1);
-    for (int64_t y0 = 0; y0 < gy; y0 += 65535) {
-        // rows are addressed through blockIdx.y; split huge N into launches
-        GemmParams q = p;
-        const int64_t rows0 = y0 * kDenseBM;
-        q.x = static_cast<const uint8_t *>(x) + rows0 * g.IN * act_size(x_type);
-        q.y = static_cast<uint8_t *>(y) + rows0 * g.OUT * act_size(y_type);
-        q.N = int32_t((N - rows0) < int64_t(65535) * kDenseBM ? (N - rows0) : int64_t(65535) * kDenseBM);
-        const dim3 gr(grid.x, unsigned((q.N + kDenseBM - 1) / kDenseBM), 1);
-        rc = launch_gemm<kDenseBM, kDenseBN, 2, 2>(q, g, gr, hipStream_t(stream));
-        if (rc) return rc;
-    }
-    return VQK_OK;
+    if (g.OUT > INT32_MAX || 3 * pad_k(g) > INT32_MAX)
+        return set_error(VQK_ENOTIMPL, "dense GEMM shape OUT %lld IN %lld", (long long)g.OUT,
+                         (long long)g.IN);
+    return dense_decode_gemm(w, g, x, x_type, N, y, y_type, workspace, ws_bytes, hipStream_t(stream));
 }
 
 int vqk_grouped_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes) {

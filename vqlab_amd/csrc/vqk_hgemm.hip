@@ -1,213 +1,113 @@
-// fp16 matrix-core GEMM for the dense prefill path, after the weight has been
-// dequantised (bit-exactly) into a workspace panel:
-//     y[m, c0 + n] = sum_k A[m, k] * B[n, k]      A = x as fp16 [M, K],
-//                                                  B = W panel fp16 [Nc, K]
-// Both operands are K-contiguous, which is what v_mfma_f32_32x32x16_f16
-// reads per lane (8 consecutive k of one row), so neither is transposed.
-//
-// Workgroup tile BM x BN x BK with WGM x WGN waves, each wave owning a
-// (BM / WGM) x (BN / WGN) block of 32x32 MFMA tiles with fp32 accumulators.
-// Tiles of A and B are copied global -> LDS by global_load_lds_dwordx4 (no
-// VGPR round trip) into NST stages: the copies of the next NST - 1 k steps
-// are in flight while one multiplies.
-// An LDS row is BK halves = BK / 8 slots of 16 bytes; slot s of row r is
-// stored at slot s ^ swz(r), so the rows one read phase touches at one
-// logical slot hit distinct 4-bank groups. The direct-to-LDS copy writes
-// consecutive slots per lane, so the swizzle is applied to the GLOBAL
-// address each lane fetches.
-// Workgroups are numbered so that the 8 XCDs (workgroups are dealt to them
-// round-robin) each own a contiguous band of B panels and sweep all row
-// tiles of A for each: a B panel is fetched into one XCD's L2 once.
-#include "vqk_common.h"
-#include "vqk_gemv.h"
+// Launchers of the dense prefill GEMM (kernels in vqk_hgemm.h) and the
+// conversion of fp32 activations into split bf16 operands.
+#include "vqk_hgemm.h"
 
 namespace vqk {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+// Tile shapes (measured on MI355X at the dense prefill shapes, M = 2048):
+//   0  256 x 256, ping-pong 4 x 2 waves (64 x 128 each), BK 32, 5 stages:
+//      the most MFMA work per LDS byte; 5120 -> 17408 is 544 tiles = two
+//      rounds of 256 CUs + 32 tiles, whose K is split 8 ways (below)
+//   1  256 x 192, ping-pong 4 x 2 waves (64 x 96 each), BK 32, 4 stages
+//      5120 -> 17408 whole: 728 tiles = 2.84 rounds, 386 us
+//   2  256 x 160, ping-pong 8 x 1 waves (32 x 160 each), BK 64, 3 stages
+//      17408 -> 5120: 256 tiles = one round, 325 us
+//   3  128 x 128, 4 waves (64 x 64 each), BK 64, 3 stages: small outputs
+// The plan takes the shape (and split) whose estimated time -- rounds x tile
+// area / relative rate -- is least: a tile count just past a multiple of
+// the CU count idles most of the GPU for a whole round (256 x 256 tiles:
+// 160 for a 2048 x 5120 output). With R whole rounds and r < C/2 tiles left
+// over (C CUs), the r tiles run as r x s K slices (s <= C / r, at most 8, at
+// least 4 k steps each) into fp32 partials that k_gemm_reduce adds in a
+// fixed order.
+struct TileShape { int bm, bn, bk; float rate; bool pp; };
+constexpr TileShape kShapes[] = {
+    {256, 256, 32, 1.f, true}, {256, 192, 32, 0.8f, true}, {256, 160, 64, 0.87f, true},
+    {128, 128, 64, 0.5f, false}};
+constexpr float kSplitCost = 1.3f;      // a split slice's time relative to its share of a tile
 
-struct HgemmParams {
-    const uint16_t *A;    // [M, K] fp16
-    const uint16_t *B;    // [Nc, K] fp16
-    void *y;
-    int32_t y_type;
-    int64_t ldy;          // elements between rows of y
-    int64_t ycol0;        // column of y that B's row 0 lands in
-    int32_t M, Nc, K;
-    int32_t tiles_m, tiles_n;
-};
+static int cu_count() {
+    int cus = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;
+    return cus;
+}
 
-template <int BM, int BN, int WGM, int WGN, int BK, int NST>
-__global__ void __launch_bounds__(64 * WGM * WGN) k_hgemm(const HgemmParams p) {
-    constexpr int NW = WGM * WGN;                  // waves: WGM along M x WGN along N
-    constexpr int WTM = BM / WGM, WTN = BN / WGN;  // wave tile
-    constexpr int TM = WTM / 32, TN = WTN / 32;
-    constexpr int RB = BK * 2;                     // bytes per LDS row
-    constexpr int SLOTS = RB / 16;                 // 16-byte slots per row
-    constexpr int RPI = 1024 / RB;                 // rows per 1 KB wave copy
-    constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB;
-    constexpr int A_INS = A_BYTES / 1024, B_INS = B_BYTES / 1024;   // 1 KB wave copies
-    constexpr int NSL = BK / 16;                   // 16-k slices per step
-    static_assert(A_INS % NW == 0 && B_INS % NW == 0, "copies must split over the waves");
-    static_assert(TM >= 1 && TN >= 1, "wave tile below one 32x32 MFMA tile");
-    static_assert(NST >= 3, "the pipeline keeps two stages in flight");
-    extern __shared__ __align__(16) uint8_t smem[];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave / WGN, wn = wave % WGN;
-    // slot swizzle: the 16 (BK 64) or 32 (BK 32) rows an LDS read phase touches
-    // at one logical slot land on distinct 4-bank groups
-    auto swz = [](int r) { return SLOTS == 8 ? ((r >> 1) & 7) : ((r >> 2) & (SLOTS - 1)); };
-
-    // XCD-aware tile order: workgroup b runs on XCD b % 8
-    const int T = p.tiles_m * p.tiles_n;
-    int t = int(blockIdx.x);
-    if (T % 8 == 0) t = (t % 8) * (T / 8) + t / 8;
-    const int bm = t % p.tiles_m, bn = t / p.tiles_m;
-    const int m0 = bm * BM, n0 = bn * BN;
-
-    // per-lane global sources of this wave's copies (row r of a tile, swizzled slot)
-    const int crow = lane / SLOTS, cslot = lane % SLOTS;
-    const uint16_t *asrc[A_INS / NW];
-    const uint16_t *bsrc[B_INS / NW];
-#pragma unroll
-    for (int j = 0; j < A_INS / NW; ++j) {
-        const int r = (wave * (A_INS / NW) + j) * RPI + crow;
-        const int gr = min(m0 + r, p.M - 1);
-        asrc[j] = p.A + int64_t(gr) * p.K + 8 * (cslot ^ swz(r));
-    }
-#pragma unroll
-    for (int j = 0; j < B_INS / NW; ++j) {
-        const int r = (wave * (B_INS / NW) + j) * RPI + crow;
-        const int gr = min(n0 + r, p.Nc - 1);
-        bsrc[j] = p.B + int64_t(gr) * p.K + 8 * (cslot ^ swz(r));
-    }
-    constexpr int STAGE = A_BYTES + B_BYTES;
-    auto issue = [&](int kt, int buf) {
-        uint8_t *abase = smem + buf * STAGE;
-        uint8_t *bbase = abase + A_BYTES;
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int j = 0; j < A_INS / NW; ++j)
-            __builtin_amdgcn_global_load_lds((global_void *)(asrc[j] + k0),
-                                             (lds_void *)(abase + (wave * (A_INS / NW) + j) * 1024),
-                                             16, 0, 0);
-#pragma unroll
-        for (int j = 0; j < B_INS / NW; ++j)
-            __builtin_amdgcn_global_load_lds((global_void *)(bsrc[j] + k0),
-                                             (lds_void *)(bbase + (wave * (B_INS / NW) + j) * 1024),
-                                             16, 0, 0);
-    };
-
-    f32x16 acc[TM][TN];
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) acc[a][b] = f32x16{};
-
-    // Software pipeline over NST LDS stages (NST - 1 copies in flight), with
-    // the operand fragments read one 16-wide k slice ahead of the MFMAs that
-    // use them (two register sets). In step k: slices 0..NSL-2 multiply while
-    // slices 1..NSL-1 are read; then this wave waits for its stage-(k+1)
-    // copies, one barrier makes stage k+1 visible and retires every wave's
-    // reads of stage k-1's buffer, the copy of stage k+NST-1 goes into it, and
-    // the last slice multiplies while slice 0 of step k+1 is read. A wave's
-    // copies complete in issue order, so "at most (NST-3) stages' copies
-    // outstanding" means stage k+1 has landed.
-    constexpr int PER_STAGE = A_INS / NW + B_INS / NW;
-    const int KT = p.K / BK;
-    const int lr = lane & 31, lk = lane >> 5;
-    auto frags = [&](int stage, int kk, h8 (&af)[TM], h8 (&bf)[TN]) {
-        const uint8_t *abase = smem + stage * STAGE;
-        const uint8_t *bbase = abase + A_BYTES;
-        const int slot = 2 * kk + lk;
-#pragma unroll
-        for (int a = 0; a < TM; ++a) {
-            const int r = wm * WTM + a * 32 + lr;
-            af[a] = *reinterpret_cast<const h8 *>(abase + r * RB + ((slot ^ swz(r)) << 4));
-        }
-#pragma unroll
-        for (int b = 0; b < TN; ++b) {
-            const int r = wn * WTN + b * 32 + lr;
-            bf[b] = *reinterpret_cast<const h8 *>(bbase + r * RB + ((slot ^ swz(r)) << 4));
-        }
-    };
-    auto mma = [&](const h8 (&af)[TM], const h8 (&bf)[TN]) {
-#pragma unroll
-        for (int a = 0; a < TM; ++a)
-#pragma unroll
-            for (int b = 0; b < TN; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
-    };
-    h8 f0a[TM], f0b[TN], f1a[TM], f1b[TN];
-#pragma unroll
-    for (int s = 0; s < NST - 1; ++s)
-        if (s < KT) issue(s, s);
-    if (KT >= NST - 1) wait_vmcnt<(NST - 2) * PER_STAGE>();
-    else wait_vmem();
-    __builtin_amdgcn_s_barrier();
-    frags(0, 0, f0a, f0b);
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cs = kt % NST;
-#pragma unroll
-        for (int kk = 1; kk < NSL; ++kk) {
-            if (kk & 1) { frags(cs, kk, f1a, f1b); mma(f0a, f0b); }
-            else { frags(cs, kk, f0a, f0b); mma(f1a, f1b); }
-        }
-        if (kt + NST - 2 < KT) wait_vmcnt<(NST - 3) * PER_STAGE>();
-        else wait_vmem();
-        __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): the last slice of stage k read
-        __builtin_amdgcn_s_barrier();
-        if (kt + NST - 1 < KT) issue(kt + NST - 1, (kt + NST - 1) % NST);
-        static_assert(NSL % 2 == 0, "an even slice count ends on the second register set");
-        frags((kt + 1) % NST, 0, f0a, f0b);         // past the last step: unused
-        mma(f1a, f1b);
-    }
-    wait_vmem();
-
-    // C register i of lane l: row 8*(i/4) + 4*(l/32) + i%4, column l%32
-#pragma unroll
-    for (int a = 0; a < TM; ++a) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int m = m0 + wm * WTM + a * 32 + (i / 4) * 8 + lk * 4 + (i % 4);
-            if (m >= p.M) continue;
-#pragma unroll
-            for (int b = 0; b < TN; ++b) {
-                const int n = n0 + wn * WTN + b * 32 + lr;
-                if (n < p.Nc) store_act(p.y, p.y_type, int64_t(m) * p.ldy + p.ycol0 + n, acc[a][b][i]);
+GemmPlan plan_gemm(int64_t M, int64_t Nc, int64_t K, size_t part_room) {
+    const int cus = cu_count();
+    GemmPlan best{};
+    double best_cost = -1.;
+    for (int i = 0; i < int(sizeof kShapes / sizeof kShapes[0]); ++i) {
+        const TileShape &sh = kShapes[i];
+        const int64_t T = ((M + sh.bm - 1) / sh.bm) * ((Nc + sh.bn - 1) / sh.bn);
+        const double area = double(sh.bm) * sh.bn / sh.rate;
+        GemmPlan pl{i, 0, 0, 0};
+        double cost = double((T + cus - 1) / cus) * area;
+        const int64_t R = T / cus, r = T % cus, kt = K / sh.bk;
+        if (sh.pp && R >= 1 && r > 0 && 2 * r <= cus) {
+            int64_t sp = cus / r;
+            sp = sp > 8 ? 8 : sp;
+            while (sp >= 2 && (kt / sp < 4 || (sp - 1) * ((kt + sp - 1) / sp) >= kt)) --sp;
+            const size_t pb = size_t(r) * size_t(sp) * size_t(sh.bm) * size_t(sh.bn) * 4;
+            const double c2 = double(R) * area + area / double(sp) * kSplitCost;
+            if (sp >= 2 && pb <= part_room && c2 < cost) {
+                cost = c2;
+                pl.full = int32_t(R * cus);
+                pl.splits = int32_t(sp);
+                pl.part_bytes = pb;
             }
         }
+        if (best_cost < 0. || cost < best_cost) { best = pl; best_cost = cost; }
     }
+    return best;
 }
 
-// x (any activation type) -> fp16 [N, IN], 8 elements per thread.
-__global__ void k_x_to_f16(const void *x, int32_t type, int64_t n8, uint16_t *out) {
-    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= n8) return;
-    *reinterpret_cast<u32x4 *>(out + i * 8) = load8_act(x, type, i * 8);
-}
-
-// Tile shapes, measured on MI355X at the dense prefill shapes (M = 2048,
-// 5120 x 17408 and 17408 x 5120): 256 x 256 with 8 waves (4 x 2, wave tile
-// 64 x 128) and 32-wide k steps in four stages (128 KB of LDS) for large
-// outputs -- each operand byte staged feeds twice the MFMA work of a 128-wide
-// tile; 128 x 128 with 4 waves and 64-wide steps in three stages otherwise,
-// whose 4x more tiles fill the GPU when the output is narrow.
-template <int BM, int BN, int WGM, int WGN, int BK, int NST>
-static int go_hgemm(HgemmParams p, hipStream_t st) {
+template <int OP, int BM, int BN, int WGM, int WGN, int BK, int NST, bool PP>
+static int go_gemm(HgemmParams p, hipStream_t st) {
     p.tiles_m = int32_t((p.M + BM - 1) / BM);
     p.tiles_n = int32_t((p.Nc + BN - 1) / BN);
     const int64_t T = int64_t(p.tiles_m) * p.tiles_n;
-    if (T > INT32_MAX) return set_error(VQK_ENOTIMPL, "GEMM grid too large");
+    const int64_t units = p.splits ? p.full + (T - p.full) * p.splits : T;
+    if (units > INT32_MAX) return set_error(VQK_ENOTIMPL, "GEMM grid too large");
     const size_t lds = size_t(NST) * (BM + BN) * BK * 2;
-    return launch_with_lds<k_hgemm<BM, BN, WGM, WGN, BK, NST>>(dim3(unsigned(T)), dim3(64 * WGM * WGN),
-                                                              lds, st, p);
+    int rc;
+    if constexpr (PP) {
+        rc = launch_with_lds<k_pgemm<OP, BM, BN, WGM, WGN, BK, NST>>(dim3(unsigned(units)), dim3(512),
+                                                                     lds, st, p);
+        if (rc || !p.splits || T == p.full) return rc;
+        hipLaunchKernelGGL((k_gemm_reduce<BM, BN, WGM, WGN>), dim3(BM * BN / 1024, unsigned(T - p.full)),
+                           dim3(256), 0, st, p);
+        return hip_status(hipGetLastError(), "split-K reduce launch");
+    } else {
+        p.splits = 0;
+        return launch_with_lds<k_hgemm<OP, BM, BN, WGM, WGN, BK, NST>>(dim3(unsigned(T)),
+                                                                       dim3(64 * WGM * WGN), lds, st, p);
+    }
 }
 
-// y[:, c0 : c0 + Nc] = A . B^T; A [M, K], B [Nc, K] fp16, K % 64 == 0,
-// both 16-byte aligned.
-int launch_hgemm(const uint16_t *A, const uint16_t *B, void *y, int32_t y_type, int64_t ldy,
-                 int64_t ycol0, int64_t M, int64_t Nc, int64_t K, hipStream_t st) {
+template <int OP>
+static int gemm_op(const HgemmParams &p, int shape, hipStream_t st) {
+    switch (shape) {
+        case 0: return go_gemm<OP, 256, 256, 4, 2, 32, 5, true>(p, st);
+        case 1: return go_gemm<OP, 256, 192, 4, 2, 32, 4, true>(p, st);
+        case 2: return go_gemm<OP, 256, 160, 8, 1, 64, 3, true>(p, st);
+        default: return go_gemm<OP, 128, 128, 2, 2, 64, 3, false>(p, st);
+    }
+}
+
+// y[:, c0 : c0 + Nc] = A . B^T; A [M, K], B [Nc, K] in fp16 (op kOpF16) or
+// bf16 (kOpBF16), K % 64 == 0, both 16-byte aligned. `plan` comes from
+// plan_gemm(M, Nc, K, room); a split plan needs plan.part_bytes of fp32
+// partials at `part` (256-byte aligned).
+int launch_hgemm(int op, const GemmPlan &plan, const uint16_t *A, const uint16_t *B, void *y,
+                 int32_t y_type, int64_t ldy, int64_t ycol0, int64_t M, int64_t Nc, int64_t K,
+                 float *part, hipStream_t st) {
+    if (M <= 0 || Nc <= 0) return VQK_OK;
+    if (K % 64 || M > INT32_MAX || Nc > INT32_MAX || K > INT32_MAX)
+        return set_error(VQK_ENOTIMPL, "GEMM shape M %lld N %lld K %lld", (long long)M, (long long)Nc,
+                         (long long)K);
+    if (plan.splits && !part) return set_error(VQK_EINVAL, "split GEMM without its partials");
     HgemmParams p;
     p.A = A;
     p.B = B;
@@ -218,16 +118,64 @@ int launch_hgemm(const uint16_t *A, const uint16_t *B, void *y, int32_t y_type, 
     p.M = int32_t(M);
     p.Nc = int32_t(Nc);
     p.K = int32_t(K);
-    if (M >= 1024 && Nc >= 1024) return go_hgemm<256, 256, 4, 2, 32, 4>(p, st);
-    return go_hgemm<128, 128, 2, 2, 64, 3>(p, st);
+    p.full = plan.full;
+    p.splits = plan.splits;
+    p.part = part;
+    return op == kOpBF16 ? gemm_op<kOpBF16>(p, plan.shape, st) : gemm_op<kOpF16>(p, plan.shape, st);
 }
 
-int launch_x_to_f16(const void *x, int32_t type, int64_t n, uint16_t *out, hipStream_t st) {
-    const int64_t n8 = n / 8;
+// Activation rows for the GEMM, ld >= IN elements per part, zero past IN:
+//   split == 0: fp16 / bf16 x copied bit for bit (x misaligned, or IN not a
+//               multiple of the GEMM's k step);
+//   split == 1: fp32 x as bf16 rows [x_hi | x_hi | x_lo], x_hi = bf16(x),
+//               x_lo = bf16(x - x_hi). Against weight rows [W_hi | W_lo | W_hi]
+//               (the fp16 weight split the same way, exactly) one bf16 GEMM
+//               over 3 * ld sums x_hi W_hi + x_hi W_lo + x_lo W_hi: the fp16
+//               weight in full and x to 16 significant bits, every product
+//               exact and summed in fp32.
+// One thread per 8 output columns of a row; elements are read one by one, so
+// x needs no alignment beyond its element size.
+__global__ void k_x_stage(const void *x, int32_t x_type, int64_t N, int64_t IN, int64_t ld, int split,
+                          uint16_t *out) {
+    const int64_t ld8 = ld / 8;
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= N * ld8) return;
+    const int64_t row = i / ld8, c0 = (i % ld8) * 8;
+    uint16_t hi[8], lo[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int64_t c = c0 + u;
+        hi[u] = lo[u] = 0;
+        if (c >= IN) continue;
+        if (!split) {
+            hi[u] = static_cast<const uint16_t *>(x)[row * IN + c];
+            continue;
+        }
+        const float v = static_cast<const float *>(x)[row * IN + c];
+        hi[u] = f32_to_bf16(v);
+        const float h = bf16_to_f32(hi[u]);
+        if ((__float_as_uint(h) & 0x7f800000u) != 0x7f800000u) lo[u] = f32_to_bf16(v - h);
+    }
+    u32x4 H, Lo;
+    H.x = hi[0] | (uint32_t(hi[1]) << 16); H.y = hi[2] | (uint32_t(hi[3]) << 16);
+    H.z = hi[4] | (uint32_t(hi[5]) << 16); H.w = hi[6] | (uint32_t(hi[7]) << 16);
+    Lo.x = lo[0] | (uint32_t(lo[1]) << 16); Lo.y = lo[2] | (uint32_t(lo[3]) << 16);
+    Lo.z = lo[4] | (uint32_t(lo[5]) << 16); Lo.w = lo[6] | (uint32_t(lo[7]) << 16);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(out + row * (split ? 3 : 1) * ld + c0);
+    dst[0] = H;
+    if (split) {
+        dst[ld8] = H;
+        dst[2 * ld8] = Lo;
+    }
+}
+
+int launch_x_stage(const void *x, int32_t x_type, int64_t N, int64_t IN, int64_t ld, uint16_t *out,
+                   hipStream_t st) {
+    const int64_t n8 = N * (ld / 8);
     if (n8 == 0) return VQK_OK;
-    hipLaunchKernelGGL(k_x_to_f16, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, st, x, type,
-                       n8, out);
-    return hip_status(hipGetLastError(), "x conversion launch");
+    hipLaunchKernelGGL(k_x_stage, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, st, x, x_type, N, IN,
+                       ld, x_type == VQK_F32 ? 1 : 0, out);
+    return hip_status(hipGetLastError(), "x staging launch");
 }
 
 }  // namespace vqk

@@ -64,6 +64,22 @@ __global__ void __launch_bounds__(256) k_pack(const uint16_t *codes, int64_t row
     }
 }
 
+// D halves to dst with one vector store.
+template <int D>
+__device__ __forceinline__ void store_halves(uint16_t *dst, const uint16_t (&v)[D]) {
+    if constexpr (D == 2) {
+        *reinterpret_cast<uint32_t *>(dst) = uint32_t(v[0]) | (uint32_t(v[1]) << 16);
+    } else if constexpr (D == 4) {
+        *reinterpret_cast<u32x2 *>(dst) = u32x2{uint32_t(v[0]) | (uint32_t(v[1]) << 16),
+                                               uint32_t(v[2]) | (uint32_t(v[3]) << 16)};
+    } else {
+        *reinterpret_cast<u32x4 *>(dst) = u32x4{uint32_t(v[0]) | (uint32_t(v[1]) << 16),
+                                               uint32_t(v[2]) | (uint32_t(v[3]) << 16),
+                                               uint32_t(v[4]) | (uint32_t(v[5]) << 16),
+                                               uint32_t(v[6]) | (uint32_t(v[7]) << 16)};
+    }
+}
+
 struct DequantArgs {
     const void *codes;
     int64_t code_cols;       // u32 words (packed) or codes (unpacked) per code row
@@ -80,14 +96,17 @@ struct DequantArgs {
     int64_t OUT, IN, NSUB;
     int64_t r0, rows;        // output rows: flat rows [r0, r0+rows) or ne*OUT
     uint16_t *out;
-    int bf16;                // 1: write bf16(the fp16 value), one RNE
+    int64_t out_ld;          // elements per output row part (>= IN; columns past IN are zeros)
+    int mode;                // kDqF16, kDqBF16 or kDqSplit
 };
 
 // One thread per (output row, code): writes D halves with one vector store.
+// Threads past the last code of a row zero its padding up to out_ld.
 template <int D>
 __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
     const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (j >= a.NSUB) return;
+    if (j * D >= a.out_ld) return;
+    const bool pad = j >= a.NSUB;
     for (int64_t orow = blockIdx.y; orow < a.rows; orow += gridDim.y) {
         int64_t flat;                       // row of the expanded [E*OUT] module
         int64_t cr = -1;
@@ -100,7 +119,7 @@ __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
         if (flat >= 0) cr = a.row_table ? int64_t(a.row_table[flat]) : flat;
         if (cr >= a.stored_rows) cr = -1;   // corrupt table entry: never read past the codes
         uint16_t vals[D];
-        if (cr < 0) {
+        if (cr < 0 || pad) {
             // dead skipzero row (+0), or an expert id outside [0, E)
 #pragma unroll
             for (int u = 0; u < D; ++u) vals[u] = 0;
@@ -130,24 +149,32 @@ __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
                 // which validation refuses; one scale serves all D values.
                 vals[u] = f32_to_h(s * h_to_f32(e[u]));
             }
-            if (a.bf16) {
-#pragma unroll
-                for (int u = 0; u < D; ++u) vals[u] = f32_to_bf16(h_to_f32(vals[u]));   // fp16 -> f32 exact
-            }
         }
-        uint16_t *dst = a.out + orow * a.IN + j * D;
-        if constexpr (D == 2) {
-            *reinterpret_cast<uint32_t *>(dst) = uint32_t(vals[0]) | (uint32_t(vals[1]) << 16);
-        } else if constexpr (D == 4) {
-            u32x2 v = {uint32_t(vals[0]) | (uint32_t(vals[1]) << 16),
-                       uint32_t(vals[2]) | (uint32_t(vals[3]) << 16)};
-            *reinterpret_cast<u32x2 *>(dst) = v;
+        if (a.mode == kDqF16) {
+            store_halves<D>(a.out + orow * a.out_ld + j * D, vals);
         } else {
-            u32x4 v = {uint32_t(vals[0]) | (uint32_t(vals[1]) << 16),
-                       uint32_t(vals[2]) | (uint32_t(vals[3]) << 16),
-                       uint32_t(vals[4]) | (uint32_t(vals[5]) << 16),
-                       uint32_t(vals[6]) | (uint32_t(vals[7]) << 16)};
-            *reinterpret_cast<u32x4 *>(dst) = v;
+            // bf16(the fp16 value): one RNE (fp16 -> f32 is exact)
+            uint16_t hi[D];
+#pragma unroll
+            for (int u = 0; u < D; ++u) hi[u] = f32_to_bf16(h_to_f32(vals[u]));
+            if (a.mode == kDqBF16) {
+                store_halves<D>(a.out + orow * a.out_ld + j * D, hi);
+            } else {
+                // [W_hi | W_lo | W_hi] rows of 3 * IN: W_lo = W - W_hi has at
+                // most 3 significant bits (a multiple of the fp16 ulp no larger
+                // than half a bf16 ulp), so W_hi + W_lo is the fp16 value exactly
+                uint16_t lo[D];
+#pragma unroll
+                for (int u = 0; u < D; ++u) {
+                    const float w = h_to_f32(vals[u]), h = bf16_to_f32(hi[u]);
+                    lo[u] = (__float_as_uint(h) & 0x7f800000u) == 0x7f800000u ? uint16_t(0)
+                                                                              : f32_to_bf16(w - h);
+                }
+                uint16_t *dst = a.out + orow * 3 * a.out_ld + j * D;
+                store_halves<D>(dst, hi);
+                store_halves<D>(dst + a.out_ld, lo);
+                store_halves<D>(dst + 2 * a.out_ld, hi);
+            }
         }
     }
 }
@@ -163,9 +190,11 @@ static dim3 rows_grid(int64_t cols, int64_t rows, int64_t rpt = 1) {
 }
 
 static int launch_dequant(const vqk_weights *w, const Geom &g, const uint32_t *eidx, int64_t r0,
-                          int64_t rows, uint16_t *out, hipStream_t st, int bf16 = 0) {
+                          int64_t rows, uint16_t *out, hipStream_t st, int mode = kDqF16,
+                          int64_t out_ld = 0) {
     DequantArgs a;
-    a.bf16 = bf16;
+    a.mode = mode;
+    a.out_ld = out_ld > g.IN ? out_ld : g.IN;
     a.codes = w->codes;
     a.code_cols = w->code_cols;
     a.bits = g.packed ? g.BITS : 0;
@@ -183,7 +212,7 @@ static int launch_dequant(const vqk_weights *w, const Geom &g, const uint32_t *e
     a.r0 = r0; a.rows = rows;
     a.out = out;
     if (rows == 0) return VQK_OK;
-    const dim3 grid = rows_grid(g.NSUB, rows, 4);
+    const dim3 grid = rows_grid(a.out_ld / g.D, rows, 4);
     switch (g.D) {
         case 2: hipLaunchKernelGGL(k_dequant<2>, grid, dim3(256), 0, st, a); break;
         case 4: hipLaunchKernelGGL(k_dequant<4>, grid, dim3(256), 0, st, a); break;
@@ -192,13 +221,17 @@ static int launch_dequant(const vqk_weights *w, const Geom &g, const uint32_t *e
     return hip_status(hipGetLastError(), "dequant launch");
 }
 
-// Rows [r0, r0 + rows) of a validated module as bf16 (the reference's cast of
-// the fp16 weight to the activation dtype before its GEMM, vq_dense.py:300-306).
-int dequant_rows_bf16(const vqk_weights *w, int64_t r0, int64_t rows, uint16_t *out, hipStream_t st) {
+// Rows [r0, r0 + rows) of a validated module in `mode`: fp16 (bit-exact), bf16
+// (the reference's cast of the fp16 weight to the activation dtype before its
+// GEMM, vq_dense.py:288, 294) or the split bf16 rows of the fp32 path; rows
+// of ld >= IN elements (per part), zero past IN. ld % D == 0.
+int dequant_rows(const vqk_weights *w, int64_t r0, int64_t rows, uint16_t *out, int mode, int64_t ld,
+                 hipStream_t st) {
     Geom g;
     int rc = make_geom(w, &g);
     if (rc) return rc;
-    return launch_dequant(w, g, nullptr, r0, rows, out, st, 1);
+    if (ld % g.D) return set_error(VQK_EINVAL, "dequant row stride %lld", (long long)ld);
+    return launch_dequant(w, g, nullptr, r0, rows, out, st, mode, ld);
 }
 
 }  // namespace vqk
