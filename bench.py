@@ -85,6 +85,11 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+L2_REQ_PER_CLK_PER_CU = 0.5      # 16 L2 channels per XCD, one request per clock each, 32 CUs
+N_CUS = 256
+PEAK_CLOCK_GHZ = 2.4
+
+
 def measured_traffic(name, key="traffic_bytes_per_call"):
     """HBM bytes per call (or per step) from the committed counter profile of
     this workload (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
@@ -657,6 +662,17 @@ def main():
                      "alg_bytes_per_call": int(alg_per_call), "us_per_call_events": round(us_call, 3)},
         "cpu_baseline": cpu,
     }
+    # tables beyond LDS: the codes past the LDS part are gathered from L2, whose
+    # 16 channels per XCD take one request per clock (0.5 per clock per CU);
+    # the committed counter profile gives the L1 -> L2 read requests per call
+    req = measured_traffic(f"moe_layer_{a.workload}_traffic.md", "l2_read_requests_per_call")
+    if req:
+        floor_us = req / (L2_REQ_PER_CLK_PER_CU * N_CUS * PEAK_CLOCK_GHZ * 1e3)
+        out["roofline"]["l2_request_floor"] = {
+            "requests_per_call": req, "floor_us": round(floor_us, 2),
+            "achieved_us": round(us_call, 3), "frac": round(floor_us / us_call, 4),
+            "basis": f"{L2_REQ_PER_CLK_PER_CU} L2 requests per clock per CU x {N_CUS} CUs x "
+                     f"{PEAK_CLOCK_GHZ} GHz (published peak clock)"}
     print(json.dumps(out), flush=True)
 
 

@@ -98,6 +98,43 @@ def test_wdec_bit_exact(D, K, packed):
     assert np.array_equal(_u16(part), w[30:40])
 
 
+@pytest.mark.parametrize("D", [2, 4, 8])
+@pytest.mark.parametrize("rows,r0", [(1, 0), (3, 5), (7, 0), (13, 2), (48, 0)])
+def test_wdec_special_products_ragged_rows(D, rows, r0):
+    """Every fp16 product class the dequant can meet -- subnormal results and
+    inputs, signed zeros, overflow to inf, RNE ties, inf / NaN / zero /
+    subnormal scales -- at row counts that leave the last stride of rows
+    partly filled and at row offsets: bit for bit (NaN positions by class)."""
+    from vqlab_amd import vq_switch as VS
+    print(f"wdec special products D={D} rows={rows} r0={r0}", flush=True)
+    rng = np.random.default_rng(100 * D + rows + r0)
+    K, IN, OUT = 16, 256, 64
+    m = make_module(rng, 1, OUT, IN, D, K, packed=True)
+    specials = np.array([2.0 ** -20, -0.0, 2.0 ** -24, 65504.0, -(2.0 ** -14), 1 + 2.0 ** -10,
+                         0.5 + 2.0 ** -11, 3.0, -2.0 ** -23, 1.0, -1.5, 2.0 ** -14, 7.0, 0.0,
+                         -65504.0, 2.0 ** -17], np.float16)
+    cb = np.stack([np.roll(specials, i)[:K] for i in range(D)], axis=1)
+    m["codebook"] = np.ascontiguousarray(cb.astype(np.float16))
+    svals = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 2.0 ** -24, 1.5, 1 + 2.0 ** -10,
+                      1024.0, 0.75, 2.0 ** -10, 1.0], np.float16)
+    m["scales"] = rng.choice(svals, m["scales"].shape).astype(np.float16)
+    m["stored"] = vo.pack(m["codes"], m["pack_bits"])
+    codes, cbd, sc = to_device(m)
+    want = vo.dequant(m["codes"].reshape(OUT, -1), m["codebook"], m["scales"].reshape(OUT, -1),
+                      64)[r0:r0 + rows]
+    got = VS.wdec_decode(codes, cbd, sc, rows, IN, 64, m["pack_bits"], r0=r0)
+    g, w = _u16(got), want.view(np.uint16)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got.float().cpu().numpy()), nan)
+    assert np.array_equal(g[~nan], w[~nan])
+    if rows < 13:
+        return
+    # the classes the case is meant to reach are all present
+    wf = want[~nan].astype(np.float32)
+    assert np.isinf(wf).any() and (wf == 0).any() and np.signbit(wf[wf == 0]).any()
+    assert ((np.abs(wf) > 0) & (np.abs(wf) < 2.0 ** -14)).any()        # subnormal results
+
+
 def test_decode_chunk_experts_and_skipzero():
     from vqlab_amd import vq_switch as VS
     rng = np.random.default_rng(5)

@@ -342,7 +342,9 @@ constexpr int kHybUpBytes = 64 * 1024;
 constexpr int kHybDownBytes = 112 * 1024;
 // Larger LDS parts when the workgroup's activations leave room (the host
 // checks): every entry moved into LDS is an L2 request per code saved.
-constexpr int kHybDownWideBytes = 136 * 1024;
+// 132 KB leaves room for 11 pairs' SwiGLU rows of a d8 row (config 3: 10 routed +
+// the shared expert) beside the routing scratch; 136 KB did not.
+constexpr int kHybDownWideBytes = 132 * 1024;
 // Waves of the workgroups with the larger LDS parts (one workgroup per CU),
 // which read x from LDS: two per SIMD, so one wave decodes while the other
 // waits on its table reads (12 for gate / up measured no faster, 16 for down
