@@ -48,6 +48,15 @@ extern "C" {
 #define VQK_I32   6
 #define VQK_I64   7
 
+/* Output rounding flag, OR'd into the y_type of any GEMV / GEMM / layer entry
+ * point: the fp32 result is rounded to fp16 first, then into y's type -- the
+ * arithmetic of the reference's default decode path, whose fused kernels
+ * return fp16 that the caller then casts to x's dtype (vq_switch.py:5306-5308,
+ * 5423). Without it a result is rounded once, from fp32, into y's type (the
+ * reference with VQ_DECODE_BF16IO=1, vq_switch.py:4421, 5303-5306). x types
+ * take no flags. */
+#define VQK_VIA_F16 0x100
+
 /* One VQ-coded linear, or a stack of E expert linears sharing one codebook
  * (VQSwitchLinear, vq_switch.py:5198-5234; VQLinear, vq_dense.py:322-334).
  *
@@ -237,6 +246,54 @@ int vqk_dense_fits(int64_t K, int64_t IN, int32_t G, int32_t D);
 int vqk_wdec_fits(int32_t D, int64_t NSUB, int32_t G, int32_t pack_bits);
 int vqk_gemmseg_fits(int32_t D, int64_t K, int32_t G, int32_t pack_bits,
                      int64_t IN);
+
+/* ---- options: the reference's VQ_* dispatch flags as one explicit struct ----
+ * The reference steers dispatch with module-global booleans read from the
+ * environment at import (vq_switch.py:43-45, 4372, 4421; vq_dense.py:55-102).
+ * Here they are arguments: a caller fills a vqk_options (vqk_options_default,
+ * or vqk_options_from_env for A/B runs -- the library reads the environment
+ * only when asked to) and passes it to the dispatching entry points below.
+ *   fused_max_n        VQ_FUSED_MAX_N: routed pairs up to which
+ *                      vqk_switch_apply runs the fused GEMV (default 512)
+ *   dense_fused_max_n  VQ_DENSE_FUSED_MAX_N: rows up to which vqk_linear_apply
+ *                      runs the fused GEMV (default 32)
+ *   decode_bf16io      VQ_DECODE_BF16IO: 0 (default) = the fused routed path
+ *                      rounds its outputs through fp16 (VQK_VIA_F16); 1 = once
+ *                      into y's type
+ *   prefill_bf16io     VQ_GEMMSEG_BF16IO: the same for the grouped GEMM path */
+typedef struct vqk_options {
+    int64_t fused_max_n;
+    int64_t dense_fused_max_n;
+    int32_t decode_bf16io;
+    int32_t prefill_bf16io;
+} vqk_options;
+void vqk_options_default(vqk_options *o);
+void vqk_options_from_env(vqk_options *o);
+
+/* VQSwitchLinear.__call__'s dispatch (vq_switch.py:5284-5423): the fused GEMV
+ * (vqk_moe_expert_gemv) for at most fused_max_n pairs, else -- or when the
+ * pairs crowd onto few experts (N >= 4 and N >= 2E: the GEMV would read an
+ * expert's rows once per pair) -- the grouped GEMM (vqk_grouped_gemm), when
+ * it takes the module's format. Same arguments as vqk_grouped_gemm plus the
+ * options (NULL = defaults); the workspace query returns 0 when the call
+ * will run the GEMV. */
+int vqk_switch_apply_workspace(const vqk_weights *w, int64_t N, const vqk_options *o,
+                               size_t *bytes);
+int vqk_switch_apply(const vqk_weights *w, const void *x, int32_t x_type,
+                     int64_t T, const uint32_t *eidx, int64_t N, int64_t xkrep,
+                     void *y, int32_t y_type, void *workspace, size_t ws_bytes,
+                     const vqk_options *o, void *stream);
+
+/* VQLinear.__call__'s dispatch (vq_dense.py:347-441): the fused dense GEMV
+ * (vqk_dense_gemv) for at most dense_fused_max_n rows when the shape has a
+ * fused kernel (vqk_dense_fits), else the decode-then-GEMM path
+ * (vqk_dense_gemm). Outputs are rounded once into y's type, as the
+ * reference's dense kernels write x's dtype directly. */
+int vqk_linear_apply_workspace(const vqk_weights *w, int64_t N, const vqk_options *o,
+                               size_t *bytes);
+int vqk_linear_apply(const vqk_weights *w, const void *x, int32_t x_type, int64_t N,
+                     void *y, int32_t y_type, void *workspace, size_t ws_bytes,
+                     const vqk_options *o, void *stream);
 
 /* ---- a14: skipzero row table (skipzero_row_table, vq_switch.py:4958-4973) --
  * rowmask uint8 [E, ceil(OUT / 8)] little bit order -> int32 [E, OUT],

@@ -274,3 +274,49 @@ def test_noalloc_scratch_size_matches_header(L):
     m = re.search(r"#define\s+VQK_NOALLOC_SCRATCH_BYTES\s+\((\d+)u\s*<<\s*(\d+)\)", txt)
     assert m, "VQK_NOALLOC_SCRATCH_BYTES not found"
     assert int(m.group(1)) << int(m.group(2)) == L.VQK_NOALLOC_SCRATCH_BYTES
+
+
+def test_options_defaults_and_env(L, monkeypatch):
+    """vqk_options: the reference's dispatch defaults (VQ_FUSED_MAX_N 512,
+    dense cutoff 32, fp16 outputs), and the VQ_* variables read only when
+    vqk_options_from_env is asked to."""
+    o = L.options()
+    assert (o.fused_max_n, o.dense_fused_max_n, o.decode_bf16io, o.prefill_bf16io) == (512, 32, 0, 0)
+    monkeypatch.setenv("VQ_FUSED_MAX_N", "77")
+    monkeypatch.setenv("VQ_DENSE_FUSED_MAX_N", "5")
+    monkeypatch.setenv("VQ_DECODE_BF16IO", "1")
+    monkeypatch.setenv("VQ_GEMMSEG_BF16IO", "0")
+    e = L.options(from_env=True)
+    assert (e.fused_max_n, e.dense_fused_max_n, e.decode_bf16io, e.prefill_bf16io) == (77, 5, 1, 0)
+    assert L.options().fused_max_n == 512            # defaults ignore the environment
+    monkeypatch.setenv("VQ_FUSED_MAX_N", "not a number")
+    assert L.options(from_env=True).fused_max_n == 512
+
+
+def test_apply_workspace_follows_dispatch(L):
+    """vqk_switch_apply_workspace is 0 where the fused GEMV runs (few pairs)
+    and the grouped GEMM's size where it does not (many pairs, or pairs
+    crowding onto few experts); vqk_linear_apply_workspace likewise."""
+    import ctypes
+    import numpy as np
+    w = L.VQKWeights()
+    w.codes, w.code_cols, w.code_type, w.pack_bits = 1 << 20, 16 * 12, L.VQK_U32, 12
+    w.codebook, w.K, w.D, w.group = 1 << 24, 4096, 4, 64
+    w.scales, w.E, w.OUT, w.IN = 1 << 28, 512, 256, 2048
+    ws, g = ctypes.c_size_t(), ctypes.c_size_t()
+    o = L.options()
+    # E = 512: VQ_FUSED_MAX_N decides; E = 64: 128 pairs crowd (N >= 2E)
+    for E, N, grouped in [(512, 8, False), (512, 512, False), (512, 513, True), (64, 100, False),
+                          (64, 128, True)]:
+        w.E = E
+        L.check(L.lib().vqk_switch_apply_workspace(ctypes.byref(w), N, ctypes.byref(o), ctypes.byref(ws)))
+        L.check(L.lib().vqk_grouped_gemm_workspace(ctypes.byref(w), N, ctypes.byref(g)))
+        assert ws.value == (g.value if grouped else 0), (N, ws.value)
+    small = L.options(fused_max_n=4)
+    L.check(L.lib().vqk_switch_apply_workspace(ctypes.byref(w), 8, ctypes.byref(small), ctypes.byref(ws)))
+    assert ws.value > 0
+    w.E = 1
+    for N, fused in [(1, True), (32, True), (65, False)]:        # 33..64: segment kernel, no workspace
+        L.check(L.lib().vqk_linear_apply_workspace(ctypes.byref(w), N, ctypes.byref(o), ctypes.byref(ws)))
+        assert (ws.value == 0) == fused, (N, ws.value)
+    assert np.int64(L.VQK_VIA_F16) == 0x100

@@ -17,6 +17,7 @@ LIB_PATH = pathlib.Path(os.environ.get("VQK_LIBRARY") or
 VQK_OK, VQK_ENOTIMPL, VQK_EINVAL, VQK_ESHARDED, VQK_EDEVICE, VQK_ENOSPACE = range(6)
 VQK_F16, VQK_BF16, VQK_F32, VQK_U8, VQK_U16, VQK_U32, VQK_I32, VQK_I64 = range(8)
 VQK_NOALLOC_SCRATCH_BYTES = 32 << 20     # include/vqk.h
+VQK_VIA_F16 = 0x100                      # output type flag: round through fp16 first
 
 c_i32, c_i64, c_p, c_sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
 
@@ -34,6 +35,11 @@ class VQKMoeDesc(ctypes.Structure):
                 ("sh_up", ctypes.POINTER(VQKWeights)), ("sh_down", ctypes.POINTER(VQKWeights)),
                 ("sh_gate_vec", c_p), ("sh_gate_vec_type", c_i32), ("top_k", c_i32),
                 ("norm_topk", c_i32)]
+
+
+class VQKOptions(ctypes.Structure):
+    _fields_ = [("fused_max_n", c_i64), ("dense_fused_max_n", c_i64),
+                ("decode_bf16io", c_i32), ("prefill_bf16io", c_i32)]
 
 
 # name -> (restype, argtypes), one entry per function of include/vqk.h
@@ -72,6 +78,16 @@ SIGNATURES = {
     "vqk_wdec_fits": (c_i32, [c_i32, c_i64, c_i32, c_i32]),
     "vqk_gemmseg_fits": (c_i32, [c_i32, c_i64, c_i32, c_i32, c_i64]),
     "vqk_skipzero_row_table_host": (c_i32, [c_p, c_i64, c_i64, c_p, ctypes.POINTER(c_i64)]),
+    "vqk_options_default": (None, [ctypes.POINTER(VQKOptions)]),
+    "vqk_options_from_env": (None, [ctypes.POINTER(VQKOptions)]),
+    "vqk_switch_apply_workspace": (c_i32, [ctypes.POINTER(VQKWeights), c_i64,
+                                           ctypes.POINTER(VQKOptions), ctypes.POINTER(c_sz)]),
+    "vqk_switch_apply": (c_i32, [ctypes.POINTER(VQKWeights), c_p, c_i32, c_i64, c_p, c_i64,
+                                 c_i64, c_p, c_i32, c_p, c_sz, ctypes.POINTER(VQKOptions), c_p]),
+    "vqk_linear_apply_workspace": (c_i32, [ctypes.POINTER(VQKWeights), c_i64,
+                                           ctypes.POINTER(VQKOptions), ctypes.POINTER(c_sz)]),
+    "vqk_linear_apply": (c_i32, [ctypes.POINTER(VQKWeights), c_p, c_i32, c_i64, c_p, c_i32, c_p,
+                                 c_sz, ctypes.POINTER(VQKOptions), c_p]),
 }
 
 _LIB = None
@@ -91,6 +107,16 @@ def lib():
             f.argtypes = args
         _LIB = L
     return _LIB
+
+
+def options(from_env: bool = False, **fields) -> VQKOptions:
+    """A vqk_options: the defaults, or (from_env) the defaults overridden by
+    the reference's VQ_* variables where set; keyword fields override both."""
+    o = VQKOptions()
+    (lib().vqk_options_from_env if from_env else lib().vqk_options_default)(ctypes.byref(o))
+    for k, v in fields.items():
+        setattr(o, k, v)
+    return o
 
 
 def last_error() -> str:

@@ -72,6 +72,8 @@ int make_geom(const vqk_weights *w, Geom *g);
 
 // Activation (x / y) element size in bytes for VQK_F16 / VQK_BF16 / VQK_F32.
 int act_size(int32_t type);
+// Output element size: act_size of an output type that may carry VQK_VIA_F16.
+int out_size(int32_t type);
 
 // ------------------------------------------------------ device conversions
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
@@ -110,6 +112,10 @@ __device__ __forceinline__ float load_act(const void *p, int32_t type, int64_t i
 }
 
 __device__ __forceinline__ void store_act(void *p, int32_t type, int64_t i, float v) {
+    if (type & VQK_VIA_F16) {                // round through fp16 first
+        v = h_to_f32(f32_to_h(v));
+        type &= ~VQK_VIA_F16;
+    }
     if (type == VQK_F32) { static_cast<float *>(p)[i] = v; return; }
     static_cast<uint16_t *>(p)[i] = type == VQK_BF16 ? f32_to_bf16(v) : f32_to_h(v);
 }

@@ -1,0 +1,124 @@
+// Options and the two dispatching entry points: VQSwitchLinear.__call__ and
+// VQLinear.__call__'s choice between the fused GEMV and the matrix-core
+// paths, with the reference's VQ_* flags as arguments (vqk_options) instead
+// of module-global environment reads.
+#include <stdlib.h>
+
+#include "vqk_common.h"
+
+using namespace vqk;
+
+namespace {
+
+constexpr int64_t kFusedMaxN = 512;       // vq_switch.py:43-45
+constexpr int64_t kDenseFusedMaxN = 32;   // vq_dense.py:55-102
+
+vqk_options resolved(const vqk_options *o) {
+    vqk_options r;
+    vqk_options_default(&r);
+    if (o) {
+        if (o->fused_max_n > 0) r.fused_max_n = o->fused_max_n;
+        if (o->dense_fused_max_n > 0) r.dense_fused_max_n = o->dense_fused_max_n;
+        r.decode_bf16io = o->decode_bf16io ? 1 : 0;
+        r.prefill_bf16io = o->prefill_bf16io ? 1 : 0;
+    }
+    return r;
+}
+
+int64_t env_i64(const char *name, int64_t dflt) {
+    const char *v = getenv(name);
+    if (!v || !*v) return dflt;
+    char *end = nullptr;
+    const long long n = strtoll(v, &end, 10);
+    return (end && *end == 0) ? int64_t(n) : dflt;
+}
+
+// The grouped GEMM for N pairs of module w (else the fused GEMV).
+bool switch_grouped(const vqk_weights *w, const Geom &g, int64_t N, const vqk_options &o) {
+    const bool crowded = N >= 4 && N >= 2 * g.E;
+    if (N <= o.fused_max_n && !crowded) return false;
+    return vqk_gemmseg_fits(g.D, g.K, g.G, w->pack_bits, g.IN) != 0;
+}
+
+bool linear_fused(const Geom &g, int64_t N, const vqk_options &o) {
+    return N <= o.dense_fused_max_n && vqk_dense_fits(g.K, g.IN, g.G, g.D) != 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+void vqk_options_default(vqk_options *o) {
+    if (!o) return;
+    o->fused_max_n = kFusedMaxN;
+    o->dense_fused_max_n = kDenseFusedMaxN;
+    o->decode_bf16io = 0;
+    o->prefill_bf16io = 0;
+}
+
+void vqk_options_from_env(vqk_options *o) {
+    if (!o) return;
+    vqk_options_default(o);
+    o->fused_max_n = env_i64("VQ_FUSED_MAX_N", kFusedMaxN);
+    o->dense_fused_max_n = env_i64("VQ_DENSE_FUSED_MAX_N", kDenseFusedMaxN);
+    o->decode_bf16io = env_i64("VQ_DECODE_BF16IO", 0) == 1;
+    o->prefill_bf16io = env_i64("VQ_GEMMSEG_BF16IO", 0) == 1;
+}
+
+int vqk_switch_apply_workspace(const vqk_weights *w, int64_t N, const vqk_options *opt, size_t *bytes) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if (!bytes || N < 0) return set_error(VQK_EINVAL, "bad arguments");
+    const vqk_options o = resolved(opt);
+    if (!switch_grouped(w, g, N, o)) {
+        *bytes = 0;
+        return VQK_OK;
+    }
+    return vqk_grouped_gemm_workspace(w, N, bytes);
+}
+
+int vqk_switch_apply(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
+                     const uint32_t *eidx, int64_t N, int64_t xkrep, void *y, int32_t y_type,
+                     void *workspace, size_t ws_bytes, const vqk_options *opt, void *stream) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if (N < 0) return set_error(VQK_EINVAL, "N=%lld", (long long)N);
+    const vqk_options o = resolved(opt);
+    const bool grouped = switch_grouped(w, g, N, o);
+    // the reference's default: fused (and grouped) outputs come back as fp16
+    // and are cast to x's dtype by the caller (vq_switch.py:5306-5308, 5423)
+    const bool via = grouped ? !o.prefill_bf16io : !o.decode_bf16io;
+    const int32_t yt = via ? (y_type | VQK_VIA_F16) : y_type;
+    if (grouped)
+        return vqk_grouped_gemm(w, x, x_type, T, eidx, N, xkrep, y, yt, workspace, ws_bytes, stream);
+    return vqk_moe_expert_gemv(w, x, x_type, T, eidx, N, xkrep, y, yt, stream);
+}
+
+int vqk_linear_apply_workspace(const vqk_weights *w, int64_t N, const vqk_options *opt, size_t *bytes) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if (!bytes || N < 0) return set_error(VQK_EINVAL, "bad arguments");
+    const vqk_options o = resolved(opt);
+    if (linear_fused(g, N, o)) {
+        *bytes = 0;
+        return VQK_OK;
+    }
+    return vqk_dense_gemm_workspace(w, N, bytes);
+}
+
+int vqk_linear_apply(const vqk_weights *w, const void *x, int32_t x_type, int64_t N, void *y,
+                     int32_t y_type, void *workspace, size_t ws_bytes, const vqk_options *opt,
+                     void *stream) {
+    Geom g;
+    int rc = make_geom(w, &g);
+    if (rc) return rc;
+    if (N < 0) return set_error(VQK_EINVAL, "N=%lld", (long long)N);
+    const vqk_options o = resolved(opt);
+    if (linear_fused(g, N, o)) return vqk_dense_gemv(w, x, x_type, N, y, y_type, stream);
+    return vqk_dense_gemm(w, x, x_type, N, y, y_type, workspace, ws_bytes, stream);
+}
+
+}  // extern "C"

@@ -466,7 +466,7 @@ static int launch_gemm(const GemmParams &p, const Geom &g, dim3 grid, hipStream_
 }
 
 static int check_acts(const void *x, int32_t x_type, const void *y, int32_t y_type) {
-    if (!act_size(x_type) || !act_size(y_type))
+    if (!act_size(x_type) || !out_size(y_type))
         return set_error(VQK_EINVAL, "x/y type must be VQK_F16, VQK_BF16 or VQK_F32");
     if (!x || !y) return set_error(VQK_EINVAL, "x and y are required");
     return VQK_OK;

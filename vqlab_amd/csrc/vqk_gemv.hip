@@ -47,7 +47,7 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
     Geom g;
     int rc = make_geom(w, &g);
     if (rc) return rc;
-    if (!act_size(x_type) || !act_size(y_type))
+    if (!act_size(x_type) || !out_size(y_type))
         return set_error(VQK_EINVAL, "x/y type must be VQK_F16, VQK_BF16 or VQK_F32");
     if (!x || !y) return set_error(VQK_EINVAL, "x and y are required");
     if (N < 0 || T < 0 || xkrep < 1 || N != T * xkrep)

@@ -31,6 +31,10 @@ int act_size(int32_t type) {
     }
 }
 
+int out_size(int32_t type) {
+    return (type & ~int32_t(VQK_VIA_F16 | 0xff)) ? 0 : act_size(type & 0xff);
+}
+
 static int64_t wpr_of(int64_t nsub, int bits) { return (nsub + kBlock - 1) / kBlock * bits; }
 
 int make_geom(const vqk_weights *w, Geom *g) {

@@ -1323,7 +1323,7 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, i
     MoePlan pl;
     int rc = moe_plan(m, T, &pl);
     if (rc) return rc;
-    if (!act_size(x_type) || !act_size(y_type))
+    if (!act_size(x_type) || !out_size(y_type))
         return set_error(VQK_EINVAL, "x/y type must be VQK_F16, VQK_BF16 or VQK_F32");
     if (!x || !y || !logits) return set_error(VQK_EINVAL, "x, logits and y are required");
     if (!workspace || ws_bytes < pl.lay.total)

@@ -8,16 +8,16 @@
                                                      vq_dense.py:262-312
   VQEmbedding(codes, codebook, vq_scales, ...)       vq_dense.py:444-513
 
-Small N runs the fused GEMV (vqk_dense_gemv). Large N runs vqk_dense_gemm:
-up to 64 rows W is decoded straight into matrix-core operands; above, the
-weight is dequantised bit-exactly into a workspace panel and multiplied by an
-LDS-tiled fp16 matrix-core GEMM. VQEmbedding decodes only the gathered rows
-(vqk_embed_gather), in one launch.
+VQLinear dispatches through vqk_linear_apply: small N runs the fused GEMV
+(vqk_dense_gemv), large N vqk_dense_gemm -- up to 64 rows W is decoded
+straight into matrix-core operands; above, the weight is dequantised into a
+workspace panel in x's arithmetic type and multiplied by libvqk's matrix-core
+GEMM. VQEmbedding decodes only the gathered rows (vqk_embed_gather), in one
+launch.
 """
 from __future__ import annotations
 
 import ctypes
-import os
 
 import torch
 
@@ -25,16 +25,10 @@ from . import _lib as L
 from . import _torch as T
 from . import vq_switch as VS
 
-# Rows up to which the fused GEMV beats the dequant + matrix-core GEMM on
-# MI355X; keyed on pack state and d like the reference's cutoffs
-# (vq_dense.py:55-102). VQ_DENSE_FUSED_MAX_N overrides for A/B.
-_DENSE_FUSED_MAX_N_BY_D = {2: 32, 4: 32, 8: 32}
-
-
 def _fused_max_n(pack_bits, d):
-    if "VQ_DENSE_FUSED_MAX_N" in os.environ:
-        return int(os.environ["VQ_DENSE_FUSED_MAX_N"])
-    return _DENSE_FUSED_MAX_N_BY_D.get(int(d), 32)
+    """Rows up to which VQLinear runs the fused GEMV (vq_dense.py:55-102): the
+    options' dense_fused_max_n (VQ_DENSE_FUSED_MAX_N, default 32)."""
+    return int(VS.options().dense_fused_max_n)
 
 
 def _decode_matmul(xf, codes_in, codebook, scales, group_size, OUT, IN, pack_bits):
@@ -92,15 +86,22 @@ class VQLinear(torch.nn.Module):
         OUT, IN = self.output_dims, self.input_dims
         lead = x.shape[:-1]
         xf = x.reshape(-1, IN)
+        T.require_cuda(xf, self.codes, self.codebook, self.vq_scales)
         N = xf.shape[0]
-        K, d = int(self.codebook.shape[0]), int(self.codebook.shape[1])
         G = IN // int(self.vq_scales.shape[-1])
-        if N <= _fused_max_n(self.pack_bits, d) and VS.dense_fits(K, IN, G, d):
-            y = VS._dense_fused(xf, self.codes, self.codebook, self.vq_scales,
-                                pack_bits=self.pack_bits, in_features=self._in_features)
-        else:
-            y = _decode_matmul(xf, self.codes, self.codebook, self.vq_scales, G, OUT, IN,
-                               self.pack_bits)
+        keep = []
+        w = T.weights(self.codes, self.codebook, self.vq_scales, G, self.pack_bits, IN, keep=keep)
+        xf = xf.contiguous()
+        y = torch.empty((N, OUT), dtype=xf.dtype, device=xf.device)
+        o = VS.options()
+        ws = ctypes.c_size_t()
+        L.check(L.lib().vqk_linear_apply_workspace(ctypes.byref(w), N, ctypes.byref(o),
+                                                   ctypes.byref(ws)), "VQLinear")
+        work = torch.empty(ws.value, dtype=torch.uint8, device=xf.device) if ws.value else None
+        L.check(L.lib().vqk_linear_apply(ctypes.byref(w), T.ptr(xf), T.act_type(xf), N, T.ptr(y),
+                                         T.act_type(y), T.ptr(work) if work is not None else None,
+                                         ws.value, ctypes.byref(o), T.stream(xf.device)),
+                "VQLinear")
         return y.reshape(*lead, OUT)
 
 

@@ -20,7 +20,6 @@ current stream and never synchronises with the host.
 from __future__ import annotations
 
 import ctypes
-import os
 
 import numpy as np
 import torch
@@ -28,9 +27,18 @@ import torch
 from . import _lib as L
 from . import _torch as T
 
-# Pairs (token, expert) at or below which decode runs the fused GEMV; above,
-# the grouped GEMM (vq_switch.py:43-45).
-VQ_FUSED_MAX_N = int(os.environ.get("VQ_FUSED_MAX_N", "512"))
+# The reference's VQ_* dispatch flags -- VQ_FUSED_MAX_N (pairs at or below which
+# decode runs the fused GEMV, vq_switch.py:43-45), VQ_DECODE_BF16IO and
+# VQ_GEMMSEG_BF16IO (vq_switch.py:4372, 4421) -- read once at import as the
+# reference does, and handed to libvqk as one explicit options struct.
+OPTIONS = None
+
+
+def options():
+    global OPTIONS
+    if OPTIONS is None:
+        OPTIONS = L.options(from_env=True)
+    return OPTIONS
 
 
 # ------------------------------------------------------------ predicates
@@ -154,6 +162,33 @@ def _gemmseg(x2, eidx, codes, codebook, scales, pack_bits, IN, xkrep, rowtbl=Non
     return y
 
 
+def _switch_apply(x2, eidx, codes, codebook, scales, pack_bits, IN, xkrep, rowtbl=None,
+                  out_dtype=None, opts=None):
+    """VQSwitchLinear's dispatch through vqk_switch_apply with the module
+    options (or `opts`); out_dtype (an extension) rounds once into it."""
+    T.require_cuda(x2, eidx, codes, codebook, scales, rowtbl)
+    G = _group(IN, scales)
+    keep = []
+    w = T.weights(codes, codebook, scales, G, pack_bits, IN, rowtbl, keep=keep)
+    x2 = x2.contiguous()
+    e = eidx.reshape(-1).to(torch.int32).contiguous()
+    N = e.numel()
+    o = opts or options()
+    if out_dtype is not None:
+        o = L.options(fused_max_n=o.fused_max_n, dense_fused_max_n=o.dense_fused_max_n,
+                      decode_bf16io=1, prefill_bf16io=1)
+    ws = ctypes.c_size_t()
+    L.check(L.lib().vqk_switch_apply_workspace(ctypes.byref(w), N, ctypes.byref(o),
+                                               ctypes.byref(ws)), "VQSwitchLinear")
+    work = torch.empty(ws.value, dtype=torch.uint8, device=x2.device) if ws.value else None
+    y = torch.empty((N, w.OUT), dtype=out_dtype or x2.dtype, device=x2.device)
+    L.check(L.lib().vqk_switch_apply(ctypes.byref(w), T.ptr(x2), T.act_type(x2), x2.shape[0],
+                                     T.ptr(e), N, int(xkrep), T.ptr(y), T.act_type(y),
+                                     T.ptr(work) if work is not None else None, ws.value,
+                                     ctypes.byref(o), T.stream(x2.device)), "VQSwitchLinear")
+    return y
+
+
 # ------------------------------------------------------------- skipzero
 def skipzero_row_table(rowmask, E, OUT):
     """uint8 [E, ceil(OUT/8)] live-row mask (little bit order) -> int32 [E, OUT]
@@ -251,20 +286,13 @@ class VQSwitchLinear(torch.nn.Module):
             lead = tuple(indices.shape)
             x2, rep = x.expand(*lead, 1, IN).reshape(N, IN), 1
         eidx = indices.reshape(-1)
-        # The fused GEMV reads an expert's rows once per pair; when the pairs
-        # crowd onto few experts (a shared expert under a token batch, N >= 2E)
-        # the grouped GEMM, which reads them once per tile of up to 16 pairs,
-        # wins even below VQ_FUSED_MAX_N. Same outputs either way.
-        crowded = N >= 4 and N >= 2 * self.num_experts
-        if (N <= VQ_FUSED_MAX_N and not crowded) or not gemmseg_fits(
-                int(self.codebook.shape[1]), int(self.codebook.shape[0]), self.group_size,
-                self.pack_bits, IN):
-            y = _fused(x2, eidx, self.codes, self.codebook, self.vq_scales,
-                       pack_bits=self.pack_bits, xkrep=rep, rowtbl=self.row_table,
-                       in_features=IN, out_dtype=out_dtype)
-        else:
-            y = _gemmseg(x2, eidx, self.codes, self.codebook, self.vq_scales, self.pack_bits,
-                         IN, rep, self.row_table, out_dtype=out_dtype)
+        # libvqk's dispatch (vqk_switch_apply): the fused GEMV up to
+        # VQ_FUSED_MAX_N pairs, else -- or when the pairs crowd onto few
+        # experts, N >= 4 and N >= 2E -- the grouped GEMM. By default the
+        # outputs are rounded through fp16 like the reference's fp16 kernels
+        # and cast; an explicit out_dtype keeps the single rounding.
+        y = _switch_apply(x2, eidx, self.codes, self.codebook, self.vq_scales, self.pack_bits,
+                          IN, rep, self.row_table, out_dtype=out_dtype)
         return y.reshape(*indices.shape, 1, OUT)
 
 
