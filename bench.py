@@ -32,7 +32,7 @@ value = packed GB/s of the live rows of the touched experts.
 
 --workload c1 (the reference's CPU-runnable case): one
 dense VQ GEMV per call (W 4096x4096, d=2, K=256, uint8 codes, x [1, 4096]
-bf16) over 48 distinct weights (403 MB) so each call streams from HBM; value
+bf16) over 120 distinct weights (1.07 GB) so each call streams from HBM; value
 = packed GB/s of codes + scales; cpu_baseline: the same GEMV as fp16 dequant +
 fp32 matvec on the host, one thread and all cores.
 
@@ -55,7 +55,7 @@ HBM_PEAK_GBS = 8000.0
 
 WORKLOADS = {
     # the reference's CPU-runnable case, on the GPU: one dense VQ GEMV per call
-    "c1": dict(OUT=4096, IN=4096, d=2, K=256, G=64, layers=48, kind="dense_gemv",
+    "c1": dict(OUT=4096, IN=4096, d=2, K=256, G=64, layers=120, kind="dense_gemv",
                desc="Single dense VQ linear, decode GEMV: W 4096x4096, d=2, K=256, uint8 codes, "
                     "x [1, 4096] (BASELINE configs[0])"),
     # name: (H, E, I, top_k, shared, d, K, bits, T, layers)
@@ -434,7 +434,7 @@ def run_mtp(torch, dev, a, w):
 
 def run_dense_gemv(torch, dev, a, w):
     """c1: one dense VQ GEMV per call (VQLinear, N = 1 -> vqk_dense_gemv), over
-    `layers` distinct weights (403 MB, past the 256 MB MALL) so every call
+    `layers` distinct weights (1.07 GB, four times the 256 MB MALL) so every call
     streams its weight from HBM."""
     from vqlab_amd.vq_dense import VQLinear
     g = torch.Generator(device=dev)
