@@ -100,80 +100,117 @@ struct DequantArgs {
     int mode;                // kDqF16, kDqBF16 or kDqSplit
 };
 
-// One thread per (output row, code): writes D halves with one vector store.
+// Code row of output row `orow`, or -1 for a dead skipzero row, an expert id
+// outside [0, E) or a corrupt table entry (the row is written as zeros).
+__device__ __forceinline__ int64_t dq_code_row(const DequantArgs &a, int64_t orow) {
+    int64_t flat;                           // row of the expanded [E*OUT] module
+    if (a.eidx) {
+        const uint32_t e = a.eidx[orow / a.OUT];
+        flat = e < uint64_t(a.E) ? int64_t(e) * a.OUT + orow % a.OUT : -1;
+    } else {
+        flat = a.r0 + orow;
+    }
+    int64_t cr = -1;
+    if (flat >= 0) cr = a.row_table ? int64_t(a.row_table[flat]) : flat;
+    return cr < a.stored_rows ? cr : -1;    // never read past the codes
+}
+
+// The D-half table entry `c` as ONE vector load (D * 2 bytes): a gather per
+// half would multiply the L2 requests that bound this kernel.
+template <int D>
+__device__ __forceinline__ void dq_entry(const uint16_t *cb, uint32_t c, uint16_t (&e)[D]) {
+    if constexpr (D == 8) {                  // through the global address space
+        const u32x4 ev = load_global(reinterpret_cast<const u32x4 *>(cb), int64_t(c));
+        __builtin_memcpy(e, &ev, sizeof e);
+    } else if constexpr (D == 4) {
+        const u32x2 ev = load_global(reinterpret_cast<const u32x2 *>(cb), int64_t(c));
+        __builtin_memcpy(e, &ev, sizeof e);
+    } else {
+        const uint32_t ev = load_global(reinterpret_cast<const uint32_t *>(cb), int64_t(c));
+        __builtin_memcpy(e, &ev, sizeof e);
+    }
+}
+
+// One thread per code column j, kDqRows output rows at a time (rows
+// blockIdx.y + i * gridDim.y of the stride): each phase -- code rows, codes,
+// scales, table entries, stores -- is issued for all of them before the next
+// waits, so a thread has kDqRows memory chains in flight instead of one
+// (the kernel is bound by the latency of its code-load -> gather chain).
 // Threads past the last code of a row zero its padding up to out_ld.
+constexpr int kDqRows = 4;
 template <int D>
 __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
     const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (j * D >= a.out_ld) return;
     const bool pad = j >= a.NSUB;
-    for (int64_t orow = blockIdx.y; orow < a.rows; orow += gridDim.y) {
-        int64_t flat;                       // row of the expanded [E*OUT] module
-        int64_t cr = -1;
-        if (a.eidx) {
-            const uint32_t e = a.eidx[orow / a.OUT];
-            flat = e < uint64_t(a.E) ? int64_t(e) * a.OUT + orow % a.OUT : -1;
-        } else {
-            flat = a.r0 + orow;
+    const int64_t gy = gridDim.y;
+    for (int64_t o0 = blockIdx.y; o0 < a.rows; o0 += gy * kDqRows) {
+        int64_t cr[kDqRows];
+#pragma unroll
+        for (int i = 0; i < kDqRows; ++i) {
+            const int64_t orow = o0 + i * gy;
+            cr[i] = (orow < a.rows && !pad) ? dq_code_row(a, orow) : -1;
         }
-        if (flat >= 0) cr = a.row_table ? int64_t(a.row_table[flat]) : flat;
-        if (cr >= a.stored_rows) cr = -1;   // corrupt table entry: never read past the codes
-        uint16_t vals[D];
-        if (cr < 0 || pad) {
-            // dead skipzero row (+0), or an expert id outside [0, E)
+        uint32_t c[kDqRows];
+        uint16_t sc[kDqRows];
 #pragma unroll
-            for (int u = 0; u < D; ++u) vals[u] = 0;
-        } else {
-            uint32_t c;
-            if (a.bits) c = packed_code(static_cast<const uint32_t *>(a.codes) + cr * a.code_cols, j, a.bits);
-            else if (a.code_bytes == 1) c = static_cast<const uint8_t *>(a.codes)[cr * a.code_cols + j];
-            else c = static_cast<const uint16_t *>(a.codes)[cr * a.code_cols + j];
-            if (c >= uint32_t(a.K)) c = uint32_t(a.K - 1);   // never read past the table
-            const float s = h_to_f32(a.scales[cr * a.ngrp + (j * D) / a.G]);
-            // the entry as ONE vector load (D * 2 bytes): a gather per half
-            // would multiply the L2 requests that bound this kernel
-            uint16_t e[D];
-            if constexpr (D == 8) {                  // through the global address space
-                const u32x4 ev = load_global(reinterpret_cast<const u32x4 *>(a.codebook), int64_t(c));
-                __builtin_memcpy(e, &ev, sizeof e);
-            } else if constexpr (D == 4) {
-                const u32x2 ev = load_global(reinterpret_cast<const u32x2 *>(a.codebook), int64_t(c));
-                __builtin_memcpy(e, &ev, sizeof e);
-            } else {
-                const uint32_t ev = load_global(reinterpret_cast<const uint32_t *>(a.codebook), int64_t(c));
-                __builtin_memcpy(e, &ev, sizeof e);
-            }
-#pragma unroll
-            for (int u = 0; u < D; ++u) {
+        for (int i = 0; i < kDqRows; ++i) {
+            c[i] = 0u;
+            sc[i] = 0;
+            if (cr[i] >= 0) {
+                if (a.bits) c[i] = packed_code(static_cast<const uint32_t *>(a.codes) + cr[i] * a.code_cols, j, a.bits);
+                else if (a.code_bytes == 1) c[i] = static_cast<const uint8_t *>(a.codes)[cr[i] * a.code_cols + j];
+                else c[i] = static_cast<const uint16_t *>(a.codes)[cr[i] * a.code_cols + j];
+                if (c[i] >= uint32_t(a.K)) c[i] = uint32_t(a.K - 1);   // never read past the table
                 // a group boundary can fall inside a subvector only if G % D != 0,
-                // which validation refuses; one scale serves all D values.
-                vals[u] = f32_to_h(s * h_to_f32(e[u]));
+                // which validation refuses; one scale serves all D values
+                sc[i] = a.scales[cr[i] * a.ngrp + (j * D) / a.G];
             }
         }
-        if (a.mode == kDqF16) {
-            store_halves<D>(a.out + orow * a.out_ld + j * D, vals);
-        } else {
-            // bf16(the fp16 value): one RNE (fp16 -> f32 is exact)
-            uint16_t hi[D];
+        uint16_t e[kDqRows][D];
 #pragma unroll
-            for (int u = 0; u < D; ++u) hi[u] = f32_to_bf16(h_to_f32(vals[u]));
-            if (a.mode == kDqBF16) {
-                store_halves<D>(a.out + orow * a.out_ld + j * D, hi);
+        for (int i = 0; i < kDqRows; ++i) {
+            if (cr[i] >= 0) {
+                dq_entry<D>(a.codebook, c[i], e[i]);
             } else {
-                // [W_hi | W_lo | W_hi] rows of 3 * IN: W_lo = W - W_hi has at
-                // most 3 significant bits (a multiple of the fp16 ulp no larger
-                // than half a bf16 ulp), so W_hi + W_lo is the fp16 value exactly
-                uint16_t lo[D];
 #pragma unroll
-                for (int u = 0; u < D; ++u) {
-                    const float w = h_to_f32(vals[u]), h = bf16_to_f32(hi[u]);
-                    lo[u] = (__float_as_uint(h) & 0x7f800000u) == 0x7f800000u ? uint16_t(0)
-                                                                              : f32_to_bf16(w - h);
+                for (int u = 0; u < D; ++u) e[i][u] = 0;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kDqRows; ++i) {
+            const int64_t orow = o0 + i * gy;
+            if (orow >= a.rows) continue;
+            // dead skipzero row, expert id outside [0, E) or padding column: +0
+            uint16_t vals[D];
+            const float s = h_to_f32(sc[i]);
+#pragma unroll
+            for (int u = 0; u < D; ++u) vals[u] = cr[i] >= 0 ? f32_to_h(s * h_to_f32(e[i][u])) : uint16_t(0);
+            if (a.mode == kDqF16) {
+                store_halves<D>(a.out + orow * a.out_ld + j * D, vals);
+            } else {
+                // bf16(the fp16 value): one RNE (fp16 -> f32 is exact)
+                uint16_t hi[D];
+#pragma unroll
+                for (int u = 0; u < D; ++u) hi[u] = f32_to_bf16(h_to_f32(vals[u]));
+                if (a.mode == kDqBF16) {
+                    store_halves<D>(a.out + orow * a.out_ld + j * D, hi);
+                } else {
+                    // [W_hi | W_lo | W_hi] rows of 3 * IN: W_lo = W - W_hi has at
+                    // most 3 significant bits (a multiple of the fp16 ulp no larger
+                    // than half a bf16 ulp), so W_hi + W_lo is the fp16 value exactly
+                    uint16_t lo[D];
+#pragma unroll
+                    for (int u = 0; u < D; ++u) {
+                        const float w = h_to_f32(vals[u]), h = bf16_to_f32(hi[u]);
+                        lo[u] = (__float_as_uint(h) & 0x7f800000u) == 0x7f800000u ? uint16_t(0)
+                                                                                  : f32_to_bf16(w - h);
+                    }
+                    uint16_t *dst = a.out + orow * 3 * a.out_ld + j * D;
+                    store_halves<D>(dst, hi);
+                    store_halves<D>(dst + a.out_ld, lo);
+                    store_halves<D>(dst + 2 * a.out_ld, hi);
                 }
-                uint16_t *dst = a.out + orow * 3 * a.out_ld + j * D;
-                store_halves<D>(dst, hi);
-                store_halves<D>(dst + a.out_ld, lo);
-                store_halves<D>(dst + 2 * a.out_ld, hi);
             }
         }
     }
