@@ -194,6 +194,8 @@ template <int BITS, int GPB>
 __device__ __forceinline__ void load_block(const GemvParams &p, int64_t cr, int blk, int sidx,
                                            uint32_t (&w)[BITS], uint32_t (&s)[GPB]) {
     if (cr >= 0) {
+        // streaming loads: config 1 ran 5.86 us per call with them, 6.33 us
+        // with plain loads (the fused layer's blocks take plain loads)
         const uint32_t *src = static_cast<const uint32_t *>(p.codes) + cr * p.row_words +
                               int64_t(blk) * BITS;
 #pragma unroll

@@ -68,8 +68,6 @@ struct MoeParams {
     float *gbuf, *ubuf;  // split gate/up phase: workspace [T, P, I] fp32 each, else NULL
     int32_t *ids_out;    // optional user copies
     float *wts_out;
-    int32_t co1, co2;    // coalesced code reads: gate / up (K1), down (K2)
-    int32_t tr1, tr2;    // byte offsets of the waves' LDS transpose buffers
 };
 
 // ------------------------------------------------------------ routing
@@ -311,13 +309,17 @@ __device__ __forceinline__ float shared_gate_dot(const void *x, int32_t x_type, 
 // One lane's code block and its scales' raw fp16 bits; the scales become
 // fp32 at their use (ScalesF32), so the wave's next loads (the up projection
 // after the gate, the table copy after the down weights) issue at once.
+// The code words are plain (cached) loads: lanes' blocks lie BITS words apart,
+// so each of the block's BITS/4 vector loads touches every 64-byte segment of
+// the row; the vector L1 serves the repeats, where streaming loads sent each
+// one to L2 again (config 3: 48.6 -> 44.7 us per layer; config 2 unchanged).
 template <int BITS, int GPB>
 __device__ __forceinline__ void moe_load(const MoeW &w, int64_t cr, int blk, int sidx, int ngrp,
                                          uint32_t (&wd)[BITS], uint32_t (&s)[GPB]) {
     if (cr >= 0) {
         const uint32_t *src = w.codes + cr * w.row_words + int64_t(blk) * BITS;
 #pragma unroll
-        for (int i = 0; i < BITS; ++i) wd[i] = __builtin_nontemporal_load(src + i);
+        for (int i = 0; i < BITS; ++i) wd[i] = src[i];
         const uint16_t *sr = w.scales + cr * ngrp + sidx;
 #pragma unroll
         for (int g = 0; g < GPB; ++g) s[g] = __builtin_nontemporal_load(sr + g);
@@ -327,82 +329,6 @@ __device__ __forceinline__ void moe_load(const MoeW &w, int64_t cr, int blk, int
 #pragma unroll
         for (int g = 0; g < GPB; ++g) s[g] = 0u;
     }
-}
-
-// The same block words read coalesced (BITS a multiple of 4, 16-byte aligned
-// rows): the `nb` lanes that share a row read its 16-byte chunks in order,
-// lane `blk` taking chunks blk, blk + nb, ... into wd[4i..4i+3], so each wave
-// instruction reads contiguous bytes. Per-lane block reads (48 bytes apart
-// for 12-bit codes) touched every 64-byte segment of the row in each of their
-// BITS/4 instructions: three times the L2 requests for the same bytes. The
-// words land in the wrong lanes until co_fix() moves them through LDS.
-template <int BITS, int GPB>
-__device__ __forceinline__ void moe_load_co(const MoeW &w, int64_t cr, int blk, int nb, int sidx,
-                                            int ngrp, uint32_t (&wd)[BITS], uint32_t (&s)[GPB]) {
-    static_assert(BITS % 4 == 0, "coalesced block reads take whole 16-byte chunks");
-    if (cr >= 0 && blk < nb) {
-        const u32x4 *row = reinterpret_cast<const u32x4 *>(w.codes + cr * w.row_words);
-#pragma unroll
-        for (int i = 0; i < BITS / 4; ++i) {
-            const u32x4 v = __builtin_nontemporal_load(row + blk + i * nb);
-            wd[4 * i] = v.x;
-            wd[4 * i + 1] = v.y;
-            wd[4 * i + 2] = v.z;
-            wd[4 * i + 3] = v.w;
-        }
-        const uint16_t *sr = w.scales + cr * ngrp + sidx;
-#pragma unroll
-        for (int g = 0; g < GPB; ++g) s[g] = __builtin_nontemporal_load(sr + g);
-    } else {
-#pragma unroll
-        for (int i = 0; i < BITS; ++i) wd[i] = 0u;
-#pragma unroll
-        for (int g = 0; g < GPB; ++g) s[g] = 0u;
-    }
-}
-
-// Chunks from moe_load_co -> the block words of each lane, through the
-// wave's BITS * 64 words of LDS at `tr`: every row group writes its chunks at
-// their row offsets (group base = its first lane x BITS words) and each lane
-// reads back the BITS words at lane x BITS. Lanes past `nb` hold no chunk and
-// write nothing (their slots belong to the group's real chunks).
-template <int BITS>
-__device__ __forceinline__ void co_fix(uint32_t *tr, int blk, int nb, uint32_t (&wd)[BITS]) {
-    const int lane = threadIdx.x & (kWave - 1);
-    u32x4 *base = reinterpret_cast<u32x4 *>(tr + (lane - blk) * BITS);
-    if (blk < nb) {
-#pragma unroll
-        for (int i = 0; i < BITS / 4; ++i)
-            base[blk + i * nb] = u32x4{wd[4 * i], wd[4 * i + 1], wd[4 * i + 2], wd[4 * i + 3]};
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    const u32x4 *mine = reinterpret_cast<const u32x4 *>(tr + lane * BITS);
-#pragma unroll
-    for (int i = 0; i < BITS / 4; ++i) {
-        const u32x4 v = mine[i];
-        wd[4 * i] = v.x;
-        wd[4 * i + 1] = v.y;
-        wd[4 * i + 2] = v.z;
-        wd[4 * i + 3] = v.w;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-}
-
-// Block load of either form, chosen at compile time (a run-time choice
-// splits the load sequence into blocks whose joins get full memory waits):
-// coalesced when CO, then co_fix before use.
-template <bool CO, int BITS, int GPB>
-__device__ __forceinline__ void moe_load_any(const MoeW &w, int64_t cr, int blk, int nb, int sidx,
-                                             int ngrp, uint32_t (&wd)[BITS], uint32_t (&s)[GPB]) {
-    if constexpr (CO) moe_load_co<BITS, GPB>(w, cr, blk, nb, sidx, ngrp, wd, s);
-    else moe_load<BITS, GPB>(w, cr, blk, sidx, ngrp, wd, s);
-}
-
-template <bool CO, int BITS>
-__device__ __forceinline__ void co_fix_any(uint32_t *tr, int blk, int nb, uint32_t (&wd)[BITS]) {
-    if constexpr (CO) co_fix<BITS>(tr, blk, nb, wd);
 }
 
 __device__ __forceinline__ int64_t moe_row(const MoeW &w, int64_t e, int OUT, int r) {
@@ -464,7 +390,7 @@ struct DownState {
 // K1 body: routing + gate/up + SwiGLU for pair `pair` of row tile `bx`. The
 // routing is left in `rl` (LDS), and `pre(rl)` runs right after it is
 // published and the first weight loads are out, before the decode.
-template <int D, int BITS, int GPB, bool CO, typename PRE>
+template <int D, int BITS, int GPB, typename PRE>
 __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, uint8_t *smem,
                                         RouteLds &rl, PRE pre) {
     constexpr bool CBL = cb_in_lds(D, BITS);
@@ -538,11 +464,10 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
         const bool ok = on && e >= 0 && r < p.I;
         crg = ok ? moe_row(wg, e, p.I, r) : -1;
         cru = ok ? moe_row(wu, e, p.I, r) : -1;
-        moe_load_any<CO, BITS, GPB>(wg, crg, blk, p.NB1, sidx, p.ngrp1, ag, sg_);
-        moe_load_any<CO, BITS, GPB>(wu, cru, blk, p.NB1, sidx, p.ngrp1, au, su_);
+        moe_load<BITS, GPB>(wg, crg, blk, sidx, p.ngrp1, ag, sg_);
+        moe_load<BITS, GPB>(wu, cru, blk, sidx, p.ngrp1, au, su_);
     }
     pre(rl);
-    uint32_t *tr = reinterpret_cast<uint32_t *>(smem + p.tr1) + wave * BITS * kWave;
 
     h2 xr[16 * D];
     load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
@@ -561,21 +486,15 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
             ncg = ok ? moe_row(wg, e, p.I, r) : -1;
             ncu = ok ? moe_row(wu, e, p.I, r) : -1;
         }
-        moe_load_any<CO, BITS, GPB>(wg, ncg, blk, p.NB1, sidx, p.ngrp1, ng, nsg);
-        moe_load_any<CO, BITS, GPB>(wu, ncu, blk, p.NB1, sidx, p.ngrp1, nu, nsu);
+        moe_load<BITS, GPB>(wg, ncg, blk, sidx, p.ngrp1, ng, nsg);
+        moe_load<BITS, GPB>(wu, ncu, blk, sidx, p.ngrp1, nu, nsu);
         float vg = 0.f, vu = 0.f;
         const ScalesF32<GPB> fg(sg_), fu(su_);
-        // the gate block decodes while the up block's words may still land
-        co_fix_any<CO, BITS>(tr, blk, p.NB1, ag);
         if constexpr (CBL) {
             if (crg >= 0) vg = block_dot<D, BITS, GPB, true>(ag, xr, fg.v, cbg, uint32_t(wg.K - 1));
-        } else {
-            if (crg >= 0) vg = block_dot_hyb<D, BITS, GPB>(ag, xr, fg.v, cbg_lds, cbg, klg, uint32_t(wg.K - 1));
-        }
-        co_fix_any<CO, BITS>(tr, blk, p.NB1, au);
-        if constexpr (CBL) {
             if (cru >= 0) vu = block_dot<D, BITS, GPB, true>(au, xr, fu.v, cbu, uint32_t(wu.K - 1));
         } else {
+            if (crg >= 0) vg = block_dot_hyb<D, BITS, GPB>(ag, xr, fg.v, cbg_lds, cbg, klg, uint32_t(wg.K - 1));
             if (cru >= 0) vu = block_dot_hyb<D, BITS, GPB>(au, xr, fu.v, cbu_lds, cbu, klu, uint32_t(wu.K - 1));
         }
         vg = group_sum(vg, lpr);
@@ -595,11 +514,11 @@ struct NoPre {
     __device__ void operator()(RouteLds &) const {}
 };
 
-template <int D, int BITS, int GPB, bool CO = false>
+template <int D, int BITS, int GPB>
 __global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ RouteLds rl;
-    up_body<D, BITS, GPB, CO>(p, int(blockIdx.x), int(blockIdx.y), smem, rl, NoPre{});
+    up_body<D, BITS, GPB>(p, int(blockIdx.x), int(blockIdx.y), smem, rl, NoPre{});
 }
 
 // K1 for tables beyond LDS: one projection per workgroup (blockIdx.z: 0 gate,
@@ -723,7 +642,7 @@ struct DownLane {
 
 // Expert, router weight and first-step weights of this lane's pair for row
 // tile `bx`; `eid(j)` / `wt(j)` give the routing (workspace or LDS).
-template <int BITS, int GPB, bool CO, typename EID, typename WT>
+template <int BITS, int GPB, typename EID, typename WT>
 __device__ __forceinline__ void down_prep(const MoeParams &p, int bx, int t, const DownLane &dl,
                                           EID eid, WT wt, DownState<BITS, GPB> &ds) {
     const int wave = threadIdx.x >> 6;
@@ -741,7 +660,7 @@ __device__ __forceinline__ void down_prep(const MoeParams &p, int bx, int t, con
     const int sidx = GPB == 1 ? dl.blk / p.bpg2 : dl.blk * GPB;
     const int r = bx * p.rows_per_wg2 + wave * dl.rpw + dl.sub;
     ds.cr = (ds.e >= 0 && r < p.H) ? moe_row(wd, ds.e, p.H, r) : -1;
-    moe_load_any<CO, BITS, GPB>(wd, ds.cr, dl.blk, p.NB2, sidx, p.ngrp2, ds.a, ds.s);
+    moe_load<BITS, GPB>(wd, ds.cr, dl.blk, sidx, p.ngrp2, ds.a, ds.s);
 }
 
 // Routed down table (all of it, or its first CBN entries) and, when the
@@ -779,7 +698,7 @@ __device__ __forceinline__ void h_first_load(const MoeParams &p, int t, HFirst &
 // the down projection of the workgroup's rows, scaled per pair by its router
 // weight and combined over the wave (the DPP row reduction is the sum). The
 // first kHFirst chunks per thread of fp16 rows come from `hf`.
-template <int D, int BITS, int GPB, bool W, bool CO>
+template <int D, int BITS, int GPB, bool W = false>
 __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint8_t *smem,
                                          const DownLane &dl, DownState<BITS, GPB> &ds,
                                          const HFirst &hf) {
@@ -850,14 +769,12 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
         const int r = row_at(st);
         return (ds.e >= 0 && r < p.H) ? moe_row(wd, ds.e, p.H, r) : -1;
     };
-    uint32_t *tr = reinterpret_cast<uint32_t *>(smem + p.tr2) + wave * BITS * kWave;
 
     for (int st = 0; st < p.steps2; ++st) {
         uint32_t n[BITS];
         uint32_t ns[GPB];
         const int64_t crn = st + 1 < p.steps2 ? code_row(st + 1) : -1;
-        moe_load_any<CO, BITS, GPB>(wd, crn, dl.blk, p.NB2, sidx, p.ngrp2, n, ns);
-        co_fix_any<CO, BITS>(tr, dl.blk, p.NB2, ds.a);
+        moe_load<BITS, GPB>(wd, crn, dl.blk, sidx, p.ngrp2, n, ns);
         float acc = 0.f;
         const ScalesF32<GPB> fs(ds.s);
         if constexpr (CBL) {
@@ -878,7 +795,7 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
     }
 }
 
-template <int D, int BITS, int GPB, bool W = false, bool CO = false>
+template <int D, int BITS, int GPB, bool W = false>
 __global__ void __launch_bounds__(moe_waves_down(W) * kWave) k_moe_down(const MoeParams p) {
     constexpr int CBN = down_cbn<D, BITS, W>();
     extern __shared__ __align__(16) uint8_t smem[];
@@ -900,10 +817,10 @@ __global__ void __launch_bounds__(moe_waves_down(W) * kWave) k_moe_down(const Mo
         wt = 0.f;
     }
     DownState<BITS, GPB> ds;
-    down_prep<BITS, GPB, CO>(p, int(blockIdx.x), t, dl, [&](int) { return id; },
-                             [&](int) { return wt; }, ds);
+    down_prep<BITS, GPB>(p, int(blockIdx.x), t, dl, [&](int) { return id; },
+                         [&](int) { return wt; }, ds);
     down_stage_cb<D, CBN, cb_in_lds(D, BITS), moe_waves_down(W) * kWave>(p, smem);
-    down_run<D, BITS, GPB, W, CO>(p, int(blockIdx.x), t, smem, dl, ds, hf);
+    down_run<D, BITS, GPB, W>(p, int(blockIdx.x), t, smem, dl, ds, hf);
 }
 
 // ------------------------------------------------ codebooks beyond LDS
@@ -1107,35 +1024,6 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     pl->wide2 = !full2 && gd.K * gd.D * 2 > kHybDownBytes && kHybDownWideBytes + xs2 <= lds_room;
     pl->smem1 = (pl->split ? size_t(pl->wide1 ? kHybSplitWideBytes : kHybSplitBytes) : 2 * cb1) + xs1;
     pl->smem2 = ((shared && full2) ? 2 : 1) * (pl->wide2 ? size_t(kHybDownWideBytes) : cb2) + xs2;
-    // Coalesced code reads where every projection of a phase has whole
-    // 16-byte chunks per block and 16-byte aligned codes; each wave then takes
-    // BITS x 256 bytes of LDS to regroup the words (when that still fits).
-    {
-        auto co_ok = [](const vqk_weights *w, const Geom &g) {
-            return g.BITS % 4 == 0 && (reinterpret_cast<uintptr_t>(w->codes) & 15) == 0;
-        };
-        bool c1 = !pl->split && co_ok(m->gate, gg) && co_ok(m->up, gu);
-        bool c2 = !pl->wide2 && co_ok(m->down, gd);
-        if (shared) {
-            Geom a, b, c;
-            make_geom(m->sh_gate, &a);
-            make_geom(m->sh_up, &b);
-            make_geom(m->sh_down, &c);
-            c1 = c1 && co_ok(m->sh_gate, a) && co_ok(m->sh_up, b);
-            c2 = c2 && co_ok(m->sh_down, c);
-        }
-        const size_t t1 = (pl->smem1 + 15) & ~size_t(15), t2 = (pl->smem2 + 15) & ~size_t(15);
-        const size_t e1 = size_t(moe_waves_up(pl->wide1)) * gg.BITS * 4 * kWave;
-        const size_t e2 = size_t(moe_waves_down(pl->wide2)) * gd.BITS * 4 * kWave;
-        c1 = c1 && t1 + e1 <= lds_room;
-        c2 = c2 && t2 + e2 <= lds_room;
-        p.co1 = c1;
-        p.co2 = c2;
-        p.tr1 = c1 ? int32_t(t1) : 0;
-        p.tr2 = c2 ? int32_t(t2) : 0;
-        if (c1) pl->smem1 = t1 + e1;
-        if (c2) pl->smem2 = t2 + e2;
-    }
     // Row steps per workgroup: about 2048 row steps per launch spread over the
     // grid; a workgroup whose LDS leaves room for no second one on a CU gets
     // enough steps that the grid fits the CUs in one round (each round would
@@ -1198,8 +1086,6 @@ int launch_moe_down(const MoeParams &p, int D, int bits, int gpb, dim3 grid, siz
 
 template <int D, int BITS, int GPB>
 static int go_up(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
-    if constexpr (BITS % 4 == 0)
-        if (p.co1) return launch_with_lds<k_moe_up<D, BITS, GPB, true>>(grid, dim3(kThreads), smem, st, p);
     return launch_with_lds<k_moe_up<D, BITS, GPB>>(grid, dim3(kThreads), smem, st, p);
 }
 template <int D, int BITS, int GPB, bool W>
@@ -1222,10 +1108,6 @@ static int launch_moe_up_split(const MoeParams &p, int d, int bits, int gpb, boo
 }
 template <int D, int BITS, int GPB, bool W = false>
 static int go_down(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
-    if constexpr (BITS % 4 == 0 && !W)
-        if (p.co2)
-            return launch_with_lds<k_moe_down<D, BITS, GPB, W, true>>(grid, dim3(moe_waves_down(W) * kWave),
-                                                                      smem, st, p);
     return launch_with_lds<k_moe_down<D, BITS, GPB, W>>(grid, dim3(moe_waves_down(W) * kWave), smem, st, p);
 }
 // Down kernel with the larger LDS part: the widths whose table is beyond LDS.
