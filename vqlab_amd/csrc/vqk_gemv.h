@@ -29,6 +29,7 @@
 // thread per row, walking its codes.
 #pragma once
 
+#include <mutex>
 #include "vqk_common.h"
 
 namespace vqk {
@@ -529,12 +530,18 @@ int launch_gemv_fast_d8(const GemvParams &p, int bits, int gpb, dim3 grid, size_
 // Launch helper: raises the dynamic-LDS cap once per kernel instance.
 template <auto KERN, typename P>
 int launch_with_lds(dim3 grid, dim3 block, size_t smem, hipStream_t st, const P &p) {
-    static bool raised = false;   // idempotent attribute update; a race only repeats it
-    if (smem > 64 * 1024 && !raised) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(KERN),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(smem));
-        if (e != hipSuccess) return hip_status(e, "hipFuncSetAttribute");
-        raised = true;
+    // the kernel's dynamic-LDS limit only ever rises, so a later launch asking
+    // for more than an earlier one is covered
+    static std::mutex mu;
+    static size_t raised_to = 64 * 1024;
+    if (smem > 64 * 1024) {
+        std::lock_guard<std::mutex> lk(mu);
+        if (smem > raised_to) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(KERN),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, int(smem));
+            if (e != hipSuccess) return hip_status(e, "hipFuncSetAttribute");
+            raised_to = smem;
+        }
     }
     hipLaunchKernelGGL(KERN, grid, block, smem, st, p);
     return hip_status(hipGetLastError(), "kernel launch");

@@ -6,10 +6,11 @@
 // tests/test_qwen3_5_parity.py:180-205 (+ sigmoid(shared_gate . x) * shared(x)).
 //
 //   k_moe_up    grid (row tiles of I, T * P), P = top_k + shared pairs per token.
-//               Every wave computes its token's routing from the logits (no
-//               extra launch, no host sync), loads its gate AND up blocks for
-//               the same rows, decodes both against LDS/L2 codebooks and
-//               writes h = silu(g) * u as fp16 into the workspace. Workgroup
+//               Wave 0 computes its token's routing from the logits (no
+//               extra launch, no host sync) while the other waves stage both
+//               codebooks and x; then waves 0-3 decode the tile's gate rows
+//               and waves 4-7 the same rows of up, and the workgroup writes
+//               h = silu(g) * u as fp16 into the workspace. Workgroup
 //               (0, pair 0) of each token also writes the routing.
 //   k_moe_down  grid (row tiles of H, T). Lanes are (pair j, block b) of one
 //               token, so a wave covers whole output rows across all the
@@ -387,20 +388,27 @@ struct DownState {
     float wj;
 };
 
-// K1 body: routing + gate/up + SwiGLU for pair `pair` of row tile `bx`. The
-// routing is left in `rl` (LDS), and `pre(rl)` runs right after it is
-// published and the first weight loads are out, before the decode.
-template <int D, int BITS, int GPB, typename PRE>
-__device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, uint8_t *smem,
-                                        RouteLds &rl, PRE pre) {
-    constexpr bool CBL = cb_in_lds(D, BITS);
+// K1: routing + gate/up + SwiGLU for pair blockIdx.y, row tile blockIdx.x, with
+// both tables in LDS. Eight waves: waves 0-3 decode the tile's gate rows,
+// waves 4-7 the same rows of up (one block per lane each), and the two halves
+// meet in LDS for silu(g) * u. With one projection per wave each lane decodes
+// 32 codes instead of 64 and two waves share a SIMD, so one decodes while the
+// other waits on its table reads (config 2: 12.35 -> 11.88 us per layer).
+template <int D, int BITS, int GPB>
+__global__ void __launch_bounds__(2 * kThreads) k_moe_up(const MoeParams p) {
     constexpr int CBN = up_cbn<D, BITS>();         // entries of each table in LDS
     constexpr int XH = kBlock * D, XS = XH + 8;
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ RouteLds rl;
     h2 *cbg_lds = reinterpret_cast<h2 *>(smem);
     h2 *cbu_lds = reinterpret_cast<h2 *>(smem + CBN * D * 2);
     f16 *xs = reinterpret_cast<f16 *>(smem + 2 * CBN * D * 2);
+    // the tile's gate values, then its up values (fp32), after x
+    float *vl = reinterpret_cast<float *>(smem + 2 * CBN * D * 2 + ((p.NB1 * XS * 2 + 15) & ~15));
 
+    const int bx = int(blockIdx.x), pair = int(blockIdx.y);
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int proj = wave >> 2, rw = wave & 3;     // projection (0 gate, 1 up), row wave
     const int lpr = 1 << p.lpr1_log2, rpw = kWave >> p.lpr1_log2;
     const int sub = lane >> p.lpr1_log2, blk = lane & (lpr - 1);
     const bool on = blk < p.NB1;
@@ -412,9 +420,9 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
 
     // Wave 0 loads the logits and routes, with no other load in flight (a
     // wave's loads complete in order, so anything queued ahead of the logits
-    // would delay the routing); waves 1-3 meanwhile stream the two codebooks
-    // and x into LDS. One barrier publishes the expert id, then all waves
-    // issue their weight loads (nothing else is outstanding, so the
+    // would delay the routing); waves 1-7 meanwhile stream the two codebooks
+    // and x into LDS. One barrier publishes the expert id, then every wave
+    // issues its weight loads (nothing else is outstanding, so the
     // barrier's wait never drains weight loads).
     int my_idx = -1;
     float my_w = 0.f;
@@ -423,12 +431,8 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
         route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &rl.rs, &e_pair, &my_idx, &my_w);
         if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
         if (lane == 0) rl.route = e_pair;
-        if (lane < p.top_k) {
-            rl.ids[lane] = my_idx;
-            rl.wts[lane] = my_w;
-        }
     } else {
-        constexpr int NT = kThreads - kWave;
+        constexpr int NT = 2 * kThreads - kWave;
         stage_codebook_fixed<D, CBN, NT, 1>(wg.codebook, wg.K, cbg_lds);
         stage_codebook_fixed<D, CBN, NT, 1>(wu.codebook, wu.K, cbu_lds);
         stage_x<XH, XS>(p.x, p.x_type, int64_t(t) * p.H, p.H, p.NB1, xs, kWave, NT);
@@ -454,71 +458,48 @@ __device__ __forceinline__ void up_body(const MoeParams &p, int bx, int pair, ui
     const int64_t e = is_shared ? 0 : ((e_pair >= 0 && e_pair < p.E) ? e_pair : -1);
     const int sidx = GPB == 1 ? blk / p.bpg1 : blk * GPB;
     const int r_wg = bx * p.rows_per_wg1;
-    auto row_at = [&](int st) { return r_wg + (st * 4 + wave) * rpw + sub; };
-
-    uint32_t ag[BITS], au[BITS];
-    uint32_t sg_[GPB], su_[GPB];
-    int64_t crg, cru;
+    auto row_at = [&](int st) { return r_wg + (st * 4 + rw) * rpw + sub; };
+    const MoeW &w = proj ? wu : wg;
+    // (this exact form measured 0.2 us per layer faster than the same
+    // steps written with a row lambda and a hoisted table bound)
+    uint32_t a[BITS];
+    uint32_t sc[GPB];
+    int64_t cr;
     {
         const int r = row_at(0);
-        const bool ok = on && e >= 0 && r < p.I;
-        crg = ok ? moe_row(wg, e, p.I, r) : -1;
-        cru = ok ? moe_row(wu, e, p.I, r) : -1;
-        moe_load<BITS, GPB>(wg, crg, blk, sidx, p.ngrp1, ag, sg_);
-        moe_load<BITS, GPB>(wu, cru, blk, sidx, p.ngrp1, au, su_);
+        cr = (on && e >= 0 && r < p.I) ? moe_row(w, e, p.I, r) : -1;
+        moe_load<BITS, GPB>(w, cr, blk, sidx, p.ngrp1, a, sc);
     }
-    pre(rl);
-
     h2 xr[16 * D];
     load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
-    const h2 *cbg = CBL ? cbg_lds : reinterpret_cast<const h2 *>(wg.codebook);
-    const h2 *cbu = CBL ? cbu_lds : reinterpret_cast<const h2 *>(wu.codebook);
-    const uint32_t klg = uint32_t(min(wg.K, CBN)), klu = uint32_t(min(wu.K, CBN));
-    uint16_t *hrow = p.h + (int64_t(t) * p.P + j) * p.I;
-
+    const h2 *cb = proj ? cbu_lds : cbg_lds;
     for (int st = 0; st < p.steps1; ++st) {
-        uint32_t ng[BITS], nu[BITS];
-        uint32_t nsg[GPB], nsu[GPB];
-        int64_t ncg = -1, ncu = -1;
+        uint32_t n[BITS];
+        uint32_t ns[GPB];
+        int64_t cn = -1;
         if (st + 1 < p.steps1) {
             const int r = row_at(st + 1);
-            const bool ok = on && e >= 0 && r < p.I;
-            ncg = ok ? moe_row(wg, e, p.I, r) : -1;
-            ncu = ok ? moe_row(wu, e, p.I, r) : -1;
+            cn = (on && e >= 0 && r < p.I) ? moe_row(w, e, p.I, r) : -1;
         }
-        moe_load<BITS, GPB>(wg, ncg, blk, sidx, p.ngrp1, ng, nsg);
-        moe_load<BITS, GPB>(wu, ncu, blk, sidx, p.ngrp1, nu, nsu);
-        float vg = 0.f, vu = 0.f;
-        const ScalesF32<GPB> fg(sg_), fu(su_);
-        if constexpr (CBL) {
-            if (crg >= 0) vg = block_dot<D, BITS, GPB, true>(ag, xr, fg.v, cbg, uint32_t(wg.K - 1));
-            if (cru >= 0) vu = block_dot<D, BITS, GPB, true>(au, xr, fu.v, cbu, uint32_t(wu.K - 1));
-        } else {
-            if (crg >= 0) vg = block_dot_hyb<D, BITS, GPB>(ag, xr, fg.v, cbg_lds, cbg, klg, uint32_t(wg.K - 1));
-            if (cru >= 0) vu = block_dot_hyb<D, BITS, GPB>(au, xr, fu.v, cbu_lds, cbu, klu, uint32_t(wu.K - 1));
-        }
-        vg = group_sum(vg, lpr);
-        vu = group_sum(vu, lpr);
+        moe_load<BITS, GPB>(w, cn, blk, sidx, p.ngrp1, n, ns);
+        float v = 0.f;
+        const ScalesF32<GPB> fs(sc);
+        if (cr >= 0) v = block_dot<D, BITS, GPB, true>(a, xr, fs.v, cb, uint32_t(w.K - 1));
+        v = group_sum(v, lpr);
         const int r = row_at(st);
-        if (blk == lpr - 1 && r < p.I) hrow[r] = f32_to_h(silu(vg) * vu);
-        crg = ncg;
-        cru = ncu;
+        if (blk == lpr - 1 && r < p.I) vl[proj * p.rows_per_wg1 + (r - r_wg)] = v;
+        cr = cn;
 #pragma unroll
-        for (int i = 0; i < BITS; ++i) { ag[i] = ng[i]; au[i] = nu[i]; }
+        for (int i = 0; i < BITS; ++i) a[i] = n[i];
 #pragma unroll
-        for (int g = 0; g < GPB; ++g) { sg_[g] = nsg[g]; su_[g] = nsu[g]; }
+        for (int g = 0; g < GPB; ++g) sc[g] = ns[g];
     }
-}
-
-struct NoPre {
-    __device__ void operator()(RouteLds &) const {}
-};
-
-template <int D, int BITS, int GPB>
-__global__ void __launch_bounds__(kThreads) k_moe_up(const MoeParams p) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ RouteLds rl;
-    up_body<D, BITS, GPB>(p, int(blockIdx.x), int(blockIdx.y), smem, rl, NoPre{});
+    __syncthreads();
+    uint16_t *hrow = p.h + (int64_t(t) * p.P + j) * p.I;
+    for (int i = tid; i < p.rows_per_wg1; i += 2 * kThreads) {
+        const int r = r_wg + i;
+        if (r < p.I) hrow[r] = f32_to_h(silu(vl[i]) * vl[p.rows_per_wg1 + i]);
+    }
 }
 
 // K1 for tables beyond LDS: one projection per workgroup (blockIdx.z: 0 gate,
@@ -1043,6 +1024,11 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
         const int nz = pl->split ? 2 : 1;
         const int nw = moe_waves_up(pl->wide1);
         plan_steps((gg.OUT + rpw - 1) / rpw, T * P * nz, pl->smem1, nw, &p.steps1);
+        if (!pl->split) {
+            // the tile's gate and up values meet in LDS after x (8 B per row)
+            while (p.steps1 > 1 && pl->smem1 + 16 + 8 * size_t(nw * rpw * p.steps1) > lds_room) --p.steps1;
+            pl->smem1 += 16 + 8 * size_t(nw * rpw * p.steps1);
+        }
         p.rows_per_wg1 = int32_t(nw * rpw * p.steps1);
         pl->grid1 = dim3(unsigned((gg.OUT + p.rows_per_wg1 - 1) / p.rows_per_wg1), unsigned(T * P),
                          unsigned(nz));
@@ -1086,7 +1072,7 @@ int launch_moe_down(const MoeParams &p, int D, int bits, int gpb, dim3 grid, siz
 
 template <int D, int BITS, int GPB>
 static int go_up(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
-    return launch_with_lds<k_moe_up<D, BITS, GPB>>(grid, dim3(kThreads), smem, st, p);
+    return launch_with_lds<k_moe_up<D, BITS, GPB>>(grid, dim3(2 * kThreads), smem, st, p);
 }
 template <int D, int BITS, int GPB, bool W>
 static int go_up_split(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
