@@ -675,6 +675,55 @@ __device__ __forceinline__ void h_first_load(const MoeParams &p, int t, HFirst &
     }
 }
 
+// The token's P SwiGLU rows (fp16) -> LDS at the padded block stride; the
+// first kHFirst chunks per thread of fp16 rows come from `hf`. With fp32
+// gate / up rows (split phase) they are built as fp16(silu(g) * u) here.
+template <int D>
+__device__ __forceinline__ void down_stage_h(const MoeParams &p, int t, f16 *xs, const HFirst &hf) {
+    constexpr int XH = kBlock * D, XS = XH + 8;
+    const int tid = threadIdx.x;
+    const uint16_t *hsrc = p.h + int64_t(t) * p.P * p.I;
+    const int64_t f0 = int64_t(t) * p.P * p.I;   // split phase: fp32 g / u rows
+    const int gpr = p.I / 8;                     // 8-value groups per row
+    const int ng = p.P * gpr;
+    constexpr int U = 8;
+    int gs = tid;
+    if (!p.gbuf) {
+#pragma unroll
+        for (int u = 0; u < kHFirst; ++u) {
+            const int g = tid + u * int(blockDim.x);
+            if (g < ng) {
+                const int jj = g / gpr, col = (g % gpr) * 8;
+                const int b = jj * p.NB2 + col / XH;
+                *reinterpret_cast<u32x4 *>(xs + b * XS + col % XH) = hf.v[u];
+            }
+        }
+        gs = tid + kHFirst * int(blockDim.x);
+    }
+    for (int g0 = gs; g0 < ng; g0 += U * blockDim.x) {
+        u32x4 hv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int g = g0 + u * blockDim.x;
+            if (p.gbuf)
+                hv[u] = g < ng ? swiglu8(p.gbuf + f0 + int64_t(g) * 8, p.ubuf + f0 + int64_t(g) * 8)
+                               : u32x4{0, 0, 0, 0};
+            else
+                hv[u] = g < ng ? *reinterpret_cast<const u32x4 *>(hsrc + int64_t(g) * 8)
+                               : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int g = g0 + u * blockDim.x;
+            if (g < ng) {
+                const int jj = g / gpr, col = (g % gpr) * 8;
+                const int b = jj * p.NB2 + col / XH;
+                *reinterpret_cast<u32x4 *>(xs + b * XS + col % XH) = hv[u];
+            }
+        }
+    }
+}
+
 // The token's P SwiGLU rows (fp16) -> LDS at the padded block stride, then
 // the down projection of the workgroup's rows, scaled per pair by its router
 // weight and combined over the wave (the DPP row reduction is the sum). The
@@ -691,48 +740,7 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
     f16 *xs = reinterpret_cast<f16 *>(smem + ((CBL && p.shared) ? 2 : 1) * CBN * D * 2);
     const int tid = threadIdx.x, wave = tid >> 6;
     const MoeW &wd = dl.is_shared ? p.sdown : p.down;
-    {
-        const uint16_t *hsrc = p.h + int64_t(t) * p.P * p.I;
-        const int64_t f0 = int64_t(t) * p.P * p.I;   // split phase: fp32 g / u rows
-        const int gpr = p.I / 8;                     // 8-value groups per row
-        const int ng = p.P * gpr;
-        constexpr int U = 8;
-        int gs = tid;
-        if (!p.gbuf) {
-#pragma unroll
-            for (int u = 0; u < kHFirst; ++u) {
-                const int g = tid + u * int(blockDim.x);
-                if (g < ng) {
-                    const int jj = g / gpr, col = (g % gpr) * 8;
-                    const int b = jj * p.NB2 + col / XH;
-                    *reinterpret_cast<u32x4 *>(xs + b * XS + col % XH) = hf.v[u];
-                }
-            }
-            gs = tid + kHFirst * int(blockDim.x);
-        }
-        for (int g0 = gs; g0 < ng; g0 += U * blockDim.x) {
-            u32x4 hv[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int g = g0 + u * blockDim.x;
-                if (p.gbuf)
-                    hv[u] = g < ng ? swiglu8(p.gbuf + f0 + int64_t(g) * 8, p.ubuf + f0 + int64_t(g) * 8)
-                                   : u32x4{0, 0, 0, 0};
-                else
-                    hv[u] = g < ng ? *reinterpret_cast<const u32x4 *>(hsrc + int64_t(g) * 8)
-                                   : u32x4{0, 0, 0, 0};
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int g = g0 + u * blockDim.x;
-                if (g < ng) {
-                    const int jj = g / gpr, col = (g % gpr) * 8;
-                    const int b = jj * p.NB2 + col / XH;
-                    *reinterpret_cast<u32x4 *>(xs + b * XS + col % XH) = hv[u];
-                }
-            }
-        }
-    }
+    down_stage_h<D>(p, t, xs, hf);
     wait_vmem();
     __syncthreads();
 
