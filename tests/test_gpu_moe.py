@@ -69,6 +69,17 @@ def test_moe_layer_c2_shape():
     _check(blk, projs, sh, shv, rng, 1, 256, 2048, 8)
 
 
+@pytest.mark.parametrize("T", [1, 2])
+def test_moe_layer_multi_step_tiles(T):
+    """H 4096, I 1024, top-7 + a shared expert, d4 K4096: each gate/up
+    workgroup walks several row steps (2 at T=1, 4 at T=2) and its gate and up
+    values meet in LDS for every one of them."""
+    print(f"moe multi-step T={T}", flush=True)
+    rng = np.random.default_rng(40 + T)
+    blk, projs, sh, shv = _block(rng, 16, 4096, 1024, 4, 4096, 7, shared=True)
+    _check(blk, projs, sh, shv, rng, T, 16, 4096, 7)
+
+
 @pytest.mark.parametrize("T", [1, 4])
 def test_moe_layer_c3_shape_shared(T):
     """Qwen3.5-397B-A17B row shapes: H 4096, I 1024, d8 K16384 14-bit,
