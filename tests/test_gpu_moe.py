@@ -80,6 +80,16 @@ def test_moe_layer_multi_step_tiles(T):
     _check(blk, projs, sh, shv, rng, T, 16, 4096, 7)
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_layer_d8_table_in_lds(T):
+    """d8 K4096 (12-bit, a 64 KB table per projection): the gate/up kernel
+    reads x from LDS per code at this width."""
+    print(f"moe d8 K4096 T={T}", flush=True)
+    rng = np.random.default_rng(50 + T)
+    blk, projs, sh, shv = _block(rng, 32, 1024, 512, 8, 4096, 4, shared=True)
+    _check(blk, projs, sh, shv, rng, T, 32, 1024, 4)
+
+
 @pytest.mark.parametrize("T", [1, 4])
 def test_moe_layer_c3_shape_shared(T):
     """Qwen3.5-397B-A17B row shapes: H 4096, I 1024, d8 K16384 14-bit,

@@ -159,6 +159,34 @@ __device__ __forceinline__ float block_dot_hyb(const uint32_t (&w)[BITS], const 
     return acc;
 }
 
+// block_dot with the table in LDS and the block's 32·D activations read from
+// LDS (`xl`) per code instead of held in 16·D registers (d8: 128 registers a
+// wave of an 8-wave workgroup cannot spare).
+template <int D, int BITS, int GPB>
+__device__ __forceinline__ float block_dot_lx(const uint32_t (&w)[BITS], const f16 *xl,
+                                              const float (&s)[GPB], const h2 *cb) {
+    typedef typename EntryT<D>::type E;
+    constexpr int CPG = kBlock / GPB;
+    const E *xv = reinterpret_cast<const E *>(__builtin_assume_aligned(xl, 16));
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < GPB; ++g) {
+        float ga = 0.f;
+#pragma unroll
+        for (int q = 0; q < CPG; ++q) {
+            const int i = g * CPG + q;
+            const E e = reinterpret_cast<const E *>(cb)[block_field<BITS>(w, i)];
+            const E x = xv[i];
+            h2 xh[D / 2];
+#pragma unroll
+            for (int k = 0; k < D / 2; ++k) xh[k] = h2{x[2 * k], x[2 * k + 1]};
+            ga = dot_vec<D>(e, xh, ga);
+        }
+        acc = fmaf(s[g], ga, acc);
+    }
+    return acc;
+}
+
 // block_dot_hyb with the block's 32·D activations read from LDS (`xl`) per
 // code instead of held in 16·D registers: the registers that frees let two
 // waves share a SIMD, each hiding the other's table-read latency.

@@ -470,8 +470,12 @@ __global__ void __launch_bounds__(2 * kThreads) k_moe_up(const MoeParams p) {
         cr = (on && e >= 0 && r < p.I) ? moe_row(w, e, p.I, r) : -1;
         moe_load<BITS, GPB>(w, cr, blk, sidx, p.ngrp1, a, sc);
     }
-    h2 xr[16 * D];
-    load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
+    // d8 reads x from LDS per code: its 128 x registers do not fit beside the
+    // rest at two waves per SIMD
+    constexpr bool XL = D == 8;
+    const f16 *xl = xs + (on ? blk : 0) * XS;
+    h2 xr[XL ? 1 : 16 * D];
+    if constexpr (!XL) load_xregs<D>(xl, xr);
     const h2 *cb = proj ? cbu_lds : cbg_lds;
     for (int st = 0; st < p.steps1; ++st) {
         uint32_t n[BITS];
@@ -484,7 +488,11 @@ __global__ void __launch_bounds__(2 * kThreads) k_moe_up(const MoeParams p) {
         moe_load<BITS, GPB>(w, cn, blk, sidx, p.ngrp1, n, ns);
         float v = 0.f;
         const ScalesF32<GPB> fs(sc);
-        if (cr >= 0) v = block_dot<D, BITS, GPB, true>(a, xr, fs.v, cb, uint32_t(w.K - 1));
+        if constexpr (XL) {
+            if (cr >= 0) v = block_dot_lx<D, BITS, GPB>(a, xl, fs.v, cb);
+        } else {
+            if (cr >= 0) v = block_dot<D, BITS, GPB, true>(a, xr, fs.v, cb, uint32_t(w.K - 1));
+        }
         v = group_sum(v, lpr);
         const int r = row_at(st);
         if (blk == lpr - 1 && r < p.I) vl[proj * p.rows_per_wg1 + (r - r_wg)] = v;
