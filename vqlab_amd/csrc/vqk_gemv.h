@@ -555,7 +555,7 @@ int launch_gemv_fast_d2(const GemvParams &p, int bits, int gpb, dim3 grid, size_
 int launch_gemv_fast_d4(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
 int launch_gemv_fast_d8(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
 
-// Launch helper: raises the dynamic-LDS cap once per kernel instance.
+// Launch helper: raises each kernel instance's dynamic-LDS cap as its launches need more.
 template <auto KERN, typename P>
 int launch_with_lds(dim3 grid, dim3 block, size_t smem, hipStream_t st, const P &p) {
     // the kernel's dynamic-LDS limit only ever rises, so a later launch asking

@@ -134,9 +134,10 @@ __device__ __forceinline__ void dq_entry(const uint16_t *cb, uint32_t c, uint16_
 // One thread per code column j, kDqRows output rows at a time (rows
 // blockIdx.y + i * gridDim.y of the stride): each phase -- code rows, codes,
 // scales, table entries, stores -- is issued for all of them before the next
-// waits, so a thread has kDqRows memory chains in flight instead of one
-// (the kernel is bound by the latency of its code-load -> gather chain).
-// Threads past the last code of a row zero its padding up to out_ld.
+// waits, so a thread has kDqRows code-load -> gather chains in flight instead
+// of one (small weights are latency-bound; a large table with random codes is
+// bound by the L2's random-read rate instead). Threads past the last code of
+// a row zero its padding up to out_ld.
 constexpr int kDqRows = 4;
 template <int D>
 __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
