@@ -159,6 +159,31 @@ __device__ __forceinline__ float block_dot_hyb(const uint32_t (&w)[BITS], const 
     return acc;
 }
 
+// block_dot with the table in LDS and all 32 entry reads issued before the
+// first product: at one wave per SIMD nothing else hides their latency.
+template <int D, int BITS, int GPB>
+__device__ __forceinline__ float block_dot_all(const uint32_t (&w)[BITS], const h2 (&xr)[16 * D],
+                                               const float (&s)[GPB], const h2 *cb) {
+    typedef typename EntryT<D>::type E;
+    constexpr int CPG = kBlock / GPB;
+    E e[kBlock];
+#pragma unroll
+    for (int i = 0; i < kBlock; ++i) e[i] = reinterpret_cast<const E *>(cb)[block_field<BITS>(w, i)];
+    __builtin_amdgcn_sched_barrier(0);
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < GPB; ++g) {
+        float ga = 0.f;
+#pragma unroll
+        for (int q = 0; q < CPG; ++q) {
+            const int i = g * CPG + q;
+            ga = dot_vec<D>(e[i], &xr[i * (D / 2)], ga);
+        }
+        acc = fmaf(s[g], ga, acc);
+    }
+    return acc;
+}
+
 // block_dot with the table in LDS and the block's 32·D activations read from
 // LDS (`xl`) per code instead of held in 16·D registers (d8: 128 registers a
 // wave of an 8-wave workgroup cannot spare).
