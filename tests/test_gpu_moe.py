@@ -90,6 +90,31 @@ def test_moe_layer_d8_table_in_lds(T):
     _check(blk, projs, sh, shv, rng, T, 32, 1024, 4)
 
 
+# (E, H, I, D, K, k, shared, norm, T): widths 2..14 bits, tables in and beyond
+# LDS, ragged row counts against the workgroup tiles, 1-3 tokens
+_GEOMS = [
+    (24, 128, 192, 2, 256, 3, False, True, 1),
+    (24, 640, 320, 2, 1024, 4, True, False, 2),
+    (32, 768, 384, 4, 512, 5, False, True, 3),
+    (16, 1536, 384, 4, 4096, 6, True, True, 1),
+    (40, 1024, 640, 4, 2048, 2, False, False, 2),
+    (16, 512, 256, 8, 256, 3, True, True, 2),
+    (20, 1024, 512, 8, 4096, 4, False, True, 1),
+    (12, 1024, 256, 8, 16384, 2, True, False, 1),
+    (12, 512, 128, 4, 16384, 3, False, True, 3),
+]
+
+
+@pytest.mark.parametrize("geom", _GEOMS, ids=[f"d{g[3]}K{g[4]}E{g[0]}T{g[8]}" for g in _GEOMS])
+def test_moe_layer_geometries(geom):
+    """The fused layer over assorted geometries against the oracle."""
+    E, H, I, D, K, k, shared, norm, T = geom
+    print(f"moe geometry {geom}", flush=True)
+    rng = np.random.default_rng(sum(geom[:6]))
+    blk, projs, sh, shv = _block(rng, E, H, I, D, K, k, shared=shared, norm=norm)
+    _check(blk, projs, sh, shv, rng, T, E, H, k, norm=norm)
+
+
 @pytest.mark.parametrize("T", [1, 4])
 def test_moe_layer_c3_shape_shared(T):
     """Qwen3.5-397B-A17B row shapes: H 4096, I 1024, d8 K16384 14-bit,
