@@ -176,11 +176,12 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
 
 // Order-preserving map float -> uint32 (NaN maps below every number, -0 to
 // the key of +0, as they compare equal) and back.
+// Written as selects (no branches: a routing wave maps its logits with it).
 __device__ __forceinline__ uint32_t f32_key(float f) {
-    uint32_t b = __float_as_uint(f);
-    if ((b & 0x7fffffffu) > 0x7f800000u) return 0u;          // NaN: never selected
-    if (b == 0x80000000u) b = 0u;
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    const uint32_t b0 = __float_as_uint(f);
+    const uint32_t b = b0 == 0x80000000u ? 0u : b0;
+    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (b0 & 0x7fffffffu) > 0x7f800000u ? 0u : k;      // NaN: never selected
 }
 __device__ __forceinline__ float key_f32(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);

@@ -104,147 +104,190 @@ struct RouteScratch {
     uint32_t sel_key[kFastTopK];
 };
 
-// Threshold-and-rank top-k (k <= 16) of a wave whose lanes hold NS keys each,
-// sorted descending. The lanes form G >= k groups (8 lanes for k <= 8, else
-// 4); the smallest group maximum tau is at most the k-th largest key (the G
-// group maxima are G distinct keys >= tau), so every selection is among the
-// keys >= tau -- about 20 of 256 for random logits. Those candidates are
-// compacted into LDS as (key << 32 | ~index), which orders them exactly as
-// the selection does (larger key first, lower index on ties), and each takes
-// its rank by counting the candidates above it; ranks below k are the
-// selections, written in order. Returns false (nothing written) when tau is
-// the key of a NaN or padding slot, or more than 64 keys are >= tau; the
-// caller then takes the sequential selection.
+// Routing of one token by one wave, in two halves: route_pick finds the
+// selections (the expert of the workgroup's own pair first of all),
+// route_weights turns them into router weights (softmax over all experts, or
+// renormalised over the selections). Lanes hold NS logits each (lane l:
+// experts s * 64 + l).
+struct RoutePick {
+    int e_want;          // expert of pair `want` (wave-uniform), -1 if none
+    int midx;            // sequential path: lane r < k holds selection r
+    uint32_t mykey;
+    bool ranked;         // selections in RouteScratch::sel_idx / sel_key
+};
+
+// Threshold-and-rank selection (k <= 16). The lanes form G >= k groups (8
+// lanes for k <= 8, else 4); the smallest group maximum tau is at most the
+// k-th largest key (the G group maxima are G distinct keys >= tau), so every
+// selection is among the keys >= tau -- about 20 of 256 for random logits.
+// Those candidates are compacted into LDS as (key << 32 | ~index), which
+// orders them exactly as the selection does (larger key first, lower index on
+// ties), and each takes its rank by counting the candidates above it; ranks
+// below k are the selections, written in order, and the pair's own expert
+// comes straight from the lane that holds rank `want` (no LDS round trip).
+// Returns false when tau is the key of a NaN or padding slot, or more than 64
+// keys are >= tau; the caller then takes the sequential selection.
 template <int NS>
-__device__ __forceinline__ bool topk_rank(const uint32_t (&key)[NS], const uint32_t (&idx)[NS], int k,
-                                          RouteScratch *rs) {
+__device__ __forceinline__ bool topk_rank(const uint32_t (&key)[NS], int k, int want, RouteScratch *rs,
+                                          int *e_want) {
     const int lane = threadIdx.x & (kWave - 1);
     uint32_t gm = key[0];
+#pragma unroll
+    for (int s = 1; s < NS; ++s) gm = max(gm, key[s]);
     gm = max(gm, dpp_u<kDppQuadXor1>(gm));
     gm = max(gm, dpp_u<kDppQuadXor2>(gm));
     if (k <= 8) gm = max(gm, dpp_u<kDppRowHalfMirror>(gm));
     const uint32_t tau = wave_min_u32(gm);
     if (tau == 0u) return false;
+    uint64_t bal[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) bal[s] = __ballot(key[s] >= tau);
     int c = 0;                                          // candidates so far (wave-uniform)
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-        const bool in = key[s] >= tau;
-        const uint64_t b = __ballot(in);
-        const int below = int(__builtin_amdgcn_mbcnt_hi(uint32_t(b >> 32),
-                                                         __builtin_amdgcn_mbcnt_lo(uint32_t(b), 0u)));
-        if (in && c + below < kWave)
-            rs->cand[c + below] = (uint64_t(key[s]) << 32) | uint64_t(~idx[s]);
-        c += __popcll(b);
+        const int pos = c + int(__builtin_amdgcn_mbcnt_hi(uint32_t(bal[s] >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo(uint32_t(bal[s]), 0u)));
+        if (key[s] >= tau && pos < kWave)
+            rs->cand[pos] = (uint64_t(key[s]) << 32) | uint64_t(~uint32_t(s * kWave + lane));
+        c += __popcll(bal[s]);
     }
     if (c > kWave) return false;
-    // zero the slots up to the next multiple of 8 so the rank loop reads whole groups
-    if (lane >= c && lane < ((c + 7) & ~7)) rs->cand[lane] = 0;
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    const uint64_t mine = lane < c ? rs->cand[lane] : 0;
+    // slots past c hold 0 (route_pick clears them before the candidates land)
+    const uint64_t mine = rs->cand[lane];
     int rank = 0;
-    for (int j0 = 0; j0 < c; j0 += 8) {
+    {
+        uint64_t v[16];                                 // the first 16 in one round trip
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = rs->cand[u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) rank += v[u] > mine ? 1 : 0;
+    }
+    for (int j0 = 16; j0 < c; j0 += 8) {
         uint64_t v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) v[u] = rs->cand[j0 + u];
 #pragma unroll
         for (int u = 0; u < 8; ++u) rank += v[u] > mine ? 1 : 0;
     }
-    if (lane < c && rank < k) {
+    const bool sel = lane < c && rank < k;
+    if (sel) {
         rs->sel_idx[rank] = ~uint32_t(mine);
         rs->sel_key[rank] = uint32_t(mine >> 32);
     }
+    int e_w = -1;
+    if (want >= 0 && want < k) {
+        const uint64_t b = __ballot(sel && rank == want);
+        if (b) e_w = __builtin_amdgcn_readlane(int(~uint32_t(mine)), __ffsll((unsigned long long)b) - 1);
+    }
+    *e_want = e_w;
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
     return true;
 }
 
-// Wave-level softmax + top-k of one token's logits (fp32, like the
-// reference's precise softmax), NS logits per lane (NS * 64 >= E). Every lane
-// returns the expert of pair `want` (or -1) in *e_want; lane r < k holds
-// selection r in (*my_idx, *my_w). Argmax is exact: logits become
-// order-preserving integer keys and each lane sorts its own keys once. The
+// Selections of one token's logits (fp32). Argmax is exact: logits become
+// order-preserving integer keys (key[], kept for route_weights). The
 // selections come from topk_rank, or (k > 16, NaN-heavy or degenerate
-// logits) from k sequential selections, each a DPP max over the lanes' head
-// keys; the lane holding it (on a tie between lanes, the one whose head has
-// the lowest index) pops its head. Either way ties go to the lower expert id
-// (stable descending order); NaN logits sort below -inf and are never chosen
-// while k <= number of finite logits.
+// logits) from k sequential selections over each lane's keys sorted once,
+// each a DPP max over the lanes' head keys; the lane holding it (on a tie
+// between lanes, the one whose head has the lowest index) pops its head.
+// Either way ties go to the lower expert id (stable descending order); NaN
+// logits sort below -inf and are never chosen while k <= number of finite
+// logits. The loads take clamped indices and no branch.
 template <int NS>
-__device__ __forceinline__ void route_wave(const float *lg, int E, int k, int norm, int want,
-                                           RouteScratch *rs, int *e_want, int *my_idx, float *my_w) {
+__device__ __forceinline__ void route_pick(const float *lg, int E, int k, int want, RouteScratch *rs,
+                                           uint32_t (&key)[NS], RoutePick &rp) {
     const int lane = threadIdx.x & (kWave - 1);
-    uint32_t key[NS], idx[NS];
     float raw[NS];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        const int i = s * kWave + lane;
-        raw[s] = i < E ? lg[i] : 0.f;
-    }
-    wait_vmem();                                         // the logits are this wave's only loads
+    for (int s = 0; s < NS; ++s) raw[s] = lg[min(s * kWave + lane, E - 1)];
+    rs->cand[lane] = 0;                                 // LDS writes of a wave land in order
+    wait_vmem();                                        // the logits are this wave's only loads
+#pragma unroll
+    for (int s = 0; s < NS; ++s) key[s] = s * kWave + lane < E ? f32_key(raw[s]) : 0u;
+    rp.midx = -1;
+    rp.mykey = 0u;
+    rp.ranked = k <= kFastTopK && topk_rank<NS>(key, k, want, rs, &rp.e_want);
+    if (rp.ranked) return;
+    // sequential selections over a sorted copy; lane r keeps selection r
+    uint32_t sk[NS], si[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-        const int i = s * kWave + lane;
-        key[s] = i < E ? f32_key(raw[s]) : 0u;
-        idx[s] = uint32_t(i);
+        sk[s] = key[s];
+        si[s] = uint32_t(s * kWave + lane);
     }
-    sort_keys_desc<NS>(key, idx);
-    const float m = key_f32(wave_max_u32(key[0]));
-    float den = 1.f;
-    if (!norm) {                                         // renormalised weights do not need it
-        float lsum = 0.f;
-#pragma unroll
-        for (int s = 0; s < NS; ++s)
-            if (key[s]) lsum += __expf(key_f32(key[s]) - m);
-        den = wave_sum(lsum);
-    }
-    int e_w = -1, midx = -1;
-    uint32_t mykey = 0;
-    const bool ranked = k <= kFastTopK && topk_rank<NS>(key, idx, k, rs);
-    if (ranked) {
-        if (want >= 0 && want < k) e_w = int(rs->sel_idx[want]);
-        if (lane < k) {
-            midx = int(rs->sel_idx[lane]);
-            mykey = rs->sel_key[lane];
-        }
-    }
-    // otherwise k sequential selections; lane r keeps selection r
-    for (int r = 0; r < (ranked ? 0 : k); ++r) {
-        const uint32_t best = wave_max_u32(key[0]);
+    sort_keys_desc<NS>(sk, si);
+    int e_w = -1;
+    for (int r = 0; r < k; ++r) {
+        const uint32_t best = wave_max_u32(sk[0]);
         int bi = -1;
         if (best) {
-            const uint64_t hit = __ballot(key[0] == best);
+            const uint64_t hit = __ballot(sk[0] == best);
             int wl;
             if ((hit & (hit - 1)) == 0) {
                 wl = __ffsll((unsigned long long)hit) - 1;
             } else {                                     // tie between lanes: lowest index
-                const uint32_t mi = wave_min_u32(key[0] == best ? idx[0] : 0xffffffffu);
+                const uint32_t mi = wave_min_u32(sk[0] == best ? si[0] : 0xffffffffu);
                 wl = int(mi & (kWave - 1));
             }
-            bi = __builtin_amdgcn_readlane(int(idx[0]), wl);
+            bi = __builtin_amdgcn_readlane(int(si[0]), wl);
             if (lane == wl) {
 #pragma unroll
                 for (int s = 0; s + 1 < NS; ++s) {
-                    key[s] = key[s + 1];
-                    idx[s] = idx[s + 1];
+                    sk[s] = sk[s + 1];
+                    si[s] = si[s + 1];
                 }
-                key[NS - 1] = 0u;
+                sk[NS - 1] = 0u;
             }
         }
         if (r == want) e_w = bi;
-        if (lane == r) { midx = bi; mykey = bi >= 0 ? best : 0u; }
+        if (lane == r) { rp.midx = bi; rp.mykey = bi >= 0 ? best : 0u; }
     }
+    rp.e_want = e_w;
+}
+
+// Router weights of the selections (fp32, like the reference's precise
+// softmax): lane r < k gets selection r in (*my_idx, *my_w). The largest
+// logit, the softmax's shift, is the first selection's.
+template <int NS>
+__device__ __forceinline__ void route_weights(const uint32_t (&key)[NS], int k, int norm, RouteScratch *rs,
+                                              const RoutePick &rp, int *my_idx, float *my_w) {
+    const int lane = threadIdx.x & (kWave - 1);
+    int midx = rp.midx;
+    uint32_t mykey = rp.mykey;
+    if (rp.ranked && lane < k) {
+        midx = int(rs->sel_idx[lane]);
+        mykey = rs->sel_key[lane];
+    }
+    const float m = key_f32(uint32_t(__builtin_amdgcn_readlane(int(mykey), 0)));
     const float pr = (lane < k && mykey) ? __expf(key_f32(mykey) - m) : 0.f;
-    float w = pr;
+    float w;
     if (norm) {
         const float psel = wave_sum(pr);
         w = psel > 0.f ? pr * (1.f / psel) : 0.f;
     } else {
-        w = pr * (1.f / den);
+        float lsum = 0.f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+            if (key[s]) lsum += __expf(key_f32(key[s]) - m);
+        w = pr * (1.f / wave_sum(lsum));
     }
-    *e_want = e_w;
-    *my_idx = midx;
+    *my_idx = lane < k ? midx : -1;
     *my_w = w;
+}
+
+// Both halves: every lane returns the expert of pair `want` (or -1) in
+// *e_want; lane r < k holds selection r in (*my_idx, *my_w).
+template <int NS>
+__device__ __forceinline__ void route_wave(const float *lg, int E, int k, int norm, int want,
+                                           RouteScratch *rs, int *e_want, int *my_idx, float *my_w) {
+    uint32_t key[NS];
+    RoutePick rp;
+    route_pick<NS>(lg, E, k, want, rs, key, rp);
+    route_weights<NS>(key, k, norm, rs, rp, my_idx, my_w);
+    *e_want = rp.e_want;
 }
 
 __device__ __forceinline__ void route(const float *lg, int E, int k, int norm, int want,
@@ -418,18 +461,19 @@ __global__ void __launch_bounds__(2 * kThreads) k_moe_up(const MoeParams p) {
     const MoeW &wu = is_shared ? p.sup : p.up;
     const float *lg = p.logits + int64_t(t) * p.E;
 
-    // Wave 0 loads the logits and routes, with no other load in flight (a
-    // wave's loads complete in order, so anything queued ahead of the logits
-    // would delay the routing); waves 1-7 meanwhile stream the two codebooks
-    // and x into LDS. One barrier publishes the expert id, then every wave
-    // issues its weight loads (nothing else is outstanding, so the
-    // barrier's wait never drains weight loads).
+    // Wave 0 loads the logits and picks the experts, with no other load in
+    // flight (a wave's loads complete in order, so anything queued ahead of
+    // the logits would delay the routing); waves 1-7 meanwhile stream the two
+    // codebooks and x into LDS. One barrier publishes the expert id, then
+    // every wave issues its weight loads (nothing else is outstanding, so the
+    // barrier's wait never drains weight loads). (Computing the router
+    // weights later, while the weights are in flight, measured slower: the
+    // barrier also waits for the table copies, about as long as the routing.)
     int my_idx = -1;
     float my_w = 0.f;
     if (wave == 0) {
         int e_pair;
         route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &rl.rs, &e_pair, &my_idx, &my_w);
-        if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
         if (lane == 0) rl.route = e_pair;
     } else {
         constexpr int NT = 2 * kThreads - kWave;
@@ -494,6 +538,7 @@ __global__ void __launch_bounds__(2 * kThreads) k_moe_up(const MoeParams p) {
     // weights by a round trip, and with them the end of the kernel
     // (config 2: 11.89 -> 11.75 us per layer)
     if (bx == 0 && j == 0 && wave == 0) {
+        if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
         if (lane < p.top_k) {
             p.ids[t * p.top_k + lane] = my_idx;
             p.wts[t * p.top_k + lane] = my_w;
@@ -547,7 +592,6 @@ __global__ void __launch_bounds__(moe_waves_up(W) * kWave) k_moe_up_split(const 
     if (wave == 0) {
         int e_pair;
         route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &rl.rs, &e_pair, &my_idx, &my_w);
-        if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
         if (lane == 0) rl.route = e_pair;
     } else {
         constexpr int NT = NWV * kWave - kWave;
@@ -601,6 +645,7 @@ __global__ void __launch_bounds__(moe_waves_up(W) * kWave) k_moe_up_split(const 
     }
     // routing / shared-gate outputs, once per token, after the weight loads
     if (bx == 0 && j == 0 && proj == 0 && wave == 0) {
+        if (my_idx < 0 || my_idx >= p.E) my_idx = -1;
         if (lane < p.top_k) {
             p.ids[t * p.top_k + lane] = my_idx;
             p.wts[t * p.top_k + lane] = my_w;
