@@ -417,8 +417,6 @@ __host__ __device__ constexpr int down_cbn() {
 struct RouteLds {
     RouteScratch rs;           // the routing wave's scratch
     int route;                 // expert of this workgroup's pair
-    int ids[kMaxTopK];
-    float wts[kMaxTopK];
 };
 
 // Down-phase state a workgroup prepares before it needs the SwiGLU input:
