@@ -390,9 +390,10 @@ constexpr int kHybUpBytes = 64 * 1024;
 constexpr int kHybDownBytes = 112 * 1024;
 // Larger LDS parts when the workgroup's activations leave room (the host
 // checks): every entry moved into LDS is an L2 request per code saved.
-// 132 KB leaves room for 11 pairs' SwiGLU rows of a d8 row (config 3: 10 routed +
-// the shared expert) beside the routing scratch; 136 KB did not.
-constexpr int kHybDownWideBytes = 132 * 1024;
+// 136 KB leaves room for 11 pairs' SwiGLU rows of a d8 row (config 3: 10 routed +
+// the shared expert); the down kernel has no routing block in LDS (config 3:
+// 132 KB -> 136 KB, 44.70 -> 44.44 us per layer).
+constexpr int kHybDownWideBytes = 136 * 1024;
 // Waves of the workgroups with the larger LDS parts (one workgroup per CU),
 // which read x from LDS: two per SIMD, so one wave decodes while the other
 // waits on its table reads (12 for gate / up measured no faster, 16 for down
@@ -1065,11 +1066,13 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     const size_t cb2 = full2 ? (size_t(1) << gd.BITS) * gd.D * 2 : size_t(kHybDownBytes);
     const size_t xs1 = size_t(gg.NB) * (kBlock * gg.D + 8) * 2;
     const size_t xs2 = size_t(P) * gd.NB * (kBlock * gd.D + 8) * 2;
-    // LDS a workgroup may take, kept clear of the 160 KB by the static routing
-    // block (and slack for alignment)
+    // LDS a workgroup may take, kept clear of the 160 KB by the gate/up
+    // kernels' static routing block (and slack for alignment); the down kernel
+    // has no static LDS
     const size_t lds_room = 160 * 1024 - sizeof(RouteLds) - 256;
+    const size_t lds_room2 = 160 * 1024 - 256;
     pl->wide1 = pl->split && gg.K * gg.D * 2 > kHybSplitBytes && kHybSplitWideBytes + xs1 <= lds_room;
-    pl->wide2 = !full2 && gd.K * gd.D * 2 > kHybDownBytes && kHybDownWideBytes + xs2 <= lds_room;
+    pl->wide2 = !full2 && gd.K * gd.D * 2 > kHybDownBytes && kHybDownWideBytes + xs2 <= lds_room2;
     pl->smem1 = (pl->split ? size_t(pl->wide1 ? kHybSplitWideBytes : kHybSplitBytes) : 2 * cb1) + xs1;
     pl->smem2 = ((shared && full2) ? 2 : 1) * (pl->wide2 ? size_t(kHybDownWideBytes) : cb2) + xs2;
     // Row steps per workgroup: about 2048 row steps per launch spread over the
