@@ -148,8 +148,9 @@ int vqk_moe_expert_gemv(const vqk_weights *w, const void *x, int32_t x_type,
  * Same contract and output order as vqk_moe_expert_gemv, for large N: the
  * pairs are count-sorted by expert ON DEVICE (no host sync, replacing the
  * host argsort at vq_switch.py:5383-5388 and the tile build at 4590-4610),
- * each expert segment is dequantised tile by tile into LDS and multiplied on
- * the bf16/fp16 matrix cores. */
+ * and each expert tile's weights are decoded bit-exactly straight into fp16
+ * matrix-core operands (codebook in LDS, or its first part in LDS and the
+ * rest gathered from L2), fp32 accumulation. */
 int vqk_grouped_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes);
 int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type,
                      int64_t T, const uint32_t *eidx, int64_t N, int64_t xkrep,
