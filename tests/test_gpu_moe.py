@@ -251,3 +251,74 @@ def test_moe_layer_decode_tables_beyond_lds(D, K, shared):
     blk, projs, sh, shv = _block(rng, E, H, I, D, K, k, shared=shared)
     for T in (1, 2):
         _check(blk, projs, sh, shv, rng, T, E, H, k)
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy()
+
+
+@pytest.mark.parametrize("fill", ["random", "zeros", "ones"])
+def test_moe_one_launch_matches_two_launches(fill):
+    """A T = 1 call of a layer whose tables fit LDS runs as one launch (the
+    down workgroups route for themselves and take the SwiGLU rows as tagged
+    64-bit words); a T = 2 call runs the two kernels. The same token gives the
+    same bits both ways, call after call on one workspace whose initial
+    contents are random bytes, zeros or all ones (a zeroed word once passed
+    the first call's tag check for word 0)."""
+    print(f"moe one launch vs two launches, workspace {fill}", flush=True)
+    rng = np.random.default_rng(11)
+    E, H, I, k = 256, 2048, 512, 8
+    blk, projs, sh, shv = _block(rng, E, H, I, 4, 4096, k)
+    x = torch.from_numpy(rng.standard_normal((2, H)).astype(np.float32)).to("cuda", torch.bfloat16)
+    lg = torch.from_numpy(rng.standard_normal((2, E)).astype(np.float32)).cuda()
+    blk.fused(x, lg)
+    if fill == "random":
+        g = torch.Generator(device="cuda").manual_seed(5)
+        blk._ws.copy_(torch.randint(0, 256, blk._ws.shape, dtype=torch.uint8, device="cuda", generator=g))
+    else:
+        blk._ws.fill_(0 if fill == "zeros" else 255)
+    for i in range(5):
+        x = torch.from_numpy(rng.standard_normal((2, H)).astype(np.float32)).to("cuda", torch.bfloat16)
+        lg = torch.from_numpy(rng.standard_normal((2, E)).astype(np.float32)).cuda()
+        y1 = blk.fused(x[:1], lg[:1])
+        y2 = blk.fused(x, lg)
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(y1[0]), _bits(y2[0])), f"call {i}"
+        if i == 0:
+            ref, _, _ = vo.moe_layer(x[:1].float().cpu().numpy(), lg[:1].cpu().numpy(),
+                                     _spec(projs["gate"]), _spec(projs["up"]), _spec(projs["down"]),
+                                     k, h_round=np.float16)
+            assert_close(y1.float().cpu().numpy(), ref, what="one launch")
+
+
+def test_moe_one_launch_graph_replays():
+    """The one-launch layer captured in a HIP graph: every replay (new inputs
+    copied in, eager calls on the same workspace in between) gives the eager
+    call's bits; the call number it keeps in the workspace advances inside the
+    graph too."""
+    print("moe one launch graph replays", flush=True)
+    rng = np.random.default_rng(12)
+    E, H, I, k = 64, 1024, 256, 6
+    blk, projs, sh, shv = _block(rng, E, H, I, 4, 4096, k)
+    x = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float32)).to("cuda", torch.bfloat16)
+    lg = torch.from_numpy(rng.standard_normal((1, E)).astype(np.float32)).cuda()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        blk.fused(x, lg)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = blk.fused(x, lg)
+    for rep in range(4):
+        x.copy_(torch.from_numpy(rng.standard_normal((1, H)).astype(np.float32)).to("cuda", torch.bfloat16))
+        lg.copy_(torch.from_numpy(rng.standard_normal((1, E)).astype(np.float32)).cuda())
+        graph.replay()
+        torch.cuda.synchronize()
+        yr = y.clone()
+        ye = blk.fused(x, lg)
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(yr), _bits(ye)), f"replay {rep}"
+        ref, _, _ = vo.moe_layer(x.float().cpu().numpy(), lg.cpu().numpy(), _spec(projs["gate"]),
+                                 _spec(projs["up"]), _spec(projs["down"]), k, h_round=np.float16)
+        assert_close(yr.float().cpu().numpy(), ref, what=f"replay {rep}")

@@ -69,6 +69,11 @@ struct MoeParams {
     float *gbuf, *ubuf;  // split gate/up phase: workspace [T, P, I] fp32 each, else NULL
     int32_t *ids_out;    // optional user copies
     float *wts_out;
+    // one-launch layer (k_moe_layer1): call number, per-workgroup stamps and
+    // tagged SwiGLU words in the workspace; gate/up workgroups and their row
+    // tiles per pair, down row tiles per token
+    uint64_t *l1_epoch, *l1_stamp, *l1_hw;
+    int32_t l1_g1, l1_gx1, l1_gx2;
 };
 
 // ------------------------------------------------------------ routing
@@ -418,7 +423,36 @@ __host__ __device__ constexpr int down_cbn() {
 struct RouteLds {
     RouteScratch rs;           // the routing wave's scratch
     int route;                 // expert of this workgroup's pair
+    uint32_t call;             // one-launch layer: the call number
 };
+
+// ------------------------------------------------ one-launch layer hand-off
+// The SwiGLU rows of the one-launch layer travel as 64-bit words: two fp16
+// values below a 32-bit tag of (call number n, word index w). For a fixed w
+// the tag is one-to-one in n (an odd multiple of n, then an invertible
+// xorshift-multiply mix), so a word left by any earlier call never carries
+// call n's tag; one 64-bit load both checks a word and delivers it. The
+// offset keeps zeroed or all-ones memory from passing in the first calls of
+// a workspace (without it tag(0, 0) == 0): for n < 4 the words whose tag is
+// 0 or 0xffffffff all have indices above 2^30.
+constexpr int kL1Spins = 1 << 16;        // bound of every poll loop (~45 ms)
+__device__ __forceinline__ uint32_t l1_tag(uint32_t n, uint32_t w) {
+    uint32_t v = n * 0x9E3779B1u + w * 0x85EBCA6Bu + 0x6A09E667u;
+    v ^= v >> 16;
+    v *= 0x7FEB352Du;
+    v ^= v >> 15;
+    v *= 0x846CA68Bu;
+    v ^= v >> 16;
+    return v;
+}
+// A workgroup's stamp once it has read call number n.
+__device__ __forceinline__ uint64_t l1_stamp(uint32_t n) { return (uint64_t(~n) << 32) | n; }
+__device__ __forceinline__ uint64_t l1_load(const uint64_t *a) {
+    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void l1_store(uint64_t *a, uint64_t v) {
+    __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Down-phase state a workgroup prepares before it needs the SwiGLU input:
 // its lane's code row, block words and scales for the first row step.
@@ -436,19 +470,19 @@ struct DownState {
 // meet in LDS for silu(g) * u. With one projection per wave each lane decodes
 // 32 codes instead of 64 and two waves share a SIMD, so one decodes while the
 // other waits on its table reads (config 2: 12.35 -> 11.88 us per layer).
-template <int D, int BITS, int GPB>
-__global__ void __launch_bounds__(2 * kThreads) k_moe_up(const MoeParams p) {
+// The body, shared with the one-launch layer (TAG: the SwiGLU rows go out as
+// tagged words, and the workgroup records the call number it read).
+template <int D, int BITS, int GPB, bool TAG>
+__device__ __forceinline__ void up_fused(const MoeParams &p, uint8_t *smem, RouteLds &rl, int bx,
+                                         int pair) {
     constexpr int CBN = up_cbn<D, BITS>();         // entries of each table in LDS
     constexpr int XH = kBlock * D, XS = XH + 8;
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ RouteLds rl;
     h2 *cbg_lds = reinterpret_cast<h2 *>(smem);
     h2 *cbu_lds = reinterpret_cast<h2 *>(smem + CBN * D * 2);
     f16 *xs = reinterpret_cast<f16 *>(smem + 2 * CBN * D * 2);
     // the tile's gate values, then its up values (fp32), after x
     float *vl = reinterpret_cast<float *>(smem + 2 * CBN * D * 2 + ((p.NB1 * XS * 2 + 15) & ~15));
 
-    const int bx = int(blockIdx.x), pair = int(blockIdx.y);
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int proj = wave >> 2, rw = wave & 3;     // projection (0 gate, 1 up), row wave
     const int lpr = 1 << p.lpr1_log2, rpw = kWave >> p.lpr1_log2;
@@ -473,17 +507,23 @@ __global__ void __launch_bounds__(2 * kThreads) k_moe_up(const MoeParams p) {
     // the barrier's path) measured 0.04 us faster for ~25 more registers.
     int my_idx = -1;
     float my_w = 0.f;
+    uint64_t ev = 0;
     if (wave == 0) {
         int e_pair;
         route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &rl.rs, &e_pair, &my_idx, &my_w);
         if (lane == 0) rl.route = e_pair;
     } else {
         constexpr int NT = 2 * kThreads - kWave;
+        if (TAG && tid == kWave) ev = l1_load(p.l1_epoch);
         stage_x<XH, XS>(p.x, p.x_type, int64_t(t) * p.H, p.H, p.NB1, xs, kWave, NT);
         stage_codebook_fixed<D, CBN, NT, 1>(wg.codebook, wg.K, cbg_lds);
         stage_codebook_fixed<D, CBN, NT, 1>(wu.codebook, wu.K, cbu_lds);
     }
     wait_vmem();
+    if (TAG && tid == kWave) {
+        rl.call = uint32_t(ev);
+        l1_store(p.l1_stamp + bx + pair * p.l1_gx1, l1_stamp(uint32_t(ev)));
+    }
     __syncthreads();
 
     // a NaN logit can leave a selection empty: such a pair reads nothing
@@ -504,8 +544,8 @@ __global__ void __launch_bounds__(2 * kThreads) k_moe_up(const MoeParams p) {
         moe_load<BITS, GPB>(w, cr, blk, sidx, p.ngrp1, a, sc);
     }
     // d8 reads x from LDS per code: its 128 x registers do not fit beside the
-    // rest at two waves per SIMD
-    constexpr bool XL = D == 8;
+    // rest at two waves per SIMD (nor, in the one-launch layer, any x at four)
+    constexpr bool XL = D == 8 || TAG;
     const f16 *xl = xs + (on ? blk : 0) * XS;
     h2 xr[XL ? 1 : 16 * D];
     if constexpr (!XL) load_xregs<D>(xl, xr);
@@ -553,11 +593,34 @@ __global__ void __launch_bounds__(2 * kThreads) k_moe_up(const MoeParams p) {
         }
     }
     __syncthreads();
-    uint16_t *hrow = p.h + (int64_t(t) * p.P + j) * p.I;
-    for (int i = tid; i < p.rows_per_wg1; i += 2 * kThreads) {
-        const int r = r_wg + i;
-        if (r < p.I) hrow[r] = f32_to_h(silu(vl[i]) * vl[p.rows_per_wg1 + i]);
+    if constexpr (TAG) {
+        // rows in pairs (r_wg and I are even): word w = (row of the token's
+        // P * I values) / 2, written through to device scope
+        const uint32_t n = rl.call;
+        const int64_t w0 = ((int64_t(t) * p.P + j) * p.I + r_wg) >> 1;
+        for (int i = tid; 2 * i < p.rows_per_wg1; i += 2 * kThreads) {
+            const int r = r_wg + 2 * i;
+            if (r < p.I) {
+                const uint32_t lo = f32_to_h(silu(vl[2 * i]) * vl[p.rows_per_wg1 + 2 * i]);
+                const uint32_t hi = f32_to_h(silu(vl[2 * i + 1]) * vl[p.rows_per_wg1 + 2 * i + 1]);
+                const uint32_t w = uint32_t(w0 + i);
+                l1_store(p.l1_hw + w, (uint64_t(l1_tag(n, w)) << 32) | (hi << 16) | lo);
+            }
+        }
+    } else {
+        uint16_t *hrow = p.h + (int64_t(t) * p.P + j) * p.I;
+        for (int i = tid; i < p.rows_per_wg1; i += 2 * kThreads) {
+            const int r = r_wg + i;
+            if (r < p.I) hrow[r] = f32_to_h(silu(vl[i]) * vl[p.rows_per_wg1 + i]);
+        }
     }
+}
+
+template <int D, int BITS, int GPB>
+__global__ void __launch_bounds__(2 * kThreads) k_moe_up(const MoeParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ RouteLds rl;
+    up_fused<D, BITS, GPB, false>(p, smem, rl, int(blockIdx.x), int(blockIdx.y));
 }
 
 // K1 for tables beyond LDS: one projection per workgroup (blockIdx.z: 0 gate,
@@ -783,14 +846,14 @@ __device__ __forceinline__ void down_stage_h(const MoeParams &p, int t, f16 *xs,
     }
 }
 
-// The token's P SwiGLU rows (fp16) -> LDS at the padded block stride, then
-// the down projection of the workgroup's rows, scaled per pair by its router
-// weight and combined over the wave (the DPP row reduction is the sum). The
-// first kHFirst chunks per thread of fp16 rows come from `hf`.
-template <int D, int BITS, int GPB, bool W = false>
-__device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint8_t *smem,
-                                         const DownLane &dl, DownState<BITS, GPB> &ds,
-                                         const HFirst &hf) {
+// The decode half of down_run, once the SwiGLU rows are in LDS: the down
+// projection of the workgroup's rows, scaled per pair by its router weight
+// and combined over the wave (the DPP row reduction is the sum); NWV waves
+// take the workgroup's row steps; XLD: x read from LDS per code with the
+// table in LDS (the one-launch layer's register budget).
+template <int D, int BITS, int GPB, bool W = false, int NWV = moe_waves_down(W), bool XLD = false>
+__device__ __forceinline__ void down_decode(const MoeParams &p, int bx, int t, uint8_t *smem,
+                                            const DownLane &dl, DownState<BITS, GPB> &ds) {
     constexpr bool CBL = cb_in_lds(D, BITS);
     constexpr int CBN = down_cbn<D, BITS, W>();
     constexpr int XH = kBlock * D, XS = XH + 8;
@@ -799,20 +862,17 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
     f16 *xs = reinterpret_cast<f16 *>(smem + ((CBL && p.shared) ? 2 : 1) * CBN * D * 2);
     const int tid = threadIdx.x, wave = tid >> 6;
     const MoeW &wd = dl.is_shared ? p.sdown : p.down;
-    down_stage_h<D>(p, t, xs, hf);
-    wait_vmem();
-    __syncthreads();
 
-    h2 xr[W ? 1 : 16 * D];                  // wide (8-wave) instances read x from LDS
+    h2 xr[(W || XLD) ? 1 : 16 * D];         // wide (8-wave) instances read x from LDS
     const f16 *xl = xs + (dl.on ? dl.j * p.NB2 + dl.blk : 0) * XS;
-    if constexpr (!W) load_xregs<D>(xl, xr);
+    if constexpr (!W && !XLD) load_xregs<D>(xl, xr);
     const h2 *cb = CBL ? (dl.is_shared ? cbs_lds : cbd_lds)
                        : reinterpret_cast<const h2 *>(wd.codebook);
     const uint32_t kmax = uint32_t(wd.K - 1);
     const uint32_t kl = dl.is_shared ? 0u : uint32_t(min(wd.K, CBN));     // partly staged: routed only
     const int sidx = GPB == 1 ? dl.blk / p.bpg2 : dl.blk * GPB;
     const int r_wg = bx * p.rows_per_wg2;
-    auto row_at = [&](int st) { return r_wg + (st * moe_waves_down(W) + wave) * dl.rpw + dl.sub; };
+    auto row_at = [&](int st) { return r_wg + (st * NWV + wave) * dl.rpw + dl.sub; };
     auto code_row = [&](int st) -> int64_t {
         const int r = row_at(st);
         return (ds.e >= 0 && r < p.H) ? moe_row(wd, ds.e, p.H, r) : -1;
@@ -825,7 +885,9 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
         moe_load<BITS, GPB>(wd, crn, dl.blk, sidx, p.ngrp2, n, ns);
         float acc = 0.f;
         const ScalesF32<GPB> fs(ds.s);
-        if constexpr (CBL) {
+        if constexpr (CBL && XLD) {
+            if (ds.cr >= 0) acc = ds.wj * block_dot_lx<D, BITS, GPB>(ds.a, xl, fs.v, cb);
+        } else if constexpr (CBL) {
             // all of the block's table reads first (four waves, one per SIMD):
             // 11.91 -> 11.88 us per config-2 layer
             if (ds.cr >= 0) acc = ds.wj * block_dot_all<D, BITS, GPB>(ds.a, xr, fs.v, cb);
@@ -843,6 +905,23 @@ __device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint
 #pragma unroll
         for (int g = 0; g < GPB; ++g) ds.s[g] = ns[g];
     }
+}
+
+// The token's P SwiGLU rows (fp16) -> LDS at the padded block stride, then
+// the down projection of the workgroup's rows, scaled per pair by its router
+// weight and combined over the wave (the DPP row reduction is the sum). The
+// first kHFirst chunks per thread of fp16 rows come from `hf`.
+template <int D, int BITS, int GPB, bool W = false>
+__device__ __forceinline__ void down_run(const MoeParams &p, int bx, int t, uint8_t *smem,
+                                         const DownLane &dl, DownState<BITS, GPB> &ds,
+                                         const HFirst &hf) {
+    constexpr bool CBL = cb_in_lds(D, BITS);
+    constexpr int CBN = down_cbn<D, BITS, W>();
+    f16 *xs = reinterpret_cast<f16 *>(smem + ((CBL && p.shared) ? 2 : 1) * CBN * D * 2);
+    down_stage_h<D>(p, t, xs, hf);
+    wait_vmem();
+    __syncthreads();
+    down_decode<D, BITS, GPB, W>(p, bx, t, smem, dl, ds);
 }
 
 template <int D, int BITS, int GPB, bool W = false>
@@ -871,6 +950,119 @@ __global__ void __launch_bounds__(moe_waves_down(W) * kWave) k_moe_down(const Mo
                          [&](int) { return wt; }, ds);
     down_stage_cb<D, CBN, cb_in_lds(D, BITS), moe_waves_down(W) * kWave>(p, smem);
     down_run<D, BITS, GPB, W>(p, int(blockIdx.x), t, smem, dl, ds, hf);
+}
+
+// ------------------------------------------------------------ one launch
+// Both phases of a layer in one launch, for tables that fit LDS, no shared
+// expert, and a grid that is resident at once (two workgroups per CU):
+// workgroups [0, G1) run the gate/up phase as k_moe_up does, and
+// [G1, G1 + G2) the down phase of one row tile of one token. A down
+// workgroup routes its token itself (the same routine, hence the same
+// experts and weights), stages its table and issues its first weight loads
+// while the gate/up phase runs, then polls the tagged SwiGLU words of its
+// token and decodes as k_moe_down does (eight waves). So the layer costs one
+// kernel boundary, and the down weights' latency overlaps the gate/up phase
+// instead of following the routing read of a second launch.
+// The call number n lives in the workspace: every workgroup reads it at its
+// start and then writes its stamp; workgroup 0, once every stamp shows n,
+// writes n + 1 for the next call, which starts after this launch ends. Any
+// initial workspace contents work (a foreign word passes a tag check with
+// probability 2^-32). Gate/up workgroups never wait on down workgroups and
+// are dispatched first (lower ids), so the polls always end; every poll loop
+// is bounded by kL1Spins all the same.
+struct L1Lds {
+    RouteLds rl;
+    int ids[kMaxTopK];
+    float wts[kMaxTopK];
+};
+
+template <int D, int BITS, int GPB>
+__device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds &ll, int cbi) {
+    constexpr int CBN = 1 << BITS;                 // the whole table (the host checks it fits)
+    constexpr int XH = kBlock * D, XS = XH + 8;
+    constexpr int NT = 2 * kThreads;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int bx = cbi % p.l1_gx2, t = cbi / p.l1_gx2;
+    f16 *xs = reinterpret_cast<f16 *>(smem + CBN * D * 2);
+    uint64_t ev = 0;
+    if (wave == 0) {
+        int e_pair, my_idx = -1;
+        float my_w = 0.f;
+        route(p.logits + int64_t(t) * p.E, p.E, p.top_k, p.norm, -1, &ll.rl.rs, &e_pair, &my_idx, &my_w);
+        if (lane < p.top_k) {
+            ll.ids[lane] = (my_idx >= 0 && my_idx < p.E) ? my_idx : -1;
+            ll.wts[lane] = my_w;
+        }
+    } else {
+        if (tid == kWave) ev = l1_load(p.l1_epoch);
+        stage_codebook_fixed<D, CBN, NT - kWave, 1>(p.down.codebook, p.down.K, reinterpret_cast<h2 *>(smem));
+    }
+    wait_vmem();
+    if (tid == kWave) {
+        ll.rl.call = uint32_t(ev);
+        l1_store(p.l1_stamp + p.l1_g1 + cbi, l1_stamp(uint32_t(ev)));
+    }
+    __syncthreads();
+    const DownLane dl(p);
+    DownState<BITS, GPB> ds;
+    down_prep<BITS, GPB>(p, bx, t, dl, [&](int j) { return ll.ids[j]; }, [&](int j) { return ll.wts[j]; },
+                         ds);
+    // the token's SwiGLU words: each thread polls up to four at a time until
+    // their tags are the call's, then writes their halves into LDS
+    const uint32_t n = ll.rl.call;
+    const int nwd = p.P * p.I / 2;
+    const int64_t w0 = int64_t(t) * nwd;
+    for (int g0 = tid; g0 < nwd; g0 += 4 * NT) {
+        uint64_t v[4] = {0, 0, 0, 0};
+        uint32_t need = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (g0 + u * NT < nwd) need |= 1u << u;
+        for (int spin = 0; need && spin < kL1Spins; ++spin) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if ((need >> u) & 1u) v[u] = l1_load(p.l1_hw + w0 + g0 + u * NT);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (((need >> u) & 1u) &&
+                    uint32_t(v[u] >> 32) == l1_tag(n, uint32_t(w0 + g0 + u * NT)))
+                    need &= ~(1u << u);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int g = g0 + u * NT;
+            if (g < nwd) {
+                const int jj = (2 * g) / p.I, col = (2 * g) % p.I;
+                const int b = jj * p.NB2 + col / XH;
+                *reinterpret_cast<uint32_t *>(xs + b * XS + col % XH) = uint32_t(v[u]);
+            }
+        }
+    }
+    __syncthreads();
+    down_decode<D, BITS, GPB, false, NT / kWave, true>(p, bx, t, smem, dl, ds);
+}
+
+template <int D, int BITS, int GPB>
+__global__ void __launch_bounds__(2 * kThreads, 4) k_moe_layer1(const MoeParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ L1Lds ll;
+    const int b = int(blockIdx.x);
+    if (b < p.l1_g1) {
+        const int bx = b % p.l1_gx1, pair = b / p.l1_gx1;
+        up_fused<D, BITS, GPB, true>(p, smem, ll.rl, bx, pair);
+        if (b == 0) {
+            // every workgroup has read the call number once its stamp shows
+            // it: advance it for the next call
+            const uint32_t n = ll.rl.call;
+            const int nwg = p.l1_g1 + p.l1_gx2 * p.T;
+            for (int i = int(threadIdx.x); i < nwg; i += 2 * kThreads)
+                for (int spin = 0; spin < kL1Spins && l1_load(p.l1_stamp + i) != l1_stamp(n); ++spin) {}
+            __syncthreads();
+            if (threadIdx.x == 0) l1_store(p.l1_epoch, uint64_t(n + 1u));
+        }
+    } else {
+        l1_down<D, BITS, GPB>(p, smem, ll, b - p.l1_g1);
+    }
 }
 
 // ------------------------------------------------ codebooks beyond LDS
@@ -919,6 +1111,7 @@ struct MoeLayout {
     size_t g, u, sgg, sgu, yd, ysh;      // composed paths (sliced-codebook GEMV, grouped GEMM)
     size_t sort;                         // grouped path: pair order and tile records
     size_t gs, us;                       // fused path, split K1: fp32 gate / up rows
+    size_t l1e, l1s, l1w;                // one launch: call number, stamps, tagged SwiGLU words
 };
 
 // Paths of the layer: the two fused decode kernels, the sliced-codebook GEMV
@@ -935,6 +1128,7 @@ static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I, int64_t H, int p
     L.h = align_up(L.sg + sizeof(float) * T);
     L.total = align_up(L.h + (path == kMoeFused && !split ? 2 * size_t(T) * P * I : 0));
     L.g = L.u = L.sgg = L.sgu = L.yd = L.ysh = L.sort = L.gs = L.us = 0;
+    L.l1e = L.l1s = L.l1w = 0;
     if (path == kMoeFused && split) {
         L.gs = L.total;
         L.us = align_up(L.gs + 4 * size_t(T) * P * I);
@@ -982,7 +1176,16 @@ struct MoePlan {
     int path;                 // MoePath
     bool split;               // fused path, tables beyond LDS: one projection per K1 workgroup
     bool wide1, wide2;        // the larger LDS parts of a partly staged table fit
+    bool l1;                  // fused path as one launch (k_moe_layer1)
+    size_t smem_l1;
+    int l1_nwg;               // its workgroups
 };
+
+// Widths of the one-launch layer's instances: tables of 256 to 4096 entries
+// at d 2 and 4, with their scale-group blocking.
+static bool l1_instance(int d, int bits, int gpb) {
+    return ((d == 2 && gpb == 1) || (d == 4 && gpb == 2)) && bits >= 8 && bits <= 12;
+}
 
 static int lg2(int64_t v) {
     int l = 0;
@@ -1135,6 +1338,36 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
         return set_error(VQK_ENOTIMPL, "fused layer: LDS need %zu / %zu B exceeds 160 KB",
                          pl->smem1, pl->smem2);
     pl->lay = moe_layout(T, k, P, gg.OUT, gg.IN, pl->path, E, pl->split);
+    // One launch: gate/up and down workgroups resident together, two per CU
+    // (LDS and 128 VGPRs each), tables in LDS, no shared expert, one format.
+    pl->l1 = false;
+    pl->smem_l1 = 0;
+    pl->l1_nwg = 0;
+    if (pl->path == kMoeFused && !pl->split && full1 && full2 && !shared && gg.D == gd.D &&
+        gg.BITS == gd.BITS && gg.gpb == gd.gpb && l1_instance(gg.D, gg.BITS, gg.gpb) &&
+        pl->grid1.z == 1 && gg.OUT % 2 == 0 && p.rows_per_wg1 % 2 == 0) {
+        const int rpw2 = kWave >> p.lpr2_log2;
+        const int64_t rows2 = int64_t(2 * kThreads / kWave) * rpw2;
+        const int64_t gx2 = (gd.OUT + rows2 - 1) / rows2;
+        const int64_t g1 = int64_t(pl->grid1.x) * pl->grid1.y;
+        const int64_t nwg = g1 + gx2 * T;
+        const size_t sm = std::max(pl->smem1, cb2 + xs2);
+        if (nwg <= 2 * ncu && 2 * (sm + sizeof(L1Lds) + 256) <= 160 * 1024) {
+            pl->l1 = true;
+            pl->smem_l1 = sm;
+            pl->l1_nwg = int(nwg);
+            p.l1_g1 = int32_t(g1);
+            p.l1_gx1 = int32_t(pl->grid1.x);
+            p.l1_gx2 = int32_t(gx2);
+            p.rows_per_wg2 = int32_t(rows2);
+            p.steps2 = 1;
+            MoeLayout &L = pl->lay;
+            L.l1e = L.total;
+            L.l1s = align_up(L.l1e + sizeof(uint64_t));
+            L.l1w = align_up(L.l1s + sizeof(uint64_t) * size_t(nwg));
+            L.total = align_up(L.l1w + sizeof(uint64_t) * size_t(T) * P * size_t(gg.OUT) / 2);
+        }
+    }
     return VQK_OK;
 }
 
@@ -1183,6 +1416,18 @@ static int launch_moe_down_wide(const MoeParams &p, int d, int bits, int gpb, di
     X(D, 10, G) X(D, 11, G) X(D, 12, G) X(D, 13, G) X(D, 14, G) X(D, 15, G) X(D, 16, G)
 #define VQK_UP_CASE(D, B, G) if (d == D && bits == B && gpb == G) return go_up<D, B, G>(p, grid, smem, st);
 #define VQK_DN_CASE(D, B, G) if (d == D && bits == B && gpb == G) return go_down<D, B, G>(p, grid, smem, st);
+
+template <int D, int BITS, int GPB>
+static int go_layer1(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
+    return launch_with_lds<k_moe_layer1<D, BITS, GPB>>(grid, dim3(2 * kThreads), smem, st, p);
+}
+#define VQK_L1_CASE(D, B, G) if (d == D && bits == B && gpb == G) return go_layer1<D, B, G>(p, grid, smem, st);
+static int launch_moe_layer1(const MoeParams &p, int d, int bits, int gpb, dim3 grid, size_t smem,
+                             hipStream_t st) {
+    VQK_L1_CASE(2, 8, 1) VQK_L1_CASE(2, 9, 1) VQK_L1_CASE(2, 10, 1) VQK_L1_CASE(2, 11, 1) VQK_L1_CASE(2, 12, 1)
+    VQK_L1_CASE(4, 8, 2) VQK_L1_CASE(4, 9, 2) VQK_L1_CASE(4, 10, 2) VQK_L1_CASE(4, 11, 2) VQK_L1_CASE(4, 12, 2)
+    return set_error(VQK_ENOTIMPL, "fused layer: no one-launch kernel for d=%d bits=%d", d, bits);
+}
 
 int launch_moe_up(const MoeParams &p, int d, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st) {
     VQK_MOE_BITS(VQK_UP_CASE, 2, 1)
@@ -1413,6 +1658,12 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, i
         return launch_moe_grouped(m, pl, ws, st);
     }
     if (pl.path == kMoeBig) return launch_moe_big(m, pl, ws, st);
+    if (pl.l1) {
+        p.l1_epoch = reinterpret_cast<uint64_t *>(ws + pl.lay.l1e);
+        p.l1_stamp = reinterpret_cast<uint64_t *>(ws + pl.lay.l1s);
+        p.l1_hw = reinterpret_cast<uint64_t *>(ws + pl.lay.l1w);
+        return launch_moe_layer1(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, dim3(unsigned(pl.l1_nwg)), pl.smem_l1, st);
+    }
     rc = split ? launch_moe_up_split(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.wide1, pl.grid1, pl.smem1, st)
                : launch_moe_up(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.grid1, pl.smem1, st);
     if (rc) return rc;
