@@ -295,6 +295,14 @@ __device__ __forceinline__ void route_wave(const float *lg, int E, int k, int no
     *e_want = rp.e_want;
 }
 
+// One instance for E <= 64 * NS (the one-launch layer: its code stays small;
+// slots past E hold key 0, so the selections and weights are route()'s).
+template <int NS>
+__device__ __forceinline__ void route_upto(const float *lg, int E, int k, int norm, int want,
+                                           RouteScratch *rs, int *e_want, int *my_idx, float *my_w) {
+    route_wave<NS>(lg, E, k, norm, want, rs, e_want, my_idx, my_w);
+}
+
 __device__ __forceinline__ void route(const float *lg, int E, int k, int norm, int want,
                                       RouteScratch *rs, int *e_want, int *my_idx, float *my_w) {
     const int ns = (E + kWave - 1) / kWave;              // wave-uniform
@@ -436,6 +444,7 @@ struct RouteLds {
 // a workspace (without it tag(0, 0) == 0): for n < 4 the words whose tag is
 // 0 or 0xffffffff all have indices above 2^30.
 constexpr int kL1Spins = 1 << 16;        // bound of every poll loop (~45 ms)
+constexpr int kL1Slots = 4;              // logits per lane of its routing: E <= 256
 __device__ __forceinline__ uint32_t l1_tag(uint32_t n, uint32_t w) {
     uint32_t v = n * 0x9E3779B1u + w * 0x85EBCA6Bu + 0x6A09E667u;
     v ^= v >> 16;
@@ -510,7 +519,10 @@ __device__ __forceinline__ void up_fused(const MoeParams &p, uint8_t *smem, Rout
     uint64_t ev = 0;
     if (wave == 0) {
         int e_pair;
-        route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &rl.rs, &e_pair, &my_idx, &my_w);
+        if constexpr (TAG)
+            route_upto<kL1Slots>(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &rl.rs, &e_pair, &my_idx, &my_w);
+        else
+            route(lg, p.E, p.top_k, p.norm, is_shared ? -1 : j, &rl.rs, &e_pair, &my_idx, &my_w);
         if (lane == 0) rl.route = e_pair;
     } else {
         constexpr int NT = 2 * kThreads - kWave;
@@ -975,6 +987,11 @@ struct L1Lds {
     int ids[kMaxTopK];
     float wts[kMaxTopK];
 };
+// Waves of a down workgroup that decode rows (all eight stage, route and
+// poll): four, so the down workgroups are as many as the gate/up ones and
+// every CU holds one of each (eight decoding waves over half the CUs doubled
+// each CU's LDS reads: 10.97 us per config-2 layer).
+constexpr int kL1DownWaves = 4;
 
 template <int D, int BITS, int GPB>
 __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds &ll, int cbi) {
@@ -988,7 +1005,8 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
     if (wave == 0) {
         int e_pair, my_idx = -1;
         float my_w = 0.f;
-        route(p.logits + int64_t(t) * p.E, p.E, p.top_k, p.norm, -1, &ll.rl.rs, &e_pair, &my_idx, &my_w);
+        route_upto<kL1Slots>(p.logits + int64_t(t) * p.E, p.E, p.top_k, p.norm, -1, &ll.rl.rs, &e_pair, &my_idx,
+                             &my_w);
         if (lane < p.top_k) {
             ll.ids[lane] = (my_idx >= 0 && my_idx < p.E) ? my_idx : -1;
             ll.wts[lane] = my_w;
@@ -1005,8 +1023,37 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
     __syncthreads();
     const DownLane dl(p);
     DownState<BITS, GPB> ds;
-    down_prep<BITS, GPB>(p, bx, t, dl, [&](int j) { return ll.ids[j]; }, [&](int j) { return ll.wts[j]; },
-                         ds);
+    const bool dec = wave < kL1DownWaves;
+    if (dec) {
+        down_prep<BITS, GPB>(p, bx, t, dl, [&](int j) { return ll.ids[j]; }, [&](int j) { return ll.wts[j]; },
+                             ds);
+        // the weights land here, before the polls: left to itself the
+        // compiler sinks these loads past the poll loop and the barrier (it is
+        // short of registers), which put a whole memory latency between the
+        // SwiGLU words' arrival and the decode
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) asm volatile("" ::"v"(ds.a[i]));
+#pragma unroll
+        for (int g = 0; g < GPB; ++g) asm volatile("" ::"v"(ds.s[g]));
+    }
+    // The block's 32 table entries, looked up while the gate/up phase still
+    // runs: the LDS gathers (bank-conflicted random reads, the decode's
+    // largest cost) leave only the dot products with x for after the SwiGLU
+    // words arrive. Held in registers (pinned, or the compiler would sink
+    // the reads past the polls).
+    typedef typename EntryT<D>::type Ent;
+    struct EntW { uint32_t w[D / 2]; };
+    EntW ent[kBlock];
+    {
+        const Ent *cbe = reinterpret_cast<const Ent *>(smem);
+        const bool live = dec && ds.cr >= 0;
+#pragma unroll
+        for (int i = 0; i < kBlock; ++i) {
+            ent[i] = __builtin_bit_cast(EntW, cbe[live ? block_field<BITS>(ds.a, i) : 0u]);
+#pragma unroll
+            for (int k2 = 0; k2 < D / 2; ++k2) asm volatile("" : "+v"(ent[i].w[k2]));
+        }
+    }
     // the token's SwiGLU words: each thread polls up to four at a time until
     // their tags are the call's, then writes their halves into LDS
     const uint32_t n = ll.rl.call;
@@ -1039,7 +1086,34 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
         }
     }
     __syncthreads();
-    down_decode<D, BITS, GPB, false, NT / kWave, true>(p, bx, t, smem, dl, ds);
+    if (dec) {
+        // the block's dot products with its x chunk, in block_dot_lx's order
+        constexpr int CPG = kBlock / GPB;
+        const Ent *xv = reinterpret_cast<const Ent *>(xs + (dl.on ? dl.j * p.NB2 + dl.blk : 0) * XS);
+        float acc = 0.f;
+        if (ds.cr >= 0) {
+            const ScalesF32<GPB> fs(ds.s);
+            float bsum = 0.f;
+#pragma unroll
+            for (int g = 0; g < GPB; ++g) {
+                float ga = 0.f;
+#pragma unroll
+                for (int q = 0; q < CPG; ++q) {
+                    const int i = g * CPG + q;
+                    const Ent x = xv[i];
+                    h2 xh[D / 2];
+#pragma unroll
+                    for (int k2 = 0; k2 < D / 2; ++k2) xh[k2] = h2{x[2 * k2], x[2 * k2 + 1]};
+                    ga = dot_vec<D>(__builtin_bit_cast(Ent, ent[i]), xh, ga);
+                }
+                bsum = fmaf(fs.v[g], ga, bsum);
+            }
+            acc = ds.wj * bsum;
+        }
+        acc = group_sum(acc, dl.lpr);
+        const int r = bx * p.rows_per_wg2 + wave * dl.rpw + dl.sub;
+        if (dl.v == dl.lpr - 1 && r < p.H) store_act(p.y, p.y_type, int64_t(t) * p.H + r, acc);
+    }
 }
 
 template <int D, int BITS, int GPB>
@@ -1344,10 +1418,10 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     pl->smem_l1 = 0;
     pl->l1_nwg = 0;
     if (pl->path == kMoeFused && !pl->split && full1 && full2 && !shared && gg.D == gd.D &&
-        gg.BITS == gd.BITS && gg.gpb == gd.gpb && l1_instance(gg.D, gg.BITS, gg.gpb) &&
+        gg.BITS == gd.BITS && gg.gpb == gd.gpb && l1_instance(gg.D, gg.BITS, gg.gpb) && E <= kL1Slots * kWave &&
         pl->grid1.z == 1 && gg.OUT % 2 == 0 && p.rows_per_wg1 % 2 == 0) {
         const int rpw2 = kWave >> p.lpr2_log2;
-        const int64_t rows2 = int64_t(2 * kThreads / kWave) * rpw2;
+        const int64_t rows2 = int64_t(kL1DownWaves) * rpw2;
         const int64_t gx2 = (gd.OUT + rows2 - 1) / rows2;
         const int64_t g1 = int64_t(pl->grid1.x) * pl->grid1.y;
         const int64_t nwg = g1 + gx2 * T;
