@@ -987,11 +987,13 @@ struct L1Lds {
     int ids[kMaxTopK];
     float wts[kMaxTopK];
 };
-// Waves of a down workgroup that decode rows (all eight stage, route and
-// poll): four, so the down workgroups are as many as the gate/up ones and
-// every CU holds one of each (eight decoding waves over half the CUs doubled
-// each CU's LDS reads: 10.97 us per config-2 layer).
-constexpr int kL1DownWaves = 4;
+// Waves of a down workgroup that decode rows (all of them stage, route and
+// poll): eight, i.e. 16 rows per workgroup and 128 down workgroups at
+// config 2. With the table entries looked up before the SwiGLU words arrive,
+// the decode after them is short, and fewer workgroups polling the words
+// shorten the hand-off: four decoding waves over 256 workgroups measured
+// 10.33 us per config-2 layer against 10.0 for eight over 128.
+constexpr int kL1DownWaves = 8;
 
 template <int D, int BITS, int GPB>
 __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds &ll, int cbi) {
