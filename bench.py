@@ -658,7 +658,9 @@ def main():
                      "traffic": measured_traffic(f"moe_layer_{a.workload}_traffic.md"),
                      "traffic_source": "profiles/moe_layer_<workload>_traffic.md (rocprofv3 "
                                        "FETCH_SIZE + WRITE_SIZE per dispatch, copy-calibrated)",
-                     "kernel": "k_moe_up (or k_moe_up_split) + k_moe_down (one fused layer call)",
+                     "kernel": ("k_moe_layer1 (the layer in one launch)" if T == 1 and not w["shared"]
+                                and w["d"] in (2, 4) and 8 <= w["bits"] <= 12 and E <= 256
+                                else "k_moe_up (or k_moe_up_split) + k_moe_down (one fused layer call)"),
                      "alg_bytes_per_call": int(alg_per_call), "us_per_call_events": round(us_call, 3)},
         "cpu_baseline": cpu,
     }

@@ -187,7 +187,10 @@ int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type,
  * host. gate/up/down are the routed projections (E experts each; gate and up
  * share one format); sh_* are the shared expert (E == 1, same formats), or
  * NULL. topk_ids / topk_w (device, [T, top_k] int32 / fp32) receive the
- * routing when non-NULL. */
+ * routing when non-NULL. A batch-1 call whose tables fit LDS (no shared
+ * expert, E <= 256) runs as one launch that keeps a call number in the
+ * workspace between calls (any initial contents work); calls sharing one
+ * workspace must not overlap. */
 typedef struct vqk_moe_desc {
     const vqk_weights *gate;
     const vqk_weights *up;
