@@ -322,3 +322,32 @@ def test_moe_one_launch_graph_replays():
         ref, _, _ = vo.moe_layer(x.float().cpu().numpy(), lg.cpu().numpy(), _spec(projs["gate"]),
                                  _spec(projs["up"]), _spec(projs["down"]), k, h_round=np.float16)
         assert_close(yr.float().cpu().numpy(), ref, what=f"replay {rep}")
+
+
+_L1_GEOMS = [
+    (24, 128, 384, 4, 1024, 3, False),
+    (200, 640, 320, 2, 4096, 6, True),
+    (256, 1024, 256, 4, 256, 8, False),
+    (48, 512, 448, 2, 512, 5, True),
+]
+
+
+@pytest.mark.parametrize("geom", _L1_GEOMS, ids=[f"d{g[3]}K{g[4]}E{g[0]}I{g[2]}" for g in _L1_GEOMS])
+def test_moe_one_launch_geometries(geom):
+    """The one-launch layer (batch 1) over assorted geometries -- E not a
+    power of two, I not a multiple of the gate/up row tile, unnormalised
+    routing, d2 and d4 at 8 to 12 bits -- against the oracle and bit for bit
+    against the two kernels (the same token inside a T = 2 call)."""
+    E, H, I, D, K, k, norm = geom
+    print(f"moe one launch geometry {geom}", flush=True)
+    rng = np.random.default_rng(sum(geom[:6]) + 100)
+    blk, projs, sh, shv = _block(rng, E, H, I, D, K, k, norm=norm)
+    x = torch.from_numpy(rng.standard_normal((2, H)).astype(np.float32)).to("cuda", torch.bfloat16)
+    lg = torch.from_numpy(rng.standard_normal((2, E)).astype(np.float32)).cuda()
+    y1 = blk.fused(x[:1], lg[:1])
+    y2 = blk.fused(x, lg)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(y1[0]), _bits(y2[0]))
+    ref, _, _ = vo.moe_layer(x[:1].float().cpu().numpy(), lg[:1].cpu().numpy(), _spec(projs["gate"]),
+                             _spec(projs["up"]), _spec(projs["down"]), k, norm=norm, h_round=np.float16)
+    assert_close(y1.float().cpu().numpy(), ref, what=f"one launch {geom}")
