@@ -1003,8 +1003,11 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int bx = cbi % p.l1_gx2, t = cbi / p.l1_gx2;
     f16 *xs = reinterpret_cast<f16 *>(smem + CBN * D * 2);
+    // the last wave routes (the gate/up workgroup beside it on the CU routes
+    // on its wave 0, and two routing waves on one SIMD slow both: 9.99 ->
+    // 9.83 us per config-2 layer); the others stage the down table
     uint64_t ev = 0;
-    if (wave == 0) {
+    if (wave == NT / kWave - 1) {
         int e_pair, my_idx = -1;
         float my_w = 0.f;
         route_upto<kL1Slots>(p.logits + int64_t(t) * p.E, p.E, p.top_k, p.norm, -1, &ll.rl.rs, &e_pair, &my_idx,
@@ -1014,11 +1017,11 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
             ll.wts[lane] = my_w;
         }
     } else {
-        if (tid == kWave) ev = l1_load(p.l1_epoch);
-        stage_codebook_fixed<D, CBN, NT - kWave, 1>(p.down.codebook, p.down.K, reinterpret_cast<h2 *>(smem));
+        if (tid == 0) ev = l1_load(p.l1_epoch);
+        stage_codebook_fixed<D, CBN, NT - kWave, 0>(p.down.codebook, p.down.K, reinterpret_cast<h2 *>(smem));
     }
     wait_vmem();
-    if (tid == kWave) {
+    if (tid == 0) {
         ll.rl.call = uint32_t(ev);
         l1_store(p.l1_stamp + p.l1_g1 + cbi, l1_stamp(uint32_t(ev)));
     }
