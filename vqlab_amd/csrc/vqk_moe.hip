@@ -1,4 +1,5 @@
-// Fused MoE decode layer: routing + SwitchGLU + combine in two kernels.
+// Fused MoE decode layer: routing + SwitchGLU + combine in one launch
+// (k_moe_layer1: batch 1, tables in LDS) or two kernels.
 //
 // Reference: mlx-lm's SparseMoeBlock / SwitchGLU around VQSwitchLinear,
 // restated in bench/decode_ladder.py:107-119 (softmax(fp32) -> top-k ->
@@ -17,6 +18,9 @@
 //               token's experts; each lane scales its partial by the router
 //               weight and the butterfly reduction IS the combine -- no
 //               atomics, deterministic.
+//   k_moe_layer1 both in one grid: the k_moe_up workgroups, then down
+//               workgroups that route for themselves, fetch their weights and
+//               table entries early and take the SwiGLU rows as tagged words.
 #include <mutex>
 
 #include "vqk_gemv.h"
@@ -970,11 +974,14 @@ __global__ void __launch_bounds__(moe_waves_down(W) * kWave) k_moe_down(const Mo
 // workgroups [0, G1) run the gate/up phase as k_moe_up does, and
 // [G1, G1 + G2) the down phase of one row tile of one token. A down
 // workgroup routes its token itself (the same routine, hence the same
-// experts and weights), stages its table and issues its first weight loads
-// while the gate/up phase runs, then polls the tagged SwiGLU words of its
-// token and decodes as k_moe_down does (eight waves). So the layer costs one
-// kernel boundary, and the down weights' latency overlaps the gate/up phase
-// instead of following the routing read of a second launch.
+// experts and weights), stages its table, loads its weights and looks up its
+// block's table entries while the gate/up phase runs, then polls the tagged
+// SwiGLU words of its token and finishes k_moe_down's arithmetic (same order,
+// same bits) with the dot products. So the layer costs one kernel boundary,
+// and the down weights' latency and table gathers overlap the gate/up phase
+// instead of following the routing read of a second launch. A poll that ran
+// out of kL1Spins (a gate/up workgroup held up for ~45 ms) would go on with
+// the words it has.
 // The call number n lives in the workspace: every workgroup reads it at its
 // start and then writes its stamp; workgroup 0, once every stamp shows n,
 // writes n + 1 for the next call, which starts after this launch ends. Any
