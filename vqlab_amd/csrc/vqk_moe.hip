@@ -864,10 +864,8 @@ __device__ __forceinline__ void down_stage_h(const MoeParams &p, int t, f16 *xs,
 
 // The decode half of down_run, once the SwiGLU rows are in LDS: the down
 // projection of the workgroup's rows, scaled per pair by its router weight
-// and combined over the wave (the DPP row reduction is the sum); NWV waves
-// take the workgroup's row steps; XLD: x read from LDS per code with the
-// table in LDS (the one-launch layer's register budget).
-template <int D, int BITS, int GPB, bool W = false, int NWV = moe_waves_down(W), bool XLD = false>
+// and combined over the wave (the DPP row reduction is the sum).
+template <int D, int BITS, int GPB, bool W = false>
 __device__ __forceinline__ void down_decode(const MoeParams &p, int bx, int t, uint8_t *smem,
                                             const DownLane &dl, DownState<BITS, GPB> &ds) {
     constexpr bool CBL = cb_in_lds(D, BITS);
@@ -879,16 +877,16 @@ __device__ __forceinline__ void down_decode(const MoeParams &p, int bx, int t, u
     const int tid = threadIdx.x, wave = tid >> 6;
     const MoeW &wd = dl.is_shared ? p.sdown : p.down;
 
-    h2 xr[(W || XLD) ? 1 : 16 * D];         // wide (8-wave) instances read x from LDS
+    h2 xr[W ? 1 : 16 * D];                  // wide (8-wave) instances read x from LDS
     const f16 *xl = xs + (dl.on ? dl.j * p.NB2 + dl.blk : 0) * XS;
-    if constexpr (!W && !XLD) load_xregs<D>(xl, xr);
+    if constexpr (!W) load_xregs<D>(xl, xr);
     const h2 *cb = CBL ? (dl.is_shared ? cbs_lds : cbd_lds)
                        : reinterpret_cast<const h2 *>(wd.codebook);
     const uint32_t kmax = uint32_t(wd.K - 1);
     const uint32_t kl = dl.is_shared ? 0u : uint32_t(min(wd.K, CBN));     // partly staged: routed only
     const int sidx = GPB == 1 ? dl.blk / p.bpg2 : dl.blk * GPB;
     const int r_wg = bx * p.rows_per_wg2;
-    auto row_at = [&](int st) { return r_wg + (st * NWV + wave) * dl.rpw + dl.sub; };
+    auto row_at = [&](int st) { return r_wg + (st * moe_waves_down(W) + wave) * dl.rpw + dl.sub; };
     auto code_row = [&](int st) -> int64_t {
         const int r = row_at(st);
         return (ds.e >= 0 && r < p.H) ? moe_row(wd, ds.e, p.H, r) : -1;
@@ -901,9 +899,7 @@ __device__ __forceinline__ void down_decode(const MoeParams &p, int bx, int t, u
         moe_load<BITS, GPB>(wd, crn, dl.blk, sidx, p.ngrp2, n, ns);
         float acc = 0.f;
         const ScalesF32<GPB> fs(ds.s);
-        if constexpr (CBL && XLD) {
-            if (ds.cr >= 0) acc = ds.wj * block_dot_lx<D, BITS, GPB>(ds.a, xl, fs.v, cb);
-        } else if constexpr (CBL) {
+        if constexpr (CBL) {
             // all of the block's table reads first (four waves, one per SIMD):
             // 11.91 -> 11.88 us per config-2 layer
             if (ds.cr >= 0) acc = ds.wj * block_dot_all<D, BITS, GPB>(ds.a, xr, fs.v, cb);
