@@ -74,6 +74,16 @@ WORKLOADS = {
                   layers=2, dead=0.2, kind="mtp",
                   desc="MTP verify batch on the config-3 layer, T=16, 20% skipzero rows "
                        "(BASELINE configs[3])"),
+    # config 4 on SURVEY 8(d)'s routing: each touched expert gets 1..min(8, T)
+    # of the batch's tokens, no token repeats an expert (mtp_logits)
+    "c4survey": dict(H=4096, E=512, I=1024, k=10, shared=True, d=8, K=16384, bits=14, T=64,
+                     layers=2, dead=0.2, kind="mtp", routing="survey",
+                     desc="MTP verify batch on the config-3 layer, T=64, 20% skipzero rows, "
+                          "each touched expert 1..8 tokens (BASELINE configs[3])"),
+    "c4t16survey": dict(H=4096, E=512, I=1024, k=10, shared=True, d=8, K=16384, bits=14, T=16,
+                        layers=2, dead=0.2, kind="mtp", routing="survey",
+                        desc="MTP verify batch on the config-3 layer, T=16, 20% skipzero rows, "
+                             "each touched expert 1..8 tokens (BASELINE configs[3])"),
     "c5": dict(N=2048, H=5120, F=17408, d=8, K=65536, kind="prefill",
                desc="Dense Qwen3.8-27B-shaped VQ prefill: 5120x17408 then 17408x5120, "
                     "x [2048, 5120] (BASELINE configs[4])"),
@@ -134,6 +144,33 @@ def expert_bytes(w):
     gu = I * (((H // d) + 31) // 32 * bits * 4 + (H // 64) * 2)
     dn = H * (((I // d) + 31) // 32 * bits * 4 + (I // 64) * 2)
     return 2 * gu + dn
+
+
+def mtp_logits(rng, T, E, k, cap=8):
+    """Router logits [T, E] (fp32) whose top-k is an MTP verify batch's routing
+    as SURVEY 8(d) draws it: experts are taken in random order, each with a
+    uniform count of 1..min(cap, T) tokens, until the T*k pairs are placed;
+    each expert's tokens are the least-loaded ones that still need experts
+    (never a token twice), so every token gets exactly k distinct experts.
+    Selected logits lie in [4, 5), the rest are N(0, 1) clipped below 3."""
+    need = np.full(T, k)
+    order = rng.permutation(E)
+    pick = np.zeros((T, E), bool)
+    left = T * k
+    for e in order:
+        if left == 0:
+            break
+        c = min(int(rng.integers(1, min(cap, T) + 1)), left, int((need > 0).sum()))
+        cand = np.flatnonzero(need > 0)
+        cand = cand[np.lexsort((rng.random(cand.size), -need[cand]))][:c]
+        pick[cand, e] = True
+        need[cand] -= 1
+        left -= c
+    if left:
+        raise RuntimeError("mtp_logits: pairs left unplaced")
+    lg = np.minimum(rng.standard_normal((T, E)), 3.0)
+    lg[pick] = 4.0 + rng.random(int(pick.sum()))
+    return lg.astype(np.float32)
 
 
 # ------------------------------------------------------------ CPU baseline
@@ -382,7 +419,12 @@ def run_mtp(torch, dev, a, w):
         layers.append(VQSparseMoeBlock(VQSwitchGLU(gp, up, dn), k, True, sh, sg))
     total = a.warmup + a.steps
     xs = [torch.randn((T, H), device=dev, generator=g).to(torch.bfloat16) for _ in range(L)]
-    logits = torch.randn((total, L, T, E), device=dev, generator=g)
+    if w.get("routing") == "survey":
+        rng = np.random.default_rng(4321)
+        logits = torch.from_numpy(np.stack([np.stack([mtp_logits(rng, T, E, k) for _ in range(L)])
+                                            for _ in range(total)])).to(dev)
+    else:
+        logits = torch.randn((total, L, T, E), device=dev, generator=g)
     ys = [None] * L
 
     def step(s):
@@ -397,18 +439,24 @@ def run_mtp(torch, dev, a, w):
     wpr_h, wpr_i = ((H // d) + 31) // 32 * bits, ((I // d) + 31) // 32 * bits
     row_gu, row_dn = wpr_h * 4 + (H // 64) * 2, wpr_i * 4 + (I // 64) * 2
     top = torch.topk(logits[a.warmup:].float(), k, dim=-1).indices.cpu().numpy()
-    packed = 0
+    packed, flop, touched = 0, 0.0, 0
     for s in range(a.steps):
         for l in range(L):
             u = np.unique(top[s, l])
             lr = live_rows[l]
+            touched += len(u)
             packed += int(lr[0][u].sum() + lr[1][u].sum()) * row_gu + int(lr[2][u].sum()) * row_dn
+            # 2 FLOP per weight of each live row, once per routed pair
+            e = top[s, l].ravel()
+            flop += 2.0 * (float(lr[0][e].sum() + lr[1][e].sum()) * H + float(lr[2][e].sum()) * I)
     packed += a.steps * L * (2 * I * row_gu + H * row_dn)          # shared expert
+    flop += a.steps * L * T * 2.0 * 3 * H * I
     calls = a.steps * L
     alg_per_call = packed / calls + 6 * K * d * 2 + T * (2 * H * 2 + E * 4)
     us_call = ev_ms * 1e3 / calls
     achieved = alg_per_call / (us_call * 1e-6) / 1e9
     value = packed / wall / 1e9
+    tfs = flop / calls / (us_call * 1e-6) / 1e12
     cpu = None if a.no_cpu else cpu_baseline(dict(w, shared=False))
     return {
         "metric": "packed-weight GB/s (% of HBM peak) and µs/call for the MTP-verify MoE layer",
@@ -416,9 +464,12 @@ def run_mtp(torch, dev, a, w):
         "config": {"workload": w["desc"], "hidden": H, "experts": E, "intermediate": I,
                    "top_k": k, "shared_expert": True, "d": d, "K": K, "index_bits": bits,
                    "group": 64, "tokens": T, "dead_row_frac": w["dead"], "io_dtype": "bf16",
-                   "layers_rotated": L},
+                   "layers_rotated": L, "routing": w.get("routing", "iid N(0,1) logits"),
+                   "touched_experts_per_call": round(touched / calls, 1)},
         "us_per_call": round(wall * 1e6 / calls, 3),
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "mfma": {"achieved": round(tfs, 2), "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
+                 "frac": round(tfs / MFMA_F16_PEAK_TFS, 4), "flop_per_call": int(flop / calls)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": (measured_traffic(f"mtp_verify_{a.workload}_traffic.md")
@@ -530,39 +581,10 @@ def run_prefill(torch, dev, a, w):
     }, wall, a.steps
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--mtp-path", default="fused", choices=("fused", "composed"),
-                    help="c4 workloads: the layer entry point, or torch glue around grouped calls")
-    a = ap.parse_args()
-    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(see DESIGN.md, 'How the path would shard').", file=sys.stderr)
-        sys.exit(2)
-    import torch
-    sys.path.insert(0, ROOT)
-    import vqlab_amd
-    vqlab_amd.load()
-    w = WORKLOADS[a.workload]
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    if w.get("kind") in ("mtp", "prefill", "dense_gemv"):
-        fn = {"mtp": run_mtp, "prefill": run_prefill, "dense_gemv": run_dense_gemv}[w["kind"]]
-        body, wall, _ = fn(torch, dev, a, w)
-        out = {"metric": body.pop("metric"), "value": body.pop("value"), "unit": body.pop("unit"),
-               "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-               "ms_per_step": round(wall * 1e3 / a.steps, 5), "higher_is_better": True,
-               "scaling": "weak", "vs_baseline": None, "dtype": body.pop("dtype"),
-               "data": "synthetic (random VQ weights, N(0,1) activations and router logits; "
-                       "no checkpoints offline)"}
-        out.update(body)
-        print(json.dumps(out), flush=True)
-        return
+def run_layer(torch, dev, a, w):
+    """c2 / c3 / c3b4: one fused MoE decode layer call (vqk_moe_decode_layer:
+    routing, gate/up, SwiGLU, down, combine on device) per layer per step,
+    over `layers` distinct random layers, captured in one HIP graph."""
     g = torch.Generator(device=dev)
     g.manual_seed(1234)
     L, T, E, H, k = w["layers"], w["T"], w["E"], w["H"], w["k"]
@@ -583,7 +605,7 @@ def main():
         d = blk._fused_desc(keep)
         ws = ctypes.c_size_t()
         LB.check(LB.lib().vqk_moe_decode_layer_workspace(ctypes.byref(d), T, ctypes.byref(ws)))
-        wbuf = torch.empty(ws.value, dtype=torch.uint8, device=dev)
+        wbuf = torch.zeros(ws.value, dtype=torch.uint8, device=dev)   # header starts zeroed
         keeps.append(keep)
         descs.append(d)
         wss.append((wbuf, ws.value))
@@ -641,10 +663,7 @@ def main():
     cpu = None if a.no_cpu else cpu_baseline(w)
     out = {
         "metric": "packed-weight GB/s (% of HBM peak) and µs/token for MoE VQ decode layer",
-        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
-        "warmup": a.warmup, "ms_per_step": round(wall * 1e3 / a.steps, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
-        "data": "synthetic (random VQ weights and N(0,1) router logits; no checkpoints offline)",
+        "value": round(value, 2), "unit": "GB/s", "dtype": "fp16",
         "config": {"workload": w["desc"], "hidden": H, "experts": E, "intermediate": w["I"],
                    "top_k": k, "shared_expert": w["shared"], "d": w["d"], "K": w["K"],
                    "index_bits": w["bits"], "group": 64, "batch": T, "io_dtype": "bf16",
@@ -675,6 +694,90 @@ def main():
             "achieved_us": round(us_call, 3), "frac": round(floor_us / us_call, 4),
             "basis": f"{L2_REQ_PER_CLK_PER_CU} L2 requests per clock per CU x {N_CUS} CUs x "
                      f"{PEAK_CLOCK_GHZ} GHz (published peak clock)"}
+    return out, wall, calls
+
+
+def _summary(name, body):
+    """The per-workload figures of the default line's `workloads` object."""
+    r = body["roofline"]
+    out = {"workload": body["config"]["workload"],
+           "us_per_call": r.get("us_per_call_events"),
+           "value": body["value"], "unit": body["unit"],
+           "roofline_frac": r["frac"], "roofline_unit": r["unit"],
+           "achieved": r["achieved"], "traffic": r.get("traffic"),
+           "alg_bytes_per_call": r.get("alg_bytes_per_call"), "kernel": r.get("kernel")}
+    if "us_per_step_events" in body:
+        out["us_per_step"] = body["us_per_step_events"]
+    if "mfma" in body:
+        out["mfma_frac"] = body["mfma"]["frac"]
+        out["touched_experts_per_call"] = body["config"]["touched_experts_per_call"]
+    if "l2_request_floor" in r:
+        out["l2_request_floor"] = r["l2_request_floor"]
+    return out
+
+
+# every BASELINE config beside the headline: (workload, timed steps)
+EXTRA_WORKLOADS = [("c1", 20), ("c3", 20), ("c3b4", 10), ("c4t16", 10), ("c4t16survey", 10),
+                   ("c4", 8), ("c4survey", 8), ("c5", 5)]
+
+
+def extra_workloads(torch, dev, a):
+    """Each other configuration timed in this process with HIP events (a few
+    steps each, no CPU baseline): µs per call, roofline fraction, traffic."""
+    res = {}
+    for name, steps in EXTRA_WORKLOADS:
+        w = WORKLOADS[name]
+        sub = argparse.Namespace(**vars(a))
+        sub.workload, sub.steps, sub.warmup, sub.no_cpu, sub.mtp_path = name, steps, 3, True, "fused"
+        t0 = time.perf_counter()
+        try:
+            body, _, _ = RUNNERS[w.get("kind", "layer")](torch, dev, sub, w)
+            res[name] = _summary(name, body)
+        except Exception as e:                      # reported, never hidden
+            res[name] = {"error": f"{type(e).__name__}: {e}"}
+        res[name]["seconds"] = round(time.perf_counter() - t0, 1)
+        log(f"workload {name}: {res[name]}")
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return res
+
+
+RUNNERS = {"layer": run_layer, "mtp": run_mtp, "prefill": run_prefill, "dense_gemv": run_dense_gemv}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="default workload only: skip the other configurations' figures")
+    ap.add_argument("--mtp-path", default="fused", choices=("fused", "composed"),
+                    help="c4 workloads: the layer entry point, or torch glue around grouped calls")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(see DESIGN.md, 'How the path would shard').", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    sys.path.insert(0, ROOT)
+    import vqlab_amd
+    vqlab_amd.load()
+    w = WORKLOADS[a.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    body, wall, _ = RUNNERS[w.get("kind", "layer")](torch, dev, a, w)
+    out = {"metric": body.pop("metric"), "value": body.pop("value"), "unit": body.pop("unit"),
+           "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+           "ms_per_step": round(wall * 1e3 / a.steps, 5), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": body.pop("dtype"),
+           "data": "synthetic (random VQ weights, N(0,1) activations and router logits; "
+                   "no checkpoints offline)"}
+    out.update(body)
+    if a.workload == "c2" and not a.no_workloads:
+        out["workloads"] = extra_workloads(torch, dev, a)
     print(json.dumps(out), flush=True)
 
 

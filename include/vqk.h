@@ -187,10 +187,25 @@ int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type,
  * host. gate/up/down are the routed projections (E experts each; gate and up
  * share one format); sh_* are the shared expert (E == 1, same formats), or
  * NULL. topk_ids / topk_w (device, [T, top_k] int32 / fp32) receive the
- * routing when non-NULL. A batch-1 call whose tables fit LDS (no shared
- * expert, E <= 256) runs as one launch that keeps a call number in the
- * workspace between calls (any initial contents work); calls sharing one
- * workspace must not overlap. */
+ * routing when non-NULL.
+ *
+ * Workspace: vqk_moe_decode_layer_workspace bytes, 256-byte aligned. Its
+ * first VQK_MOE_HEADER_BYTES are a header that must be zero before the
+ * workspace's first call (hipMemset once when it is allocated, or
+ * vqk_moe_layer_reset) and that only layer calls may write afterwards; the
+ * rest is scratch whose contents do not matter. One workspace may serve any
+ * number of layers, geometries and T, one call at a time: calls sharing a
+ * workspace must not overlap. A batch-1 call whose tables fit LDS (no shared
+ * expert, E <= 256, d 2 or 4 with 8-12-bit codes) runs as ONE launch whose
+ * workgroups hand the SwiGLU rows to each other through the header, with a
+ * call number kept there between calls. Its waits are bounded (~45 ms): a wait
+ * that runs out -- only possible when other work holds the GPU's compute
+ * units that long -- makes that call's affected output rows NaN and sets the
+ * header's error word, after which every later one-launch call on the
+ * workspace returns NaN rows until vqk_moe_layer_reset. No launch ever
+ * computes on data that did not arrive. vqk_moe_layer_status reports the
+ * error word. */
+#define VQK_MOE_HEADER_BYTES 49152u
 typedef struct vqk_moe_desc {
     const vqk_weights *gate;
     const vqk_weights *up;
@@ -211,6 +226,16 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type,
                          int32_t y_type, int32_t *topk_ids, float *topk_w,
                          void *workspace, size_t ws_bytes, void *stream);
 
+/* Header state of a layer workspace (NULL = the current device's
+ * no-allocation scratch), with no counterpart in the reference:
+ * vqk_moe_layer_status synchronises `stream` and returns VQK_OK, or
+ * VQK_EDEVICE with a message when a one-launch call's wait ran out on this
+ * workspace; it changes nothing. vqk_moe_layer_reset zeroes the header with a
+ * kernel on `stream` (no host synchronisation), clearing the error word and
+ * the call number. */
+int vqk_moe_layer_status(const void *workspace, void *stream);
+int vqk_moe_layer_reset(void *workspace, void *stream);
+
 /* ---- no-allocation variant of vqk_moe_decode_layer ------------------------
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
@@ -222,6 +247,8 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type,
  * VQK_ENOSPACE before any launch (config 4 at T = 64 needs about 19 MB).
  * Every call on one GPU shares that GPU's array: calls that overlap on one
  * GPU (two streams, two threads) race and must be serialised by the caller.
+ * The array starts zeroed (static device storage), which its header needs;
+ * vqk_moe_layer_status / vqk_moe_layer_reset with workspace NULL act on it.
  * The stream must belong to the current device (else VQK_EINVAL). */
 #define VQK_NOALLOC_SCRATCH_BYTES (32u << 20)
 int vqk_moe_decode_layer_noalloc(const vqk_moe_desc *m, const void *x, int32_t x_type,
@@ -264,21 +291,32 @@ int vqk_gemmseg_fits(int32_t D, int64_t K, int32_t G, int32_t pack_bits,
  *   decode_bf16io      VQ_DECODE_BF16IO: 0 (default) = the fused routed path
  *                      rounds its outputs through fp16 (VQK_VIA_F16); 1 = once
  *                      into y's type
- *   prefill_bf16io     VQ_GEMMSEG_BF16IO: the same for the grouped GEMM path */
+ *   prefill_bf16io     VQ_GEMMSEG_BF16IO: the same for the grouped GEMM path
+ *                      (both flags keep the single rounding for bf16 x only,
+ *                      like the reference's _keep_bf16, vq_switch.py:5306,
+ *                      5369; other x types still round through fp16)
+ *   crowded_grouped    an extension beyond the reference's dispatch, no VQ_*
+ *                      flag: 1 (default) also sends calls whose pairs crowd
+ *                      onto few experts (N >= 4 and N >= 2E) to the grouped
+ *                      GEMM, which reads each expert's rows once per tile
+ *                      instead of once per pair; 0 = the reference's rule
+ *                      (N > fused_max_n only). Both paths meet the same
+ *                      accuracy bar; the summation order differs. */
 typedef struct vqk_options {
     int64_t fused_max_n;
     int64_t dense_fused_max_n;
     int32_t decode_bf16io;
     int32_t prefill_bf16io;
+    int32_t crowded_grouped;
 } vqk_options;
 void vqk_options_default(vqk_options *o);
 void vqk_options_from_env(vqk_options *o);
 
 /* VQSwitchLinear.__call__'s dispatch (vq_switch.py:5284-5423): the fused GEMV
- * (vqk_moe_expert_gemv) for at most fused_max_n pairs, else -- or when the
- * pairs crowd onto few experts (N >= 4 and N >= 2E: the GEMV would read an
- * expert's rows once per pair) -- the grouped GEMM (vqk_grouped_gemm), when
- * it takes the module's format. Same arguments as vqk_grouped_gemm plus the
+ * (vqk_moe_expert_gemv) for at most fused_max_n pairs, else -- or, with
+ * crowded_grouped (an extension, see vqk_options), when the pairs crowd onto
+ * few experts -- the grouped GEMM (vqk_grouped_gemm), when it takes the
+ * module's format. Same arguments as vqk_grouped_gemm plus the
  * options (NULL = defaults); the workspace query returns 0 when the call
  * will run the GEMV. */
 int vqk_switch_apply_workspace(const vqk_weights *w, int64_t N, const vqk_options *o,

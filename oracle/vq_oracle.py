@@ -224,12 +224,24 @@ def route(logits: np.ndarray, top_k: int, norm: bool = True):
     test_qwen3_5_parity.py:187-191). Ties are broken towards the lower
     expert id (stable descending sort); on continuous logits they have
     probability zero. Returns (ids [T, k] int64 in descending-weight order,
-    weights [T, k] float64)."""
+    weights [T, k] float64).
+
+    NaN logits (which make the reference's softmax NaN throughout) are this
+    build's defined extension: they take no part in the softmax, rank below
+    every other logit (-inf included) and are never selected; a row with
+    fewer than top_k non-NaN logits fills its last selections with id -1 and
+    weight 0. Every row needs a finite logit."""
     lg = np.asarray(logits, np.float64)
-    pr = np.exp(lg - lg.max(-1, keepdims=True))
+    nan = np.isnan(lg)
+    lgm = np.where(nan, -np.inf, lg)
+    pr = np.exp(lgm - lgm.max(-1, keepdims=True))
     pr = pr / pr.sum(-1, keepdims=True)
-    idx = np.argsort(-pr, axis=-1, kind="stable")[:, :top_k]
+    pos = np.broadcast_to(np.arange(lg.shape[-1]), lg.shape)
+    idx = np.stack([np.lexsort((pos[t], nan[t], -pr[t])) for t in range(lg.shape[0])])[:, :top_k]
     w = np.take_along_axis(pr, idx, -1)
+    dead = np.take_along_axis(nan, idx, -1)
+    idx = np.where(dead, -1, idx)
+    w = np.where(dead, 0.0, w)
     if norm:
         w = w / w.sum(-1, keepdims=True)
     return idx, w
@@ -325,7 +337,8 @@ def moe_layer(x, logits, gate, up, down, top_k, norm=True, shared=None,
     for t in range(T):
         for j in range(top_k):
             e = int(ids[t, j])
-            y[t] += w[t, j] * mlp(x[t], gate, up, down, e)
+            if e >= 0:                     # -1: a selection left empty (NaN logits)
+                y[t] += w[t, j] * mlp(x[t], gate, up, down, e)
         if shared is not None:
             z = float(np.asarray(shared_gate, np.float64) @ x[t])
             sg = float(bf16_round(sigmoid(bf16_round(z)))) if ref else sigmoid(z)

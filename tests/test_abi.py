@@ -320,3 +320,60 @@ def test_apply_workspace_follows_dispatch(L):
         L.check(L.lib().vqk_linear_apply_workspace(ctypes.byref(w), N, ctypes.byref(o), ctypes.byref(ws)))
         assert (ws.value == 0) == fused, (N, ws.value)
     assert np.int64(L.VQK_VIA_F16) == 0x100
+
+
+def test_moe_header_constant_and_paths(L):
+    """The Python mirror of VQK_MOE_HEADER_BYTES is the header's value; the
+    layer's workspace starts with that header at every T; the one-launch form
+    is planned for batch 1 only (config-2 shape: T = 1 one launch, T = 2 the
+    two fused kernels), and the test hook switches it off. Host only: plans,
+    no launches."""
+    import ctypes
+    import sys
+    sys.path.insert(0, str(ROOT / "tests"))
+    from vq_cases import PATH_FUSED, PATH_GROUPED, PATH_ONE_LAUNCH, hooks
+    txt = (ROOT / "include" / "vqk.h").read_text()
+    m = re.search(r"#define\s+VQK_MOE_HEADER_BYTES\s+(\d+)u", txt)
+    assert m and int(m.group(1)) == L.VQK_MOE_HEADER_BYTES
+    for hook in ("vqk__test_l1_spins", "vqk__test_l1_mode", "vqk__test_moe_path"):
+        assert hasattr(L.lib(), hook) and hook not in txt
+
+    def proj(E, OUT, IN, base):
+        w = L.VQKWeights()
+        w.codes, w.code_cols, w.code_type, w.pack_bits = base, (IN // 4 + 31) // 32 * 12, L.VQK_U32, 12
+        w.codebook, w.K, w.D, w.group = base + (1 << 26), 4096, 4, 64
+        w.scales, w.E, w.OUT, w.IN = base + (1 << 27), E, OUT, IN
+        return w
+    E, H, I = 256, 2048, 512
+    ws_ = [proj(E, I, H, 1 << 30), proj(E, I, H, 2 << 30), proj(E, H, I, 3 << 30)]
+    d = L.VQKMoeDesc()
+    d.gate, d.up, d.down = (ctypes.pointer(w) for w in ws_)
+    d.top_k, d.norm_topk = 8, 1
+    p, sz = ctypes.c_int32(), ctypes.c_size_t()
+    for T, want in ((1, PATH_ONE_LAUNCH), (2, PATH_FUSED), (4, PATH_FUSED), (64, PATH_GROUPED)):
+        L.check(hooks().vqk__test_moe_path(ctypes.byref(d), T, ctypes.byref(p)))
+        assert p.value == want, (T, p.value)
+        L.check(L.lib().vqk_moe_decode_layer_workspace(ctypes.byref(d), T, ctypes.byref(sz)))
+        assert sz.value > L.VQK_MOE_HEADER_BYTES
+    prev = hooks().vqk__test_l1_mode(1)
+    try:
+        L.check(hooks().vqk__test_moe_path(ctypes.byref(d), 1, ctypes.byref(p)))
+        assert p.value == PATH_FUSED
+    finally:
+        hooks().vqk__test_l1_mode(prev)
+
+
+def test_options_crowded_rule_is_switchable(L):
+    """crowded_grouped (an extension beyond the reference's dispatch) is on
+    by default; off, only fused_max_n decides, as in the reference."""
+    import ctypes
+    w = L.VQKWeights()
+    w.codes, w.code_cols, w.code_type, w.pack_bits = 1 << 20, 16 * 12, L.VQK_U32, 12
+    w.codebook, w.K, w.D, w.group = 1 << 24, 4096, 4, 64
+    w.scales, w.E, w.OUT, w.IN = 1 << 28, 64, 256, 2048
+    assert L.options().crowded_grouped == 1
+    ws = ctypes.c_size_t()
+    for crowded, grouped in ((1, True), (0, False)):
+        o = L.options(crowded_grouped=crowded)
+        L.check(L.lib().vqk_switch_apply_workspace(ctypes.byref(w), 128, ctypes.byref(o), ctypes.byref(ws)))
+        assert (ws.value > 0) == grouped

@@ -257,38 +257,59 @@ def _bits(t):
     return t.contiguous().view(torch.int16).cpu().numpy()
 
 
+def _xl(rng, T, H, E):
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to("cuda", torch.bfloat16)
+    lg = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).cuda()
+    return x, lg
+
+
 @pytest.mark.parametrize("fill", ["random", "zeros", "ones"])
 def test_moe_one_launch_matches_two_launches(fill):
     """A T = 1 call of a layer whose tables fit LDS runs as one launch (the
     down workgroups route for themselves and take the SwiGLU rows as tagged
-    64-bit words); a T = 2 call runs the two kernels. The same token gives the
-    same bits both ways, call after call on one workspace whose initial
-    contents are random bytes, zeros or all ones (a zeroed word once passed
-    the first call's tag check for word 0)."""
-    print(f"moe one launch vs two launches, workspace {fill}", flush=True)
+    64-bit words through the workspace header); T = 2 runs the two kernels,
+    and so does T = 1 with the one launch switched off. The same token gives
+    the same bits all three ways, call after call on one workspace whose
+    scratch part holds random bytes, zeros or all ones (the header starts
+    zeroed, as the contract asks). In between, T = 2 calls whose second token
+    is all zeros write zero SwiGLU rows across the scratch part: they must not
+    disturb the following one-launch calls."""
+    from vq_cases import PATH_FUSED, PATH_ONE_LAUNCH, moe_path, two_kernels
+    print(f"moe one launch vs two launches, scratch {fill}", flush=True)
     rng = np.random.default_rng(11)
     E, H, I, k = 256, 2048, 512, 8
     blk, projs, sh, shv = _block(rng, E, H, I, 4, 4096, k)
-    x = torch.from_numpy(rng.standard_normal((2, H)).astype(np.float32)).to("cuda", torch.bfloat16)
-    lg = torch.from_numpy(rng.standard_normal((2, E)).astype(np.float32)).cuda()
+    assert moe_path(blk, 1) == PATH_ONE_LAUNCH and moe_path(blk, 2) == PATH_FUSED
+    with two_kernels():
+        assert moe_path(blk, 1) == PATH_FUSED
+    x, lg = _xl(rng, 2, H, E)
     blk.fused(x, lg)
     if fill == "random":
         g = torch.Generator(device="cuda").manual_seed(5)
         blk._ws.copy_(torch.randint(0, 256, blk._ws.shape, dtype=torch.uint8, device="cuda", generator=g))
     else:
         blk._ws.fill_(0 if fill == "zeros" else 255)
+    blk.reset()
     for i in range(5):
-        x = torch.from_numpy(rng.standard_normal((2, H)).astype(np.float32)).to("cuda", torch.bfloat16)
-        lg = torch.from_numpy(rng.standard_normal((2, E)).astype(np.float32)).cuda()
+        x, lg = _xl(rng, 2, H, E)
         y1 = blk.fused(x[:1], lg[:1])
         y2 = blk.fused(x, lg)
+        with two_kernels():
+            yk = blk.fused(x[:1], lg[:1])
+        xz = x.clone()
+        xz[1] = 0
+        blk.fused(xz, lg)
+        y1b = blk.fused(x[:1], lg[:1])
         torch.cuda.synchronize()
-        assert np.array_equal(_bits(y1[0]), _bits(y2[0])), f"call {i}"
+        assert np.array_equal(_bits(y1[0]), _bits(y2[0])), f"call {i}: one launch vs T=2"
+        assert np.array_equal(_bits(y1), _bits(yk)), f"call {i}: one launch vs two kernels"
+        assert np.array_equal(_bits(y1b), _bits(y1)), f"call {i}: after a zero-row T=2 call"
         if i == 0:
             ref, _, _ = vo.moe_layer(x[:1].float().cpu().numpy(), lg[:1].cpu().numpy(),
                                      _spec(projs["gate"]), _spec(projs["up"]), _spec(projs["down"]),
                                      k, h_round=np.float16)
             assert_close(y1.float().cpu().numpy(), ref, what="one launch")
+    blk.status()
 
 
 def test_moe_one_launch_graph_replays():
@@ -338,16 +359,135 @@ def test_moe_one_launch_geometries(geom):
     power of two, I not a multiple of the gate/up row tile, unnormalised
     routing, d2 and d4 at 8 to 12 bits -- against the oracle and bit for bit
     against the two kernels (the same token inside a T = 2 call)."""
+    from vq_cases import PATH_ONE_LAUNCH, moe_path, two_kernels
     E, H, I, D, K, k, norm = geom
     print(f"moe one launch geometry {geom}", flush=True)
     rng = np.random.default_rng(sum(geom[:6]) + 100)
     blk, projs, sh, shv = _block(rng, E, H, I, D, K, k, norm=norm)
-    x = torch.from_numpy(rng.standard_normal((2, H)).astype(np.float32)).to("cuda", torch.bfloat16)
-    lg = torch.from_numpy(rng.standard_normal((2, E)).astype(np.float32)).cuda()
+    assert moe_path(blk, 1) == PATH_ONE_LAUNCH and moe_path(blk, 2) != PATH_ONE_LAUNCH
+    x, lg = _xl(rng, 2, H, E)
     y1 = blk.fused(x[:1], lg[:1])
     y2 = blk.fused(x, lg)
+    with two_kernels():
+        yk = blk.fused(x[:1], lg[:1])
     torch.cuda.synchronize()
     assert np.array_equal(_bits(y1[0]), _bits(y2[0]))
+    assert np.array_equal(_bits(y1), _bits(yk))
     ref, _, _ = vo.moe_layer(x[:1].float().cpu().numpy(), lg[:1].cpu().numpy(), _spec(projs["gate"]),
                              _spec(projs["up"]), _spec(projs["down"]), k, norm=norm, h_round=np.float16)
     assert_close(y1.float().cpu().numpy(), ref, what=f"one launch {geom}")
+
+
+def _share(ws_size, *blks):
+    ws = torch.zeros(ws_size, dtype=torch.uint8, device="cuda")
+    for b in blks:
+        b._ws = ws
+    return ws
+
+
+def test_moe_one_launch_geometries_share_a_workspace():
+    """Two one-launch geometries (different grids, word counts and row
+    tiles) alternate on ONE workspace: the call number and the hand-off words
+    sit at fixed header offsets and the tags name the word's header index, so
+    neither geometry's words can pass for the other's. Every call is bit for
+    bit the two-kernel form of the same token."""
+    from vq_cases import PATH_ONE_LAUNCH, moe_path, two_kernels
+    print("moe one launch: two geometries on one workspace", flush=True)
+    rng = np.random.default_rng(31)
+    ga = (256, 2048, 512, 4, 4096, 8)
+    gb = (64, 1024, 256, 4, 256, 6)
+    ba, pa, _, _ = _block(rng, *ga)
+    bb, pb, _, _ = _block(rng, *gb)
+    assert moe_path(ba, 1) == PATH_ONE_LAUNCH and moe_path(bb, 1) == PATH_ONE_LAUNCH
+    _share(1 << 20, ba, bb)
+    for i in range(4):
+        for blk, g in ((ba, ga), (bb, gb), (bb, gb), (ba, ga)):
+            E, H = g[0], g[1]
+            x, lg = _xl(rng, 1, H, E)
+            y = blk.fused(x, lg)
+            with two_kernels():
+                yk = blk.fused(x, lg)
+            torch.cuda.synchronize()
+            assert np.array_equal(_bits(y), _bits(yk)), f"round {i} geometry {g}"
+    ba.status()
+
+
+def test_moe_one_launch_gives_up_loudly():
+    """A one-launch wait that runs out never computes through: the
+    affected rows come out NaN and the header's error word is set (all
+    kernels still end normally -- the give-up is forced from the host with a
+    zero wait bound). Later one-launch calls on that workspace give NaN rows
+    until reset; vqk_moe_layer_status reports it; after reset the layer
+    gives the two-kernel form's bits again."""
+    from vq_cases import PATH_ONE_LAUNCH, l1_spins, moe_path, two_kernels
+    print("moe one launch: forced give-up", flush=True)
+    rng = np.random.default_rng(32)
+    E, H, I, D, K, k = 64, 1024, 256, 4, 256, 6
+    blk, projs, _, _ = _block(rng, E, H, I, D, K, k)
+    assert moe_path(blk, 1) == PATH_ONE_LAUNCH
+    x, lg = _xl(rng, 1, H, E)
+    y0 = blk.fused(x, lg)
+    blk.status()
+    with l1_spins(0):
+        yg = blk.fused(x, lg)
+        torch.cuda.synchronize()
+    assert bool(torch.isnan(yg.float()).all()), "every down workgroup gave up: all rows NaN"
+    with pytest.raises(RuntimeError, match="ran out"):
+        blk.status()
+    ys = blk.fused(x, lg)                       # sticky: still NaN, no wait
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(ys.float()).all())
+    with two_kernels():                         # the other paths never read the header
+        yk = blk.fused(x, lg)
+        torch.cuda.synchronize()
+    assert np.array_equal(_bits(yk), _bits(y0))
+    blk.reset()
+    yr = blk.fused(x, lg)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(yr), _bits(y0))
+    blk.status()
+
+
+_T1_LOGITS = ["ties", "all_equal", "ten_finite", "signed_zeros", "nan_mix", "few_valid"]
+
+
+@pytest.mark.parametrize("case", _T1_LOGITS)
+def test_moe_one_launch_special_logits(case):
+    """Batch-1 routing inside the one-launch layer (every workgroup routes the
+    token itself) on tied, all-equal, -inf, +-0 and NaN logits: the same
+    experts and weights as the oracle (ties to the lower id; NaN never chosen,
+    a selection left without a non-NaN logit is id -1 / weight 0), outputs
+    within the bar, and bit for bit the two-kernel form."""
+    from vq_cases import PATH_ONE_LAUNCH, moe_path, two_kernels
+    print(f"moe one launch special logits {case}", flush=True)
+    rng = np.random.default_rng(33)
+    E, H, I, D, K, k = 64, 1024, 256, 4, 256, 6
+    blk, projs, _, _ = _block(rng, E, H, I, D, K, k)
+    assert moe_path(blk, 1) == PATH_ONE_LAUNCH
+    lg = (np.round(rng.standard_normal(E) * 2) / 2).astype(np.float32)
+    if case == "all_equal":
+        lg[:] = 0.0
+    elif case == "ten_finite":
+        lg[10:] = -np.inf
+    elif case == "signed_zeros":
+        lg[:] = -1.0
+        lg[rng.permutation(E)[:12]] = 0.0
+        lg[rng.permutation(E)[:12]] = -0.0
+    elif case == "nan_mix":
+        lg[rng.permutation(E)[:20]] = np.nan
+    elif case == "few_valid":
+        lg[:] = np.nan
+        lg[[5, 40, 17, 33]] = [0.25, -0.5, 0.25, 1.0]
+    x = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float32)).to("cuda", torch.bfloat16)
+    lgt = torch.from_numpy(lg[None]).cuda()
+    y, ids, w = blk.fused(x, lgt, return_route=True)
+    with two_kernels():
+        yk = blk.fused(x, lgt)
+    torch.cuda.synchronize()
+    rids, rw = vo.route(lg[None], k)
+    assert np.array_equal(ids.cpu().numpy(), rids), (ids.cpu().numpy(), rids)
+    assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(_bits(y), _bits(yk))
+    ref, _, _ = vo.moe_layer(x.float().cpu().numpy(), lg[None], _spec(projs["gate"]),
+                             _spec(projs["up"]), _spec(projs["down"]), k, h_round=np.float16)
+    assert_close(y.float().cpu().numpy(), ref, what=f"special logits {case}")

@@ -275,6 +275,27 @@ def test_route_brute_force():
     assert np.array_equal(ids, ids2) and np.allclose(w, w2)
 
 
+def test_route_nan_logits_drop_out():
+    """NaN logits take no part: the routing equals the routing of the same
+    row with the NaN entries deleted (ids mapped back), in both weight modes;
+    with fewer than k non-NaN logits the last selections are (-1, 0)."""
+    rng = np.random.default_rng(13)
+    lg = rng.standard_normal((6, 48)).astype(np.float32)
+    lg[:, ::5] = np.nan
+    lg[2, :30] = -np.inf
+    keep = np.flatnonzero(~np.isnan(lg[0]))
+    for norm in (True, False):
+        ids, w = vo.route(lg, 8, norm)
+        sub_ids, sub_w = vo.route(lg[:, keep], 8, norm)
+        assert np.array_equal(ids, keep[sub_ids])
+        assert np.allclose(w, sub_w, rtol=0, atol=1e-15)
+    few = np.full((1, 16), np.nan, np.float32)
+    few[0, [3, 9, 4]] = [0.5, -1.0, 0.5]
+    ids, w = vo.route(few, 5)
+    assert list(ids[0]) == [3, 4, 9, -1, -1]
+    assert np.allclose(w[0, 3:], 0.0) and np.isclose(w[0].sum(), 1.0)
+
+
 def _proj(rng, E, OUT, IN, d=4, K=64, G=64):
     return {"codes": rng.integers(0, K, (E, OUT, IN // d)).astype(np.uint16),
             "codebook": (rng.standard_normal((K, d)) * 0.05).astype(np.float16),

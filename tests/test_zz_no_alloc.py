@@ -81,7 +81,7 @@ def test_noalloc_matches_workspace_entry(case):
         need = ctypes.c_size_t()
         L.check(L.lib().vqk_moe_decode_layer_workspace(ctypes.byref(d), T, ctypes.byref(need)))
         assert need.value <= L.VQK_NOALLOC_SCRATCH_BYTES
-        ws = torch.empty(max(1, need.value), dtype=torch.uint8, device="cuda")
+        ws = torch.zeros(max(1, need.value), dtype=torch.uint8, device="cuda")
         y0, i0, w0 = _call(L, Tt, d, x, lg, T, k, ws)
         y1, i1, w1 = _call(L, Tt, d, x, lg, T, k, None)
         torch.cuda.synchronize()
@@ -94,6 +94,40 @@ def test_noalloc_matches_workspace_entry(case):
                                    k, shared=shared_spec, shared_gate=sgv, h_round=np.float16)
         assert np.array_equal(i1.cpu().numpy(), rid)
         assert_close(y1.float().cpu().numpy(), ref, what=f"noalloc T={T}")
+
+
+def test_noalloc_one_launch_geometries_alternate():
+    """The scratch array is shared by every layer: two one-launch geometries
+    alternating through vqk_moe_decode_layer_noalloc (the call number and the
+    hand-off words at fixed header offsets, tags naming the word's header
+    index) give, call after call, the bits of the two-kernel form through a
+    caller workspace; the scratch header reports no error afterwards."""
+    from vqlab_amd import _lib as L, _torch as Tt
+    from vq_cases import PATH_ONE_LAUNCH, moe_path, two_kernels
+    print("noalloc: two one-launch geometries alternate", flush=True)
+    rng = np.random.default_rng(77)
+    geoms = [(256, 2048, 512, 4, 4096, 8), (64, 1024, 256, 4, 256, 6)]
+    blks = []
+    for g in geoms:
+        blk, *_ = _block(rng, *g, False)
+        assert moe_path(blk, 1) == PATH_ONE_LAUNCH
+        keep = []
+        blks.append((blk, blk._fused_desc(keep), keep, g))
+    for rnd in range(3):
+        for blk, d, _, g in blks + blks[::-1]:
+            E, H, k = g[0], g[1], g[5]
+            x = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float32)).to("cuda", torch.bfloat16)
+            lg = torch.from_numpy(rng.standard_normal((1, E)).astype(np.float32)).cuda()
+            y1, i1, w1 = _call(L, Tt, d, x, lg, 1, k, None)
+            need = ctypes.c_size_t()
+            L.check(L.lib().vqk_moe_decode_layer_workspace(ctypes.byref(d), 1, ctypes.byref(need)))
+            ws = torch.zeros(need.value, dtype=torch.uint8, device="cuda")
+            with two_kernels():
+                y0, i0, w0 = _call(L, Tt, d, x, lg, 1, k, ws)
+            torch.cuda.synchronize()
+            assert torch.equal(i1, i0) and torch.equal(w1, w0), f"routing round {rnd} {g}"
+            assert torch.equal(y1.view(torch.int16), y0.view(torch.int16)), f"outputs round {rnd} {g}"
+    L.check(L.lib().vqk_moe_layer_status(None, Tt.stream()), "noalloc scratch status")
 
 
 def test_noalloc_refuses_oversized_call():

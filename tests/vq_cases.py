@@ -73,3 +73,71 @@ def assert_rel_max(y, ref, tol=2e-2, what=""):
     assert y.shape == ref.shape, (y.shape, ref.shape)
     rel = float(np.abs(y - ref).max() / max(float(np.abs(ref).max()), 1e-6)) if y.size else 0.0
     assert rel < tol, f"{what}: max-abs error {rel:.3e} of max |ref| (bar {tol})"
+
+
+# ---------------------------------------------------------------- test hooks
+_HOOKS = None
+
+
+def hooks():
+    """libvqk's test hooks (exported, deliberately not in include/vqk.h):
+    vqk__test_l1_spins(n) -> previous bound of the one-launch layer's waits;
+    vqk__test_l1_mode(m) -> previous mode (0 one launch where it applies,
+    1 never); vqk__test_moe_path(desc*, T, int32*) -> status, the path a layer
+    call takes (0 two fused kernels, 1 sliced GEMVs, 2 grouped, 3 one launch)."""
+    global _HOOKS
+    if _HOOKS is None:
+        import ctypes
+        from vqlab_amd import _lib as L
+        lib = L.lib()
+        for name, res, args in (("vqk__test_l1_spins", ctypes.c_int, [ctypes.c_int]),
+                                ("vqk__test_l1_mode", ctypes.c_int, [ctypes.c_int]),
+                                ("vqk__test_moe_path", ctypes.c_int32,
+                                 [ctypes.POINTER(L.VQKMoeDesc), ctypes.c_int64,
+                                  ctypes.POINTER(ctypes.c_int32)])):
+            f = getattr(lib, name)
+            f.restype, f.argtypes = res, args
+        _HOOKS = lib
+    return _HOOKS
+
+
+PATH_FUSED, PATH_SLICED, PATH_GROUPED, PATH_ONE_LAUNCH = range(4)
+
+
+def moe_path(blk, T):
+    """The path vqk_moe_decode_layer takes for block `blk` at T tokens."""
+    import ctypes
+    from vqlab_amd import _lib as L
+    keep = []
+    d = blk._fused_desc(keep)
+    p = ctypes.c_int32(-1)
+    L.check(hooks().vqk__test_moe_path(ctypes.byref(d), int(T), ctypes.byref(p)))
+    return p.value
+
+
+class two_kernels:
+    """Context: every layer call planned inside takes the two-kernel form
+    where it would have taken one launch."""
+
+    def __enter__(self):
+        self._prev = hooks().vqk__test_l1_mode(1)
+        return self
+
+    def __exit__(self, *exc):
+        hooks().vqk__test_l1_mode(self._prev)
+        return False
+
+
+class l1_spins:
+    """Context: the one-launch layer's waits give up after n rounds."""
+
+    def __init__(self, n):
+        self.n = n
+
+    def __enter__(self):
+        self._prev = hooks().vqk__test_l1_spins(self.n)
+        return self
+
+    def __exit__(self, *exc):
+        hooks().vqk__test_l1_spins(self._prev)
+        return False

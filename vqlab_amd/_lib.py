@@ -17,6 +17,7 @@ LIB_PATH = pathlib.Path(os.environ.get("VQK_LIBRARY") or
 VQK_OK, VQK_ENOTIMPL, VQK_EINVAL, VQK_ESHARDED, VQK_EDEVICE, VQK_ENOSPACE = range(6)
 VQK_F16, VQK_BF16, VQK_F32, VQK_U8, VQK_U16, VQK_U32, VQK_I32, VQK_I64 = range(8)
 VQK_NOALLOC_SCRATCH_BYTES = 32 << 20     # include/vqk.h
+VQK_MOE_HEADER_BYTES = 49152             # include/vqk.h: zero before a layer workspace's first call
 VQK_VIA_F16 = 0x100                      # output type flag: round through fp16 first
 
 c_i32, c_i64, c_p, c_sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
@@ -39,7 +40,8 @@ class VQKMoeDesc(ctypes.Structure):
 
 class VQKOptions(ctypes.Structure):
     _fields_ = [("fused_max_n", c_i64), ("dense_fused_max_n", c_i64),
-                ("decode_bf16io", c_i32), ("prefill_bf16io", c_i32)]
+                ("decode_bf16io", c_i32), ("prefill_bf16io", c_i32),
+                ("crowded_grouped", c_i32)]
 
 
 # name -> (restype, argtypes), one entry per function of include/vqk.h
@@ -72,6 +74,8 @@ SIGNATURES = {
                                      c_i32, c_p, c_p, c_p, c_sz, c_p]),
     "vqk_moe_decode_layer_noalloc": (c_i32, [ctypes.POINTER(VQKMoeDesc), c_p, c_i32, c_i64, c_p,
                                              c_p, c_i32, c_p, c_p, c_p]),
+    "vqk_moe_layer_status": (c_i32, [c_p, c_p]),
+    "vqk_moe_layer_reset": (c_i32, [c_p, c_p]),
     "vqk_embed_gather": (c_i32, [ctypes.POINTER(VQKWeights), c_p, c_i32, c_i64, c_p, c_i32,
                                  c_p]),
     "vqk_dense_fits": (c_i32, [c_i64, c_i64, c_i32, c_i32]),

@@ -21,6 +21,7 @@ vqk_options resolved(const vqk_options *o) {
         if (o->dense_fused_max_n > 0) r.dense_fused_max_n = o->dense_fused_max_n;
         r.decode_bf16io = o->decode_bf16io ? 1 : 0;
         r.prefill_bf16io = o->prefill_bf16io ? 1 : 0;
+        r.crowded_grouped = o->crowded_grouped ? 1 : 0;
     }
     return r;
 }
@@ -33,9 +34,12 @@ int64_t env_i64(const char *name, int64_t dflt) {
     return (end && *end == 0) ? int64_t(n) : dflt;
 }
 
-// The grouped GEMM for N pairs of module w (else the fused GEMV).
+// The grouped GEMM for N pairs of module w (else the fused GEMV). The
+// crowded rule (N >= 4 and N >= 2E: the GEMV would read each expert's rows
+// once per pair) has no counterpart in the reference's dispatch
+// (vq_switch.py:5341-5350); crowded_grouped = 0 turns it off.
 bool switch_grouped(const vqk_weights *w, const Geom &g, int64_t N, const vqk_options &o) {
-    const bool crowded = N >= 4 && N >= 2 * g.E;
+    const bool crowded = o.crowded_grouped && N >= 4 && N >= 2 * g.E;
     if (N <= o.fused_max_n && !crowded) return false;
     return vqk_gemmseg_fits(g.D, g.K, g.G, w->pack_bits, g.IN) != 0;
 }
@@ -54,6 +58,7 @@ void vqk_options_default(vqk_options *o) {
     o->dense_fused_max_n = kDenseFusedMaxN;
     o->decode_bf16io = 0;
     o->prefill_bf16io = 0;
+    o->crowded_grouped = 1;
 }
 
 void vqk_options_from_env(vqk_options *o) {
@@ -88,8 +93,11 @@ int vqk_switch_apply(const vqk_weights *w, const void *x, int32_t x_type, int64_
     const vqk_options o = resolved(opt);
     const bool grouped = switch_grouped(w, g, N, o);
     // the reference's default: fused (and grouped) outputs come back as fp16
-    // and are cast to x's dtype by the caller (vq_switch.py:5306-5308, 5423)
-    const bool via = grouped ? !o.prefill_bf16io : !o.decode_bf16io;
+    // and are cast to x's dtype by the caller (vq_switch.py:5306-5308, 5423);
+    // the bf16-I/O flags keep one rounding only for bf16 x (_keep_bf16 =
+    // flag and in_dtype == bf16, vq_switch.py:5306, 5369)
+    const bool keep = (grouped ? o.prefill_bf16io : o.decode_bf16io) && x_type == VQK_BF16;
+    const bool via = !keep;
     const int32_t yt = via ? (y_type | VQK_VIA_F16) : y_type;
     if (grouped)
         return vqk_grouped_gemm(w, x, x_type, T, eidx, N, xkrep, y, yt, workspace, ws_bytes, stream);

@@ -21,6 +21,7 @@
 //   k_moe_layer1 both in one grid: the k_moe_up workgroups, then down
 //               workgroups that route for themselves, fetch their weights and
 //               table entries early and take the SwiGLU rows as tagged words.
+#include <atomic>
 #include <mutex>
 
 #include "vqk_gemv.h"
@@ -73,11 +74,13 @@ struct MoeParams {
     float *gbuf, *ubuf;  // split gate/up phase: workspace [T, P, I] fp32 each, else NULL
     int32_t *ids_out;    // optional user copies
     float *wts_out;
-    // one-launch layer (k_moe_layer1): call number, per-workgroup stamps and
-    // tagged SwiGLU words in the workspace; gate/up workgroups and their row
-    // tiles per pair, down row tiles per token
-    uint64_t *l1_epoch, *l1_stamp, *l1_hw;
+    // one-launch layer (k_moe_layer1): call number, error word, per-workgroup
+    // stamps and tagged SwiGLU words in the workspace header; gate/up
+    // workgroups and their row tiles per pair, down row tiles per token; the
+    // bound of every wait
+    uint64_t *l1_epoch, *l1_err, *l1_stamp, *l1_hw;
     int32_t l1_g1, l1_gx1, l1_gx2;
+    int32_t l1_spins;
 };
 
 // ------------------------------------------------------------ routing
@@ -439,24 +442,48 @@ struct RouteLds {
 };
 
 // ------------------------------------------------ one-launch layer hand-off
-// The SwiGLU rows of the one-launch layer travel as 64-bit words: two fp16
-// values below a 32-bit tag of (call number n, word index w). For a fixed w
-// the tag is one-to-one in n (an odd multiple of n, then an invertible
-// xorshift-multiply mix), so a word left by any earlier call never carries
-// call n's tag; one 64-bit load both checks a word and delivers it. The
-// offset keeps zeroed or all-ones memory from passing in the first calls of
-// a workspace (without it tag(0, 0) == 0): for n < 4 the words whose tag is
-// 0 or 0xffffffff all have indices above 2^30.
-constexpr int kL1Spins = 1 << 16;        // bound of every poll loop (~45 ms)
+// Every layer workspace starts with a header at fixed offsets, the same for
+// every geometry, path and T, that only one-launch calls write: the call
+// number n, a sticky error word, one stamp per workgroup and the hand-off
+// words. The SwiGLU rows travel as 64-bit words: two fp16 values below a
+// 32-bit tag of (n, w), w the word's index in the header's word region. The
+// tag has its top bit set, and its low 31 bits are one-to-one in n mod 2^31
+// for a fixed w (an odd multiple of n, then an invertible xorshift-multiply
+// mix of 31-bit values). So a zeroed word (a header that starts zeroed) never
+// passes, and a word that any earlier one-launch call left at index w -- of
+// this geometry or another, on this workspace -- carries an earlier call
+// number and never passes, unless it was left exactly a multiple of 2^31
+// calls ago and no call since wrote index w. One 64-bit load both checks a
+// word and delivers it.
+// Every wait is bounded by MoeParams::l1_spins rounds (kL1Spins, ~45 ms, by
+// default). A word that does not arrive in time enters the down dot products
+// as NaN -- every output row that would have used it comes out NaN -- and
+// sets kL1ErrPoll in the error word; workgroup 0, if a stamp does not
+// arrive, sets kL1ErrStamp and leaves the call number as it is. Once the
+// error word is set, the down workgroups of every later call on that
+// workspace take every word as missing without waiting (NaN rows), until
+// the header is zeroed again (vqk_moe_layer_reset); vqk_moe_layer_status
+// reports it.
+constexpr int kL1Spins = 1 << 16;        // default bound of every wait (~45 ms)
 constexpr int kL1Slots = 4;              // logits per lane of its routing: E <= 256
+constexpr uint64_t kL1ErrPoll = 1, kL1ErrStamp = 2;
+// header layout (bytes): call number, error word, stamps, words
+constexpr size_t kHdrEpoch = 0, kHdrError = 8, kHdrStamps = 256;
+constexpr int kL1MaxWg = 1024;           // workgroups of a one-launch grid
+constexpr int kL1MaxWords = 4096;        // hand-off words: P * I / 2 (d4: P * NB2 <= 64 -> 4096)
+constexpr size_t kHdrWords = kHdrStamps + 8 * size_t(kL1MaxWg);
+constexpr size_t kHdrBytes = VQK_MOE_HEADER_BYTES;
+static_assert(kHdrWords % 256 == 0 && kHdrWords + 8 * size_t(kL1MaxWords) <= kHdrBytes,
+              "the one-launch header must hold its stamps and words");
 __device__ __forceinline__ uint32_t l1_tag(uint32_t n, uint32_t w) {
-    uint32_t v = n * 0x9E3779B1u + w * 0x85EBCA6Bu + 0x6A09E667u;
+    constexpr uint32_t M = 0x7fffffffu;
+    uint32_t v = (n * 0x9E3779B1u + w * 0x85EBCA6Bu + 0x6A09E667u) & M;
     v ^= v >> 16;
-    v *= 0x7FEB352Du;
+    v = (v * 0x7FEB352Du) & M;
     v ^= v >> 15;
-    v *= 0x846CA68Bu;
+    v = (v * 0x846CA68Bu) & M;
     v ^= v >> 16;
-    return v;
+    return v | 0x80000000u;
 }
 // A workgroup's stamp once it has read call number n.
 __device__ __forceinline__ uint64_t l1_stamp(uint32_t n) { return (uint64_t(~n) << 32) | n; }
@@ -975,20 +1002,19 @@ __global__ void __launch_bounds__(moe_waves_down(W) * kWave) k_moe_down(const Mo
 // SwiGLU words of its token and finishes k_moe_down's arithmetic (same order,
 // same bits) with the dot products. So the layer costs one kernel boundary,
 // and the down weights' latency and table gathers overlap the gate/up phase
-// instead of following the routing read of a second launch. A poll that ran
-// out of kL1Spins (a gate/up workgroup held up for ~45 ms) would go on with
-// the words it has.
-// The call number n lives in the workspace: every workgroup reads it at its
-// start and then writes its stamp; workgroup 0, once every stamp shows n,
-// writes n + 1 for the next call, which starts after this launch ends. Any
-// initial workspace contents work (a foreign word passes a tag check with
-// probability 2^-32). Gate/up workgroups never wait on down workgroups and
-// are dispatched first (lower ids), so the polls always end; every poll loop
-// is bounded by kL1Spins all the same.
+// instead of following the routing read of a second launch.
+// The call number n lives in the workspace header: every workgroup reads it
+// at its start and then writes its stamp; workgroup 0, once every stamp shows
+// n, writes n + 1 for the next call, which starts after this launch ends.
+// Gate/up workgroups never wait on anything and are dispatched first (lower
+// ids); the down workgroups and workgroup 0 wait on them, each wait bounded
+// (l1_spins). A wait that gives up is reported, never computed through: the
+// missing words enter as NaN and the header's error word is set.
 struct L1Lds {
     RouteLds rl;
     int ids[kMaxTopK];
     float wts[kMaxTopK];
+    uint64_t call_bad;   // down workgroups: call number | (error word set at the start) << 32
 };
 // Waves of a down workgroup that decode rows (all of them stage, route and
 // poll): eight, i.e. 16 rows per workgroup and 128 down workgroups at
@@ -1009,7 +1035,7 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
     // the last wave routes (the gate/up workgroup beside it on the CU routes
     // on its wave 0, and two routing waves on one SIMD slow both: 9.99 ->
     // 9.83 us per config-2 layer); the others stage the down table
-    uint64_t ev = 0;
+    uint64_t ev = 0, er = 0;
     if (wave == NT / kWave - 1) {
         int e_pair, my_idx = -1;
         float my_w = 0.f;
@@ -1020,12 +1046,15 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
             ll.wts[lane] = my_w;
         }
     } else {
-        if (tid == 0) ev = l1_load(p.l1_epoch);
+        if (tid == 0) {
+            ev = l1_load(p.l1_epoch);
+            er = l1_load(p.l1_err);
+        }
         stage_codebook_fixed<D, CBN, NT - kWave, 0>(p.down.codebook, p.down.K, reinterpret_cast<h2 *>(smem));
     }
     wait_vmem();
     if (tid == 0) {
-        ll.rl.call = uint32_t(ev);
+        ll.call_bad = (uint64_t(er != 0) << 32) | uint32_t(ev);
         l1_store(p.l1_stamp + p.l1_g1 + cbi, l1_stamp(uint32_t(ev)));
     }
     __syncthreads();
@@ -1063,8 +1092,16 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
         }
     }
     // the token's SwiGLU words: each thread polls up to four at a time until
-    // their tags are the call's, then writes their halves into LDS
-    const uint32_t n = ll.rl.call;
+    // their tags are the call's, then writes their halves into LDS. A word
+    // still missing once l1_spins rounds have passed (or at once, after an
+    // earlier call's error) enters as two fp16 NaNs, so every row whose dot
+    // products would have used it comes out NaN, and its thread sets the
+    // error word. (A workgroup-wide give-up flag in LDS, set before the
+    // barrier, cost 0.15 us per config-2 layer.)
+    const uint64_t cb = ll.call_bad;               // one LDS read ahead of the polls
+    const uint32_t n = uint32_t(cb);
+    const bool skip = (cb >> 32) != 0;
+    const int bound = skip ? 0 : p.l1_spins;
     const int nwd = p.P * p.I / 2;
     const int64_t w0 = int64_t(t) * nwd;
     for (int g0 = tid; g0 < nwd; g0 += 4 * NT) {
@@ -1073,7 +1110,7 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             if (g0 + u * NT < nwd) need |= 1u << u;
-        for (int spin = 0; need && spin < kL1Spins; ++spin) {
+        for (int spin = 0; need && spin < bound; ++spin) {
 #pragma unroll
             for (int u = 0; u < 4; ++u)
                 if ((need >> u) & 1u) v[u] = l1_load(p.l1_hw + w0 + g0 + u * NT);
@@ -1089,9 +1126,12 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
             if (g < nwd) {
                 const int jj = (2 * g) / p.I, col = (2 * g) % p.I;
                 const int b = jj * p.NB2 + col / XH;
-                *reinterpret_cast<uint32_t *>(xs + b * XS + col % XH) = uint32_t(v[u]);
+                *reinterpret_cast<uint32_t *>(xs + b * XS + col % XH) =
+                    ((need >> u) & 1u) ? 0x7E007E00u : uint32_t(v[u]);
             }
         }
+        if (need && !skip)
+            __hip_atomic_fetch_or(p.l1_err, kL1ErrPoll, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (dec) {
@@ -1120,7 +1160,8 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
         }
         acc = group_sum(acc, dl.lpr);
         const int r = bx * p.rows_per_wg2 + wave * dl.rpw + dl.sub;
-        if (dl.v == dl.lpr - 1 && r < p.H) store_act(p.y, p.y_type, int64_t(t) * p.H + r, acc);
+        if (dl.v == dl.lpr - 1 && r < p.H)
+            store_act(p.y, p.y_type, int64_t(t) * p.H + r, acc);
     }
 }
 
@@ -1134,13 +1175,26 @@ __global__ void __launch_bounds__(2 * kThreads, 4) k_moe_layer1(const MoeParams 
         up_fused<D, BITS, GPB, true>(p, smem, ll.rl, bx, pair);
         if (b == 0) {
             // every workgroup has read the call number once its stamp shows
-            // it: advance it for the next call
+            // it: advance it for the next call (or, if a stamp never came,
+            // report that and leave it)
             const uint32_t n = ll.rl.call;
             const int nwg = p.l1_g1 + p.l1_gx2 * p.T;
-            for (int i = int(threadIdx.x); i < nwg; i += 2 * kThreads)
-                for (int spin = 0; spin < kL1Spins && l1_load(p.l1_stamp + i) != l1_stamp(n); ++spin) {}
-            __syncthreads();
-            if (threadIdx.x == 0) l1_store(p.l1_epoch, uint64_t(n + 1u));
+            int miss = 0;
+            for (int i = int(threadIdx.x); i < nwg; i += 2 * kThreads) {
+                int spin = 0;
+                while (l1_load(p.l1_stamp + i) != l1_stamp(n))
+                    if (++spin >= p.l1_spins) {
+                        miss = 1;
+                        break;
+                    }
+            }
+            const bool lost = __syncthreads_or(miss) != 0;
+            if (threadIdx.x == 0) {
+                if (lost)
+                    __hip_atomic_fetch_or(p.l1_err, kL1ErrStamp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else
+                    l1_store(p.l1_epoch, uint64_t(n + 1u));
+            }
         }
     } else {
         l1_down<D, BITS, GPB>(p, smem, ll, b - p.l1_g1);
@@ -1188,12 +1242,14 @@ __global__ void __launch_bounds__(256) k_moe_combine(const MoeParams p, const fl
 // ------------------------------------------------------------ host side
 static size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
+// Offsets in a layer workspace. Every layout starts with the one-launch
+// header (kHdrBytes: call number, error word, stamps, hand-off words), so no
+// other path, geometry or T ever writes into it.
 struct MoeLayout {
     size_t ids, wts, sg, h, total;
     size_t g, u, sgg, sgu, yd, ysh;      // composed paths (sliced-codebook GEMV, grouped GEMM)
     size_t sort;                         // grouped path: pair order and tile records
     size_t gs, us;                       // fused path, split K1: fp32 gate / up rows
-    size_t l1e, l1s, l1w;                // one launch: call number, stamps, tagged SwiGLU words
 };
 
 // Paths of the layer: the two fused decode kernels, the sliced-codebook GEMV
@@ -1204,13 +1260,12 @@ enum MoePath { kMoeFused = 0, kMoeBig = 1, kMoeGrouped = 2 };
 static MoeLayout moe_layout(int64_t T, int k, int P, int64_t I, int64_t H, int path, int64_t E,
                             bool split) {
     MoeLayout L;
-    L.ids = 0;
+    L.ids = kHdrBytes;
     L.wts = align_up(L.ids + sizeof(int32_t) * T * k);
     L.sg = align_up(L.wts + sizeof(float) * T * k);
     L.h = align_up(L.sg + sizeof(float) * T);
     L.total = align_up(L.h + (path == kMoeFused && !split ? 2 * size_t(T) * P * I : 0));
     L.g = L.u = L.sgg = L.sgu = L.yd = L.ysh = L.sort = L.gs = L.us = 0;
-    L.l1e = L.l1s = L.l1w = 0;
     if (path == kMoeFused && split) {
         L.gs = L.total;
         L.us = align_up(L.gs + 4 * size_t(T) * P * I);
@@ -1262,6 +1317,12 @@ struct MoePlan {
     size_t smem_l1;
     int l1_nwg;               // its workgroups
 };
+
+// Test hooks (vqk__test_*, not part of include/vqk.h): the bound of the
+// one-launch layer's waits, and a switch that keeps every call on the other
+// paths, so tests can force a give-up and compare the two forms.
+static std::atomic<int> g_l1_spins{kL1Spins};
+static std::atomic<int> g_l1_mode{0};        // 0 = one launch where it applies, 1 = never
 
 // Widths of the one-launch layer's instances: tables of 256 to 4096 entries
 // at d 2 and 4, with their scale-group blocking.
@@ -1420,21 +1481,23 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
         return set_error(VQK_ENOTIMPL, "fused layer: LDS need %zu / %zu B exceeds 160 KB",
                          pl->smem1, pl->smem2);
     pl->lay = moe_layout(T, k, P, gg.OUT, gg.IN, pl->path, E, pl->split);
-    // One launch: gate/up and down workgroups resident together, two per CU
-    // (LDS and 128 VGPRs each), tables in LDS, no shared expert, one format.
+    // One launch: batch 1, gate/up and down workgroups resident together, two
+    // per CU (LDS and 128 VGPRs each), tables in LDS, no shared expert, one
+    // format, the stamps and words within the header.
     pl->l1 = false;
     pl->smem_l1 = 0;
     pl->l1_nwg = 0;
-    if (pl->path == kMoeFused && !pl->split && full1 && full2 && !shared && gg.D == gd.D &&
-        gg.BITS == gd.BITS && gg.gpb == gd.gpb && l1_instance(gg.D, gg.BITS, gg.gpb) && E <= kL1Slots * kWave &&
-        pl->grid1.z == 1 && gg.OUT % 2 == 0 && p.rows_per_wg1 % 2 == 0) {
+    if (T == 1 && g_l1_mode.load() == 0 && pl->path == kMoeFused && !pl->split && full1 && full2 && !shared &&
+        gg.D == gd.D && gg.BITS == gd.BITS && gg.gpb == gd.gpb && l1_instance(gg.D, gg.BITS, gg.gpb) &&
+        E <= kL1Slots * kWave && pl->grid1.z == 1 && gg.OUT % 2 == 0 && p.rows_per_wg1 % 2 == 0 &&
+        int64_t(P) * gg.OUT / 2 <= kL1MaxWords) {
         const int rpw2 = kWave >> p.lpr2_log2;
         const int64_t rows2 = int64_t(kL1DownWaves) * rpw2;
         const int64_t gx2 = (gd.OUT + rows2 - 1) / rows2;
         const int64_t g1 = int64_t(pl->grid1.x) * pl->grid1.y;
         const int64_t nwg = g1 + gx2 * T;
         const size_t sm = std::max(pl->smem1, cb2 + xs2);
-        if (nwg <= 2 * ncu && 2 * (sm + sizeof(L1Lds) + 256) <= 160 * 1024) {
+        if (nwg <= std::min<int64_t>(2 * ncu, kL1MaxWg) && 2 * (sm + sizeof(L1Lds) + 256) <= 160 * 1024) {
             pl->l1 = true;
             pl->smem_l1 = sm;
             pl->l1_nwg = int(nwg);
@@ -1443,11 +1506,7 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
             p.l1_gx2 = int32_t(gx2);
             p.rows_per_wg2 = int32_t(rows2);
             p.steps2 = 1;
-            MoeLayout &L = pl->lay;
-            L.l1e = L.total;
-            L.l1s = align_up(L.l1e + sizeof(uint64_t));
-            L.l1w = align_up(L.l1s + sizeof(uint64_t) * size_t(nwg));
-            L.total = align_up(L.l1w + sizeof(uint64_t) * size_t(T) * P * size_t(gg.OUT) / 2);
+            p.l1_spins = g_l1_spins.load();
         }
     }
     return VQK_OK;
@@ -1690,11 +1749,72 @@ static int scratch_of_current_device(void *stream, void **out) {
     return VQK_OK;
 }
 
+// Zeroes a workspace header (a fill kernel, not a memset: the call may be
+// captured into a graph).
+__global__ void __launch_bounds__(256) k_zero_header(u32x4 *h, int n) {
+    const int i = int(blockIdx.x) * 256 + int(threadIdx.x);
+    if (i < n) h[i] = u32x4{0, 0, 0, 0};
+}
+
 }  // namespace vqk
 
 using namespace vqk;
 
 extern "C" {
+
+// ---- test hooks: exported, deliberately not in include/vqk.h -------------
+// vqk__test_l1_spins: bound of the one-launch layer's waits for calls planned
+// after it (n >= 0; returns the previous bound). vqk__test_l1_mode: 0 = one
+// launch where it applies (default), 1 = never. vqk__test_moe_path: the path
+// a call would take: 0 two fused kernels, 1 sliced-codebook GEMVs, 2 grouped
+// GEMMs, 3 one launch.
+int vqk__test_l1_spins(int n) { return g_l1_spins.exchange(n < 0 ? kL1Spins : n); }
+int vqk__test_l1_mode(int m) { return g_l1_mode.exchange(m); }
+int vqk__test_moe_path(const vqk_moe_desc *m, int64_t T, int32_t *path) {
+    MoePlan pl;
+    const int rc = moe_plan(m, T, &pl);
+    if (rc) return rc;
+    if (!path) return set_error(VQK_EINVAL, "path is NULL");
+    *path = pl.l1 ? 3 : pl.path;
+    return VQK_OK;
+}
+
+int vqk_moe_layer_status(const void *workspace, void *stream) {
+    const void *ws = workspace;
+    int rc;
+    if (!ws) {
+        void *s = nullptr;
+        if ((rc = scratch_of_current_device(stream, &s))) return rc;
+        ws = s;
+    }
+    if ((rc = hip_status(hipStreamSynchronize(hipStream_t(stream)), "hipStreamSynchronize"))) return rc;
+    uint64_t err = 0;
+    if ((rc = hip_status(hipMemcpy(&err, static_cast<const uint8_t *>(ws) + kHdrError, sizeof err,
+                                   hipMemcpyDeviceToHost),
+                         "reading the layer workspace's error word")))
+        return rc;
+    if (err)
+        return set_error(VQK_EDEVICE,
+                         "one-launch MoE layer: %s%s; those calls and every later one-launch call on "
+                         "this workspace wrote NaN rows (vqk_moe_layer_reset clears it)",
+                         (err & kL1ErrPoll) ? "a down workgroup's wait for the SwiGLU words ran out" : "",
+                         (err & kL1ErrStamp) ? ((err & kL1ErrPoll) ? ", and a workgroup never started in time"
+                                                                   : "a workgroup never started in time")
+                                             : "");
+    return VQK_OK;
+}
+
+int vqk_moe_layer_reset(void *workspace, void *stream) {
+    void *ws = workspace;
+    int rc;
+    if (!ws && (rc = scratch_of_current_device(stream, &ws))) return rc;
+    if (reinterpret_cast<uintptr_t>(ws) & 15)
+        return set_error(VQK_EINVAL, "workspace must be 16-byte aligned");
+    const int n = int(kHdrBytes / 16);
+    hipLaunchKernelGGL(k_zero_header, dim3(unsigned((n + 255) / 256)), dim3(256), 0, hipStream_t(stream),
+                       static_cast<u32x4 *>(ws), n);
+    return hip_status(hipGetLastError(), "header reset launch");
+}
 
 int vqk_moe_decode_layer_workspace(const vqk_moe_desc *m, int64_t T, size_t *bytes) {
     if (!bytes) return set_error(VQK_EINVAL, "bytes is NULL");
@@ -1741,9 +1861,10 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, i
     }
     if (pl.path == kMoeBig) return launch_moe_big(m, pl, ws, st);
     if (pl.l1) {
-        p.l1_epoch = reinterpret_cast<uint64_t *>(ws + pl.lay.l1e);
-        p.l1_stamp = reinterpret_cast<uint64_t *>(ws + pl.lay.l1s);
-        p.l1_hw = reinterpret_cast<uint64_t *>(ws + pl.lay.l1w);
+        p.l1_epoch = reinterpret_cast<uint64_t *>(ws + kHdrEpoch);
+        p.l1_err = reinterpret_cast<uint64_t *>(ws + kHdrError);
+        p.l1_stamp = reinterpret_cast<uint64_t *>(ws + kHdrStamps);
+        p.l1_hw = reinterpret_cast<uint64_t *>(ws + kHdrWords);
         return launch_moe_layer1(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, dim3(unsigned(pl.l1_nwg)), pl.smem_l1, st);
     }
     rc = split ? launch_moe_up_split(p, pl.g1.D, pl.g1.BITS, pl.g1.gpb, pl.wide1, pl.grid1, pl.smem1, st)

@@ -11,8 +11,8 @@ bench/decode_ladder.py:107-119 and tests/test_qwen3_5_parity.py:180-205:
         + sigmoid(shared_expert_gate(x)) * shared_expert(x)
 
 VQSparseMoeBlock runs that whole block as one fused decode layer
-(vqk_moe_decode_layer: routing on device, two kernels, no host sync) when
-the shapes fit, and otherwise composes the per-projection kernels
+(vqk_moe_decode_layer: routing on device, one or two kernels, no host sync)
+when the shapes fit, and otherwise composes the per-projection kernels
 (VQSwitchLinear) with torch's routing ops on the same device.
 """
 from __future__ import annotations
@@ -122,7 +122,9 @@ class VQSparseMoeBlock(torch.nn.Module):
         L.check(L.lib().vqk_moe_decode_layer_workspace(ctypes.byref(d), Tt, ctypes.byref(ws)),
                 "moe layer")
         if self._ws is None or self._ws.numel() < ws.value or self._ws.device != x.device:
-            self._ws = torch.empty(max(ws.value, 1), dtype=torch.uint8, device=x.device)
+            # the header (call number, error word, hand-off words) starts zeroed
+            self._ws = torch.zeros(max(ws.value, L.VQK_MOE_HEADER_BYTES), dtype=torch.uint8,
+                                   device=x.device)
         y = torch.empty((Tt, x.shape[1]), dtype=x.dtype, device=x.device)
         ids = torch.empty((Tt, self.top_k), dtype=torch.int32, device=x.device) if return_route else None
         w = torch.empty((Tt, self.top_k), dtype=torch.float32, device=x.device) if return_route else None
@@ -131,6 +133,20 @@ class VQSparseMoeBlock(torch.nn.Module):
                                              T.ptr(w), T.ptr(self._ws), ws.value,
                                              T.stream(x.device)), "moe layer")
         return (y, ids, w) if return_route else y
+
+    def status(self):
+        """Raise RuntimeError if a one-launch call on this block's workspace
+        gave up a wait (its rows, and those of every later one-launch call
+        until reset(), are NaN); synchronises the current stream."""
+        if self._ws is not None:
+            L.check(L.lib().vqk_moe_layer_status(T.ptr(self._ws), T.stream(self._ws.device)),
+                    "moe layer")
+
+    def reset(self):
+        """Zero the workspace header (clears a reported error)."""
+        if self._ws is not None:
+            L.check(L.lib().vqk_moe_layer_reset(T.ptr(self._ws), T.stream(self._ws.device)),
+                    "moe layer")
 
     # ----------------------------------------------------------- composed
     def composed(self, x, logits):

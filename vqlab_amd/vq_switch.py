@@ -174,18 +174,26 @@ def _switch_apply(x2, eidx, codes, codebook, scales, pack_bits, IN, xkrep, rowtb
     e = eidx.reshape(-1).to(torch.int32).contiguous()
     N = e.numel()
     o = opts or options()
-    if out_dtype is not None:
-        o = L.options(fused_max_n=o.fused_max_n, dense_fused_max_n=o.dense_fused_max_n,
-                      decode_bf16io=1, prefill_bf16io=1)
     ws = ctypes.c_size_t()
     L.check(L.lib().vqk_switch_apply_workspace(ctypes.byref(w), N, ctypes.byref(o),
                                                ctypes.byref(ws)), "VQSwitchLinear")
     work = torch.empty(ws.value, dtype=torch.uint8, device=x2.device) if ws.value else None
     y = torch.empty((N, w.OUT), dtype=out_dtype or x2.dtype, device=x2.device)
+    wk = T.ptr(work) if work is not None else None
+    if out_dtype is not None:
+        # the same dispatch (a workspace means the grouped GEMM), one rounding
+        if ws.value:
+            L.check(L.lib().vqk_grouped_gemm(ctypes.byref(w), T.ptr(x2), T.act_type(x2), x2.shape[0],
+                                             T.ptr(e), N, int(xkrep), T.ptr(y), T.act_type(y), wk,
+                                             ws.value, T.stream(x2.device)), "VQSwitchLinear")
+        else:
+            L.check(L.lib().vqk_moe_expert_gemv(ctypes.byref(w), T.ptr(x2), T.act_type(x2),
+                                                x2.shape[0], T.ptr(e), N, int(xkrep), T.ptr(y),
+                                                T.act_type(y), T.stream(x2.device)), "VQSwitchLinear")
+        return y
     L.check(L.lib().vqk_switch_apply(ctypes.byref(w), T.ptr(x2), T.act_type(x2), x2.shape[0],
-                                     T.ptr(e), N, int(xkrep), T.ptr(y), T.act_type(y),
-                                     T.ptr(work) if work is not None else None, ws.value,
-                                     ctypes.byref(o), T.stream(x2.device)), "VQSwitchLinear")
+                                     T.ptr(e), N, int(xkrep), T.ptr(y), T.act_type(y), wk,
+                                     ws.value, ctypes.byref(o), T.stream(x2.device)), "VQSwitchLinear")
     return y
 
 
@@ -287,8 +295,9 @@ class VQSwitchLinear(torch.nn.Module):
             x2, rep = x.expand(*lead, 1, IN).reshape(N, IN), 1
         eidx = indices.reshape(-1)
         # libvqk's dispatch (vqk_switch_apply): the fused GEMV up to
-        # VQ_FUSED_MAX_N pairs, else -- or when the pairs crowd onto few
-        # experts, N >= 4 and N >= 2E -- the grouped GEMM. By default the
+        # VQ_FUSED_MAX_N pairs, else -- or, an extension beyond the
+        # reference, when the pairs crowd onto few experts (N >= 4 and
+        # N >= 2E) -- the grouped GEMM. By default the
         # outputs are rounded through fp16 like the reference's fp16 kernels
         # and cast; an explicit out_dtype keeps the single rounding.
         y = _switch_apply(x2, eidx, self.codes, self.codebook, self.vq_scales, self.pack_bits,
