@@ -533,3 +533,20 @@ def test_embed_rows_is_gather_of_full_dequant():
     got = vo.embed_rows(ids, codes, cb, sc, 32)
     assert got.shape == (3, 4, 64)
     assert np.array_equal(got.view(np.uint16), full[ids].view(np.uint16))
+
+
+def test_mtp_logits_follow_the_survey_routing():
+    """bench.mtp_logits (the config-4 benchmark's and tests' MTP routing):
+    under the oracle's routing every token gets k distinct experts, every
+    touched expert 1..min(8, T) tokens, and the touched-expert count is the
+    survey's (~140 of 512 at T = 64)."""
+    from bench import mtp_logits
+    rng = np.random.default_rng(21)
+    for T, lo, hi in ((4, 8, 40), (16, 25, 60), (64, 110, 170)):
+        lg = mtp_logits(rng, T, 512, 10)
+        ids, _ = vo.route(lg, 10)
+        assert all(len(set(r)) == 10 for r in ids)
+        cnt = np.bincount(ids.ravel(), minlength=512)
+        touched = cnt[cnt > 0]
+        assert touched.min() >= 1 and touched.max() <= min(8, T)
+        assert lo <= touched.size <= hi, touched.size
