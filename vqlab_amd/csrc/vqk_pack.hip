@@ -138,36 +138,80 @@ __device__ __forceinline__ void dq_entry(const uint16_t *cb, uint32_t c, uint16_
 // of one (small weights are latency-bound; a large table with random codes is
 // bound by the L2's random-read rate instead). Threads past the last code of
 // a row zero its padding up to out_ld.
+// The code format is a template parameter: with it decided at run time the
+// compiler waited for each row's code load before issuing the next row's (one
+// HBM round trip per row; config 5: 97-101 us per 17408 x 5120 linear).
 constexpr int kDqRows = 4;
-template <int D>
+enum : int { kCfPacked = 0, kCfU8 = 1, kCfU16 = 2 };
+template <int D, int CF>
 __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
     const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (j * D >= a.out_ld) return;
     const bool pad = j >= a.NSUB;
     const int64_t gy = gridDim.y;
-    for (int64_t o0 = blockIdx.y; o0 < a.rows; o0 += gy * kDqRows) {
-        int64_t cr[kDqRows];
+    // where code j sits in a packed row: word wi, shift sh (a field never
+    // leaves its 32-code block, so a second word is within the row)
+    int64_t wi = 0;
+    int sh = 0;
+    if (CF == kCfPacked) {
+        const int64_t bit = (j >> 5) * (int64_t(kBlock) * a.bits) + (j & 31) * a.bits;
+        wi = bit >> 5;
+        sh = int(bit & 31);
+    }
+    const int64_t wi1 = wi + 1 < a.code_cols ? wi + 1 : wi;
+    const bool any = a.stored_rows > 0;
+    // codes and scales of the kDqRows rows of step o0 (row -1: nothing used).
+    // Every row's loads are issued before any is used; a row with no code row
+    // reads row 0 (so the loads need no branch) and is zeroed after.
+    auto load_step = [&](int64_t o0, int64_t (&cr)[kDqRows], uint32_t (&c)[kDqRows],
+                         uint16_t (&sc)[kDqRows]) {
 #pragma unroll
         for (int i = 0; i < kDqRows; ++i) {
             const int64_t orow = o0 + i * gy;
             cr[i] = (orow < a.rows && !pad) ? dq_code_row(a, orow) : -1;
         }
-        uint32_t c[kDqRows];
-        uint16_t sc[kDqRows];
+        if (!any) {
+#pragma unroll
+            for (int i = 0; i < kDqRows; ++i) { c[i] = 0u; sc[i] = 0; }
+            return;
+        }
+        uint32_t w0[kDqRows], w1[kDqRows];
 #pragma unroll
         for (int i = 0; i < kDqRows; ++i) {
-            c[i] = 0u;
-            sc[i] = 0;
-            if (cr[i] >= 0) {
-                if (a.bits) c[i] = packed_code(static_cast<const uint32_t *>(a.codes) + cr[i] * a.code_cols, j, a.bits);
-                else if (a.code_bytes == 1) c[i] = static_cast<const uint8_t *>(a.codes)[cr[i] * a.code_cols + j];
-                else c[i] = static_cast<const uint16_t *>(a.codes)[cr[i] * a.code_cols + j];
-                if (c[i] >= uint32_t(a.K)) c[i] = uint32_t(a.K - 1);   // never read past the table
-                // a group boundary can fall inside a subvector only if G % D != 0,
-                // which validation refuses; one scale serves all D values
-                sc[i] = a.scales[cr[i] * a.ngrp + (j * D) / a.G];
+            const int64_t row = cr[i] >= 0 ? cr[i] : 0;
+            if (CF == kCfPacked) {
+                const uint32_t *r = static_cast<const uint32_t *>(a.codes) + row * a.code_cols;
+                w0[i] = r[wi];
+                w1[i] = r[wi1];
+            } else if (CF == kCfU8) {
+                w0[i] = static_cast<const uint8_t *>(a.codes)[row * a.code_cols + j];
+            } else {
+                w0[i] = static_cast<const uint16_t *>(a.codes)[row * a.code_cols + j];
             }
+            // a group boundary can fall inside a subvector only if G % D != 0,
+            // which validation refuses; one scale serves all D values
+            sc[i] = a.scales[row * a.ngrp + (j * D) / a.G];
         }
+#pragma unroll
+        for (int i = 0; i < kDqRows; ++i) {
+            uint32_t v = w0[i];
+            if (CF == kCfPacked) {
+                v >>= sh;
+                if (sh + a.bits > 32) v |= w1[i] << (32 - sh);
+                v &= (1u << a.bits) - 1u;
+            }
+            c[i] = cr[i] >= 0 ? v : 0u;
+            sc[i] = cr[i] >= 0 ? sc[i] : uint16_t(0);
+        }
+    };
+    for (int64_t o0 = blockIdx.y; o0 < a.rows; o0 += gy * kDqRows) {
+        int64_t cr[kDqRows];
+        uint32_t c[kDqRows];
+        uint16_t sc[kDqRows];
+        load_step(o0, cr, c, sc);
+#pragma unroll
+        for (int i = 0; i < kDqRows; ++i)
+            if (c[i] >= uint32_t(a.K)) c[i] = uint32_t(a.K - 1);   // never read past the table
         uint16_t e[kDqRows][D];
 #pragma unroll
         for (int i = 0; i < kDqRows; ++i) {
@@ -227,6 +271,13 @@ static dim3 rows_grid(int64_t cols, int64_t rows, int64_t rpt = 1) {
     return dim3(unsigned(gx), unsigned(gy), 1);
 }
 
+template <int D>
+static void launch_dq(int cf, dim3 grid, hipStream_t st, const DequantArgs &a) {
+    if (cf == kCfPacked) hipLaunchKernelGGL((k_dequant<D, kCfPacked>), grid, dim3(256), 0, st, a);
+    else if (cf == kCfU8) hipLaunchKernelGGL((k_dequant<D, kCfU8>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_dequant<D, kCfU16>), grid, dim3(256), 0, st, a);
+}
+
 static int launch_dequant(const vqk_weights *w, const Geom &g, const uint32_t *eidx, int64_t r0,
                           int64_t rows, uint16_t *out, hipStream_t st, int mode = kDqF16,
                           int64_t out_ld = 0) {
@@ -251,11 +302,10 @@ static int launch_dequant(const vqk_weights *w, const Geom &g, const uint32_t *e
     a.out = out;
     if (rows == 0) return VQK_OK;
     const dim3 grid = rows_grid(a.out_ld / g.D, rows, 4);
-    switch (g.D) {
-        case 2: hipLaunchKernelGGL(k_dequant<2>, grid, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(k_dequant<4>, grid, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL(k_dequant<8>, grid, dim3(256), 0, st, a); break;
-    }
+    const int cf = g.packed ? kCfPacked : (g.BITS == 8 ? kCfU8 : kCfU16);
+    if (g.D == 2) launch_dq<2>(cf, grid, st, a);
+    else if (g.D == 4) launch_dq<4>(cf, grid, st, a);
+    else launch_dq<8>(cf, grid, st, a);
     return hip_status(hipGetLastError(), "dequant launch");
 }
 
