@@ -1,6 +1,7 @@
 """Benchmark of the VQ MoE decode layer on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c1|c2|c3|c3b4|c4|c4t16|c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload c1|c2|c3|c3b4|c4|c4t16|c4survey|c4t16survey|c5|gather]
 
 Default workload: a Qwen3.6-35B-A3B-shaped MoE
 decode layer -- hidden 2048, 256 experts of intermediate 512, top-8 softmax
@@ -84,6 +85,9 @@ WORKLOADS = {
                         layers=2, dead=0.2, kind="mtp", routing="survey",
                         desc="MTP verify batch on the config-3 layer, T=16, 20% skipzero rows, "
                              "each touched expert 1..8 tokens (BASELINE configs[3])"),
+    # measurement probe: the random-gather rate of an L2-resident table
+    "gather": dict(kind="gather",
+                   desc="random 16-byte gathers from a 256 KB / 1 MB L2-resident table (probe)"),
     "c5": dict(N=2048, H=5120, F=17408, d=8, K=65536, kind="prefill",
                desc="Dense Qwen3.8-27B-shaped VQ prefill: 5120x17408 then 17408x5120, "
                     "x [2048, 5120] (BASELINE configs[4])"),
@@ -687,6 +691,7 @@ def run_layer(torch, dev, a, w):
     # 16 channels per XCD take one request per clock (0.5 per clock per CU);
     # the committed counter profile gives the L1 -> L2 read requests per call
     req = measured_traffic(f"moe_layer_{a.workload}_traffic.md", "l2_read_requests_per_call")
+    cap = measured_traffic("moe_layer_c3_traffic.md", "l2_request_cap_per_us_per_cu")
     if req:
         floor_us = req / (L2_REQ_PER_CLK_PER_CU * N_CUS * PEAK_CLOCK_GHZ * 1e3)
         out["roofline"]["l2_request_floor"] = {
@@ -694,6 +699,13 @@ def run_layer(torch, dev, a, w):
             "achieved_us": round(us_call, 3), "frac": round(floor_us / us_call, 4),
             "basis": f"{L2_REQ_PER_CLK_PER_CU} L2 requests per clock per CU x {N_CUS} CUs x "
                      f"{PEAK_CLOCK_GHZ} GHz (published peak clock)"}
+        if cap:
+            mfloor = req / (cap * N_CUS)
+            out["roofline"]["l2_request_floor"].update({
+                "measured_cap_floor_us": round(mfloor, 2),
+                "measured_cap_frac": round(mfloor / us_call, 4),
+                "measured_cap_basis": f"{cap} L1->L2 requests per us per CU, the gather probe's "
+                                      "rate (bench.py --workload gather)"})
     return out, wall, calls
 
 
@@ -742,7 +754,49 @@ def extra_workloads(torch, dev, a):
     return res
 
 
-RUNNERS = {"layer": run_layer, "mtp": run_mtp, "prefill": run_prefill, "dense_gemv": run_dense_gemv}
+def run_gather(torch, dev, a, w):
+    """The random-gather rate the hardware sustains from an L2-resident table
+    (libvqk's vqk__probe_gather test hook): the codebook reads beyond the LDS
+    part of the config-3 / config-4 kernels and the config-5 dequant. Reported
+    as 16-byte gathers per us per CU at 4, 8 and 16 waves per CU."""
+    import ctypes
+    from vqlab_amd import _lib as LB, _torch as TT
+    lib = LB.lib()
+    lib.vqk__probe_gather.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    ncu = torch.cuda.get_device_properties(dev).multi_processor_count
+    table = torch.randint(0, 2**31 - 1, (1 << 18,), dtype=torch.int32, device=dev)   # 1 MiB
+    sink = torch.empty(ncu * 4 * 256, dtype=torch.int32, device=dev)
+    st = TT.stream(dev)
+    rows = []
+    for kb in (256, 1024):
+        for wpc in (4, 8, 16):
+            for inflight in (1, 8):
+                wgs, rounds = ncu * wpc // 4, 200
+                LB.check(lib.vqk__probe_gather(TT.ptr(table), kb << 10, wgs, inflight, 4, TT.ptr(sink), st))
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                LB.check(lib.vqk__probe_gather(TT.ptr(table), kb << 10, wgs, inflight, rounds,
+                                               TT.ptr(sink), st))
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3
+                rate = wgs * 256 * rounds * inflight / us / ncu
+                rows.append({"table_kb": kb, "waves_per_cu": wpc, "loads_in_flight": inflight,
+                             "gathers_per_us_per_cu": round(rate, 1)})
+                log(rows[-1])
+    best = max(r["gathers_per_us_per_cu"] for r in rows if r["table_kb"] == 256)
+    return {"metric": "random 16-byte gathers per us per CU from an L2-resident table",
+            "value": best, "unit": "gathers/us/CU", "dtype": "u32",
+            "config": {"workload": w["desc"], "cus": ncu},
+            "rates": rows,
+            "roofline": {"bound": "l2", "achieved": best, "peak": None, "unit": "gathers/us/CU",
+                         "frac": None},
+            "cpu_baseline": None}, 0.0, 1
+
+
+RUNNERS = {"layer": run_layer, "mtp": run_mtp, "prefill": run_prefill, "dense_gemv": run_dense_gemv,
+           "gather": run_gather}
 
 
 def main():
