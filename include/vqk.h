@@ -53,9 +53,22 @@ extern "C" {
  * arithmetic of the reference's default decode path, whose fused kernels
  * return fp16 that the caller then casts to x's dtype (vq_switch.py:5306-5308,
  * 5423). Without it a result is rounded once, from fp32, into y's type (the
- * reference with VQ_DECODE_BF16IO=1, vq_switch.py:4421, 5303-5306). x types
- * take no flags. */
+ * reference with VQ_DECODE_BF16IO=1, vq_switch.py:4421, 5303-5306). */
 #define VQK_VIA_F16 0x100
+
+/* Wide-activation flag, OR'd into the x_type of vqk_moe_expert_gemv /
+ * vqk_dense_gemv for d = 8 modules only (VQK_EINVAL otherwise): x enters the
+ * products unrounded -- bf16 and fp32 activations widened exactly to fp32,
+ * each codebook half widened to fp32, fp32 multiply-adds -- instead of being
+ * narrowed to fp16 first. It is the arithmetic of the reference's
+ * float4-staged d8 decode kernels (vq_switch.py:1440-1458, 1576-1586, and
+ * _SRC_FUSED_PACKED_D8 after 1316), which VQ_DECODE_BF16IO feeds bf16 x
+ * uncast (vq_switch.py:4412-4417, 5306); its d2 / d4 decode kernels stage x
+ * as fp16 and round it in-kernel, and its grouped prefill converts bf16 x to
+ * fp16 on stage-in even under VQ_GEMMSEG_BF16IO (vq_switch.py:4364-4372), so
+ * those paths take no flag. vqk_switch_apply sets it by itself (see
+ * vqk_options.decode_bf16io). No other entry point accepts it. */
+#define VQK_X_KEEP 0x200
 
 /* One VQ-coded linear, or a stack of E expert linears sharing one codebook
  * (VQSwitchLinear, vq_switch.py:5198-5234; VQLinear, vq_dense.py:322-334).
@@ -290,11 +303,14 @@ int vqk_gemmseg_fits(int32_t D, int64_t K, int32_t G, int32_t pack_bits,
  *                      runs the fused GEMV (default 32)
  *   decode_bf16io      VQ_DECODE_BF16IO: 0 (default) = the fused routed path
  *                      rounds its outputs through fp16 (VQK_VIA_F16); 1 = once
- *                      into y's type
- *   prefill_bf16io     VQ_GEMMSEG_BF16IO: the same for the grouped GEMM path
- *                      (both flags keep the single rounding for bf16 x only,
- *                      like the reference's _keep_bf16, vq_switch.py:5306,
- *                      5369; other x types still round through fp16)
+ *                      into y's type, and at d = 8 bf16 x enters the GEMV
+ *                      unrounded (VQK_X_KEEP)
+ *   prefill_bf16io     VQ_GEMMSEG_BF16IO: the single output rounding for the
+ *                      grouped GEMM path; x is still converted to fp16 on
+ *                      stage-in, as the reference's does (vq_switch.py:
+ *                      4364-4372). Both flags act on bf16 x only, like the
+ *                      reference's _keep_bf16 (vq_switch.py:5306, 5369);
+ *                      other x types still round through fp16
  *   crowded_grouped    an extension beyond the reference's dispatch, no VQ_*
  *                      flag: 1 (default) also sends calls whose pairs crowd
  *                      onto few experts (N >= 4 and N >= 2E) to the grouped

@@ -32,6 +32,9 @@ Pinning (what checks each function; see tests/test_oracle.py):
                    (vq_oracle.c) including subnormal, inf and NaN inputs.
   decode_matmul    float64 brute-force loop on tiny shapes; closed forms
                    (one-hot codebook, constant scales).
+  dequant_exact    equals dequant wherever s * cb is an fp16 value (scales
+                   that are powers of two); per-group brute-force loop of the
+                   reference's fused formula on tiny shapes.
   route            brute-force sort; weights sum to one; softmax invariance.
   moe_layer        identical-expert invariant (combine of equal experts ==
                    one expert), per-pair loop restatement; the shared-expert
@@ -184,15 +187,41 @@ def decode_matmul(x: np.ndarray, w16: np.ndarray, acc: str = "f64") -> np.ndarra
     return np.asarray(x, np.float32).astype(dt) @ np.asarray(w16).astype(dt).T
 
 
+def dequant_exact(codes: np.ndarray, codebook: np.ndarray, scales: np.ndarray,
+                  group: int) -> np.ndarray:
+    """W[r, j*d+u] = f64(cb[c_rj, u]) * f64(s[r, (j*d+u)//G]), unrounded.
+
+    The fused decode kernels never form an fp16 weight: they sum the code
+    dots <cb[c], x> of a scale group and scale that sum once
+    (`acc = fma((float)srow[g], gacc, acc)`, vq_switch.py:1344-1350, 978-985),
+    so in exact arithmetic their weight is this product (distributivity).
+    """
+    codes = np.asarray(codes).astype(np.int64)
+    cb = np.asarray(codebook, np.float16).astype(np.float64)
+    s = np.asarray(scales, np.float16).astype(np.float64)
+    d = cb.shape[1]
+    lead, nsub = codes.shape[:-1], codes.shape[-1]
+    w = cb[codes].reshape(lead + (nsub * d,))
+    sx = np.repeat(s, group, axis=-1)[..., : nsub * d]
+    with np.errstate(invalid="ignore", over="ignore"):
+        return w * sx
+
+
 def expert_gemv(x, eidx, codes, codebook, scales, group, xkrep=1,
-                row_table=None, acc="f64"):
+                row_table=None, acc="f64", weights="fp16"):
     """y[n, r] for pairs n: token row n // xkrep against expert eidx[n].
 
     Mirrors _fused's contract (vq_switch.py:2919-2963, XKREP 4422-4451):
     codes [E, OUT, NSUB] unpacked (or compact [NLIVE, NSUB] with a row
     table [E, OUT], -1 = dead row -> exact +0, vq_switch.py:760-771).
+    weights "fp16": the dequantised fp16 weight (dequant); "exact": the
+    fused kernels' per-group scaling unrounded (dequant_exact), for checks
+    whose bar is tighter than one fp16 rounding of W. x is taken in
+    float32 (bf16 values exactly); a path that stages it as fp16 gets it
+    rounded by the caller.
     """
     x = np.asarray(x, np.float32)
+    deq = dequant_exact if weights == "exact" else dequant
     eidx = np.asarray(eidx).astype(np.int64).reshape(-1)
     n_pairs = eidx.shape[0]
     if row_table is None:
@@ -206,13 +235,14 @@ def expert_gemv(x, eidx, codes, codebook, scales, group, xkrep=1,
         e = int(eidx[n])
         if e not in cache:
             if row_table is None:
-                w = dequant(codes[e], codebook, scales[e], group)
+                w = deq(codes[e], codebook, scales[e], group)
             else:
                 rt = np.asarray(row_table)[e]
                 live = rt >= 0
-                w = np.zeros((out, codes.shape[-1] * codebook.shape[1]), np.float16)
+                w = np.zeros((out, codes.shape[-1] * codebook.shape[1]),
+                             np.float64 if weights == "exact" else np.float16)
                 if live.any():
-                    w[live] = dequant(codes[rt[live]], codebook, scales[rt[live]], group)
+                    w[live] = deq(codes[rt[live]], codebook, scales[rt[live]], group)
             cache[e] = w.astype(dt)
         y[n] = x[n // xkrep].astype(dt) @ cache[e].T
     return y

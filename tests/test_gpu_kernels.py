@@ -266,6 +266,81 @@ def test_expert_gemv_unpacked_and_bad_ids():
     assert (y[2] == 0).all()
 
 
+# ------------------------------------------------- wide x (VQK_X_KEEP, d=8)
+def _wide_x(rng, IN):
+    """Two bf16 token rows that fp16 staging cannot hold: row 0 reaches
+    |x| = 4e5 (fp16 overflows above 65504), row 1 lies in fp16's subnormal
+    range (1e-7 .. 1e-6, one to four significant bits left)."""
+    sgn = np.where(rng.random((2, IN)) < 0.5, -1.0, 1.0)
+    big = sgn[0] * np.exp(rng.uniform(0.0, np.log(4e5), IN))
+    tiny = sgn[1] * np.exp(rng.uniform(np.log(1e-7), np.log(1e-6), IN))
+    return torch.from_numpy(np.stack([big, tiny]).astype(np.float32)).to("cuda", torch.bfloat16)
+
+
+@pytest.mark.parametrize("case", [
+    # (E, OUT, IN, K, G, packed): c3 gate/up rows (14-bit table partly in
+    # LDS, 4 scale groups per block); a 12-bit table in LDS with groups of two
+    # blocks; 13 bits at 64 blocks per row (the fp16 kernels' LDS cannot hold
+    # that table part and row: they take the generic kernel); ragged unpacked
+    # rows (generic kernel)
+    (6, 1024, 4096, 16384, 64, True),
+    (4, 512, 2048, 4096, 512, True),
+    (3, 128, 16384, 8192, 64, True),
+    (3, 300, 1000, 256, 8, False),
+])
+def test_expert_gemv_d8_wide_x(case):
+    """VQK_X_KEEP: bf16 x beyond fp16's range and below its normal range
+    enters the d8 GEMV unrounded, fp32 products with the widened table, as
+    the reference's float4-staged d8 kernels take it under VQ_DECODE_BF16IO
+    (vq_switch.py:1440-1458, 4412-4417). Bar: |y - ref| <= 3e-5 * (|x| @ |W|^T)
+    against the float64 fused formula (oracle weights="exact"), an fp32
+    accumulation bar that fp16 staging of either row misses (checked)."""
+    import ctypes
+    from vqlab_amd import _lib as L, _torch as TT, vq_switch as VS
+    E, OUT, IN, K, G, packed = case
+    print(f"wide x {case}", flush=True)
+    rng = np.random.default_rng(sum(case[:5]))
+    m = make_module(rng, E, OUT, IN, 8, K, G=G, packed=packed)
+    codes, cb, sc = to_device(m)
+    x = _wide_x(rng, IN)
+    k = 3
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(2)]).reshape(-1).astype(np.int32)
+    eidx = torch.from_numpy(ids).cuda()
+    xf = x.float().cpu().numpy()
+    ref = vo.expert_gemv(xf, ids, m["codes"], m["codebook"], m["scales"], G, xkrep=k,
+                         weights="exact")
+    absref = vo.expert_gemv(np.abs(xf), ids, m["codes"], np.abs(m["codebook"]), m["scales"], G,
+                            xkrep=k, weights="exact")
+    bar = 3e-5 * absref
+    keep = []
+    w = TT.weights(codes, cb, sc, G, m["pack_bits"], IN if packed else None, keep=keep)
+
+    def run(xt):
+        y = torch.empty((2 * k, OUT), dtype=torch.float32, device="cuda")
+        L.check(L.lib().vqk_moe_expert_gemv(ctypes.byref(w), TT.ptr(x), xt, 2, TT.ptr(eidx), 2 * k,
+                                            k, TT.ptr(y), L.VQK_F32, TT.stream(x.device)), "wide x")
+        return y
+
+    yt = run(L.VQK_BF16 | L.VQK_X_KEEP)
+    y = yt.cpu().numpy().astype(np.float64)
+    err = np.abs(y - ref)
+    i = np.unravel_index(np.argmax(err - bar), err.shape)
+    assert np.isfinite(y).all() and (err <= bar).all(), (i, y[i], ref[i], bar[i])
+    # the fp16-staged kernel misses the bar: row 0 overflows, row 1 loses bits
+    y16 = run(L.VQK_BF16).cpu().numpy().astype(np.float64)
+    assert not np.isfinite(y16[:k]).all()
+    assert (np.abs(y16[k:] - ref[k:]) > bar[k:]).any()
+    # the dispatch sets the flag for bf16 x under decode_bf16io (one output
+    # rounding), and the out_dtype form runs the same kernel
+    o = L.options(decode_bf16io=1, crowded_grouped=0)
+    yo = VS._switch_apply(x, eidx, codes, cb, sc, m["pack_bits"], IN, k, out_dtype=torch.float32,
+                          opts=o)
+    assert torch.equal(yo, yt)
+    yb = VS._switch_apply(x, eidx, codes, cb, sc, m["pack_bits"], IN, k, opts=o)
+    assert yb.dtype == torch.bfloat16
+    assert (np.abs(_np(yb) - ref) <= bar + np.abs(ref) * 2.0 ** -8).all()
+
+
 def test_switch_linear_module_and_errors():
     from vqlab_amd import vq_switch as VS
     rng = np.random.default_rng(12)

@@ -243,6 +243,43 @@ def test_expert_gemv_xkrep_and_row_table():
     assert (yc[1, :3] == 0).all() and (yc[0, 5] == 0)
 
 
+def test_exact_weights_pins():
+    """dequant_exact: (1) equals dequant wherever s * cb is an fp16 value
+    (power-of-two scales, codebook values on a coarse grid); (2) the exact
+    expert GEMV equals a per-group loop of the reference's fused formula
+    y = sum_g s_g * sum_{codes of g} <cb[c], x> (vq_switch.py:1336-1350) on
+    tiny shapes; (3) it differs from the fp16 weight exactly by that
+    weight's rounding, so a dropped scale or a wrong group index fails (1)."""
+    rng = np.random.default_rng(21)
+    E, OUT, NSUB, d, K, G = 2, 6, 16, 8, 32, 32
+    codes = rng.integers(0, K, (E, OUT, NSUB)).astype(np.uint16)
+    cb = (rng.integers(-64, 64, (K, d)) / 256.0).astype(np.float16)     # exact in fp16
+    sp2 = (2.0 ** rng.integers(-3, 3, (E, OUT, NSUB * d // G))).astype(np.float16)
+    w16 = vo.dequant(codes, cb, sp2, G).astype(np.float64)
+    assert np.array_equal(vo.dequant_exact(codes, cb, sp2, G), w16)
+    # (2) brute force, general scales
+    sc = rng.uniform(0.5, 1.5, (E, OUT, NSUB * d // G)).astype(np.float16)
+    x = rng.standard_normal((3, NSUB * d)).astype(np.float32)
+    eidx = np.array([1, 0, 1])
+    y = vo.expert_gemv(x, eidx, codes, cb, sc, G, weights="exact")
+    spg = G // d
+    for n in range(3):
+        e = eidx[n]
+        for r in range(OUT):
+            acc = 0.0
+            for g in range(NSUB // spg):
+                ga = 0.0
+                for j in range(g * spg, (g + 1) * spg):
+                    for u in range(d):
+                        ga += float(cb[codes[e, r, j], u]) * float(x[n, j * d + u])
+                acc += float(sc[e, r, g]) * ga
+            assert abs(y[n, r] - acc) <= 1e-12 * max(1.0, abs(acc))
+    # (3) the fp16 weight is the exact one rounded once
+    we = vo.dequant_exact(codes, cb, sc, G)
+    assert np.array_equal(we.astype(np.float16), vo.dequant(codes, cb, sc, G))
+    assert not np.array_equal(we, vo.dequant(codes, cb, sc, G).astype(np.float64))
+
+
 def test_row_table_brute_force():
     rng = np.random.default_rng(9)
     E, OUT = 5, 37

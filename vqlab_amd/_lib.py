@@ -19,6 +19,7 @@ VQK_F16, VQK_BF16, VQK_F32, VQK_U8, VQK_U16, VQK_U32, VQK_I32, VQK_I64 = range(8
 VQK_NOALLOC_SCRATCH_BYTES = 32 << 20     # include/vqk.h
 VQK_MOE_HEADER_BYTES = 49152             # include/vqk.h: zero before a layer workspace's first call
 VQK_VIA_F16 = 0x100                      # output type flag: round through fp16 first
+VQK_X_KEEP = 0x200                       # x type flag (d=8 GEMV): x enters the products unrounded
 
 c_i32, c_i64, c_p, c_sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
 

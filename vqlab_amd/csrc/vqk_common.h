@@ -16,12 +16,17 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;            // CDNA wavefront width
 constexpr int kBlock = 32;           // codes per packing block
 constexpr int kThreads = 256;        // threads per workgroup of the GEMV kernels
+constexpr int kLdsBytes = 160 * 1024; // LDS a gfx950 workgroup may hold
 constexpr int kCbLdsMax = 64 * 1024; // largest codebook table staged in LDS (bytes)
 constexpr int kGemvHybBytes = 128 * 1024;  // part of a larger table the GEMV keeps in LDS
+// Part of a larger table the GEMV keeps in LDS: less for the wide-x
+// instances, whose fp32 activation row (up to 64 blocks of 1 KB) needs room.
+__host__ __device__ constexpr int gemv_hyb_bytes(bool xf) { return xf ? kCbLdsMax : kGemvHybBytes; }
 
 // Output forms of the weight dequant: fp16 (the bit-exact weight), bf16 (one
 // RNE of it) or rows [W_hi | W_lo | W_hi] of 3 * IN bf16 with W_hi + W_lo = W.

@@ -101,7 +101,10 @@ int vqk_switch_apply(const vqk_weights *w, const void *x, int32_t x_type, int64_
     const int32_t yt = via ? (y_type | VQK_VIA_F16) : y_type;
     if (grouped)
         return vqk_grouped_gemm(w, x, x_type, T, eidx, N, xkrep, y, yt, workspace, ws_bytes, stream);
-    return vqk_moe_expert_gemv(w, x, x_type, T, eidx, N, xkrep, y, yt, stream);
+    // the d8 decode kernels take that bf16 x unrounded (float4 staging,
+    // vq_switch.py:4412-4417); d2 / d4 ones stage it as fp16
+    const int32_t xt = keep && g.D == 8 ? (x_type | VQK_X_KEEP) : x_type;
+    return vqk_moe_expert_gemv(w, x, xt, T, eidx, N, xkrep, y, yt, stream);
 }
 
 int vqk_linear_apply_workspace(const vqk_weights *w, int64_t N, const vqk_options *opt, size_t *bytes) {

@@ -27,6 +27,16 @@
 // Shapes outside the fast kernel's reach (ragged NSUB, rows not word
 // aligned, NB > 64, unusual scale groups) run on the generic kernel: one
 // thread per row, walking its codes.
+//
+// Wide-x instances (XF, d = 8 only, x_type flag VQK_X_KEEP): x is staged in
+// LDS as fp32 -- bf16 and fp32 activations exactly -- and each table entry's
+// halves are widened to fp32 and multiplied with fp32 FMAs, the arithmetic of
+// the reference's float4-staged d8 kernels (vq_switch.py:1440-1458,
+// 1576-1586, and the packed d8 thread-per-row kernel after 1316) that
+// VQ_DECODE_BF16IO feeds bf16 x unrounded (vq_switch.py:4412-4417). Lanes
+// read their block's activations from LDS per code (256 fp32 values per
+// block would not fit in registers), and a table too large for LDS keeps
+// only its first kCbLdsMax bytes there, leaving room for the fp32 row.
 #pragma once
 
 #include <mutex>
@@ -244,6 +254,46 @@ __device__ __forceinline__ float block_dot_hyb_lx(const uint32_t (&w)[BITS], con
     return acc;
 }
 
+// block_dot of the wide-x instances: the block's 32·D activations as fp32 in
+// LDS (`xl`), every entry half widened exactly to fp32. CBL: the whole table
+// is in `cbl`; otherwise entries below `kl` come from `cbl`, the rest from
+// the global table `cbg` (clamped to kmax).
+template <int D, int BITS, int GPB, bool CBL>
+__device__ __forceinline__ float block_dot_xf(const uint32_t (&w)[BITS], const float *xl,
+                                              const float (&s)[GPB], const h2 *cbl,
+                                              const h2 *cbg, uint32_t kl, uint32_t kmax) {
+    typedef typename EntryT<D>::type E;
+    constexpr int CPG = kBlock / GPB;
+    const f32x4 *xv = reinterpret_cast<const f32x4 *>(__builtin_assume_aligned(xl, 16));
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < GPB; ++g) {
+        float ga = 0.f;
+#pragma unroll
+        for (int q = 0; q < CPG; ++q) {
+            const int i = g * CPG + q;
+            const uint32_t c = block_field<BITS>(w, i);
+            E e;
+            if constexpr (CBL) {
+                e = reinterpret_cast<const E *>(cbl)[c];
+            } else {
+                if (c < kl) e = reinterpret_cast<const E *>(cbl)[c];
+                else e = reinterpret_cast<const E *>(cbg)[min(c, kmax)];
+            }
+#pragma unroll
+            for (int k = 0; k < D / 4; ++k) {
+                const f32x4 x = xv[i * (D / 4) + k];
+                ga = fmaf(float(e[4 * k]), x.x, ga);
+                ga = fmaf(float(e[4 * k + 1]), x.y, ga);
+                ga = fmaf(float(e[4 * k + 2]), x.z, ga);
+                ga = fmaf(float(e[4 * k + 3]), x.w, ga);
+            }
+        }
+        acc = fmaf(s[g], ga, acc);
+    }
+    return acc;
+}
+
 template <int BITS, int GPB>
 __device__ __forceinline__ void load_block(const GemvParams &p, int64_t cr, int blk, int sidx,
                                            uint32_t (&w)[BITS], uint32_t (&s)[GPB]) {
@@ -434,6 +484,69 @@ __device__ __forceinline__ void stage_x(const void *x, int32_t type, int64_t bas
     }
 }
 
+// Eight activations starting at element i -> fp32, exactly (16-byte aligned
+// rows only, checked by the caller).
+__device__ __forceinline__ void load8_f32(const void *x, int32_t type, int64_t i, float (&v)[8]) {
+    if (type == VQK_F32) {
+        const f32x4 a = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(x) + i);
+        const f32x4 b = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(x) + i + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        return;
+    }
+    const u32x4 u = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(x) + i);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint16_t lo = uint16_t(w[k]), hi = uint16_t(w[k] >> 16);
+        v[2 * k] = type == VQK_BF16 ? bf16_to_f32(lo) : h_to_f32(lo);
+        v[2 * k + 1] = type == VQK_BF16 ? bf16_to_f32(hi) : h_to_f32(hi);
+    }
+}
+
+// One activation row -> fp32 in LDS (the wide-x instances), blocks of XH
+// values at a padded stride XS (floats), zero past IN; the loads of a
+// thread's groups are all issued before the first store, as in stage_x.
+template <int XH, int XS>
+__device__ __forceinline__ void stage_xf(const void *x, int32_t type, int64_t base, int IN, int NB,
+                                         float *xs) {
+    static_assert(XH % 8 == 0 && XS % 4 == 0, "8-value groups stay inside a 16-byte aligned block");
+    const int me = threadIdx.x, nt = blockDim.x;
+    const int esz = type == VQK_F32 ? 4 : 2;
+    const bool vec = ((reinterpret_cast<uintptr_t>(x) + uint64_t(base) * esz) & 15) == 0 &&
+                     (IN & 7) == 0;
+    if (vec) {
+        constexpr int U = 2;
+        const int ng = NB * XH / 8;
+        for (int g0 = me; g0 < ng; g0 += U * nt) {
+            float v[U][8];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int g = g0 + u * nt;
+                if (g < ng && g * 8 < IN) {
+                    load8_f32(x, type, base + g * 8, v[u]);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) v[u][k] = 0.f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int g = g0 + u * nt;
+                if (g < ng) {
+                    const int i = g * 8;
+                    f32x4 *d = reinterpret_cast<f32x4 *>(xs + (i / XH) * XS + (i % XH));
+                    d[0] = f32x4{v[u][0], v[u][1], v[u][2], v[u][3]};
+                    d[1] = f32x4{v[u][4], v[u][5], v[u][6], v[u][7]};
+                }
+            }
+        }
+        return;
+    }
+    for (int i = me; i < NB * XH; i += nt)
+        xs[(i / XH) * XS + (i % XH)] = i < IN ? load_act(x, type, base + i) : 0.f;
+}
+
 // The lane's 32*D staged activations -> 16*D half2 registers. Read as plain
 // 32-bit words (the compiler merges them into 128-bit LDS reads):
 // bit-casting elements of a u32x4 value miscompiled, every element read as
@@ -450,16 +563,17 @@ __device__ __forceinline__ void load_xregs(const f16 *src, h2 (&xr)[16 * D]) {
 }
 
 // ------------------------------------------------------------ fast kernel
-template <int D, int BITS, int GPB>
+template <int D, int BITS, int GPB, bool XF = false>
 __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
     constexpr bool CBL = cb_in_lds(D, BITS);
-    // LDS table entries: the whole table, or the first kGemvHybBytes of it
-    constexpr int CBN = CBL ? (1 << BITS) : kGemvHybBytes / (2 * D);
-    constexpr int XH = kBlock * D;               // x halves per block
-    constexpr int XS = XH + 8;                   // padded LDS stride: 16 B skew per block
+    // LDS table entries: the whole table, or the first part of it
+    constexpr int CBN = CBL ? (1 << BITS) : gemv_hyb_bytes(XF) / (2 * D);
+    constexpr int XH = kBlock * D;               // x values per block
+    constexpr int XS = XH + (XF ? 4 : 8);        // padded LDS stride: 16 B skew per block
     extern __shared__ __align__(16) uint8_t smem[];
     h2 *cb_lds = reinterpret_cast<h2 *>(smem);
     f16 *xs = reinterpret_cast<f16 *>(smem + CBN * D * 2);
+    float *xsf = reinterpret_cast<float *>(smem + CBN * D * 2);
 
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int lpr = 1 << p.lpr_log2, rpw = kWave >> p.lpr_log2;
@@ -487,12 +601,14 @@ __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
     load_block<BITS, GPB>(p, cr, blk, sidx, w, s);   // in flight during staging
 
     stage_codebook_fixed<D, CBN, kThreads>(p.codebook, p.K, cb_lds);
-    stage_x<XH, XS>(p.x, p.x_type, int64_t(tok) * p.x_stride, p.IN, p.NB, xs);
+    if constexpr (XF) stage_xf<XH, XS>(p.x, p.x_type, int64_t(tok) * p.x_stride, p.IN, p.NB, xsf);
+    else stage_x<XH, XS>(p.x, p.x_type, int64_t(tok) * p.x_stride, p.IN, p.NB, xs);
     wait_vmem();
     __syncthreads();
 
     h2 xr[16 * D];
-    load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
+    if constexpr (!XF) load_xregs<D>(xs + (on ? blk : 0) * XS, xr);
+    const float *xl = xsf + (on ? blk : 0) * XS;
     const h2 *cb = CBL ? cb_lds : reinterpret_cast<const h2 *>(p.codebook);
     const uint32_t kmax = uint32_t(p.K - 1);
     const uint32_t kl = uint32_t(min(p.K, CBN));
@@ -504,7 +620,11 @@ __global__ void __launch_bounds__(kThreads) k_gemv_fast(const GemvParams p) {
         load_block<BITS, GPB>(p, crn, blk, sidx, wn, sn);
         float v = 0.f;
         const ScalesF32<GPB> fs(s);
-        if constexpr (CBL) {
+        if constexpr (XF) {
+            if (cr >= 0)
+                v = block_dot_xf<D, BITS, GPB, CBL>(w, xl, fs.v, cb_lds,
+                                                    reinterpret_cast<const h2 *>(p.codebook), kl, kmax);
+        } else if constexpr (CBL) {
             if (cr >= 0) v = block_dot<D, BITS, GPB, true>(w, xr, fs.v, cb, kmax);
         } else {
             if (cr >= 0) v = block_dot_hyb<D, BITS, GPB>(w, xr, fs.v, cb_lds, cb, kl, kmax);
@@ -534,15 +654,20 @@ __device__ __forceinline__ uint32_t generic_code(const GemvParams &p, int64_t cr
     return static_cast<const uint16_t *>(p.codes)[cr * p.code_cols + j];
 }
 
-// One thread per (pair, row); x row staged once per workgroup as plain fp16.
-template <int D>
+// One thread per (pair, row); x row staged once per workgroup as plain fp16
+// (XF: as fp32, the wide-x arithmetic).
+template <int D, bool XF = false>
 __global__ void __launch_bounds__(kThreads) k_gemv_generic(const GemvParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     f16 *xs = reinterpret_cast<f16 *>(smem);
+    float *xsf = reinterpret_cast<float *>(smem);
     const int pair = p.pair0 + int(blockIdx.y);
     const int tok = pair / p.xkrep;
-    for (int i = threadIdx.x; i < p.IN; i += blockDim.x)
-        xs[i] = f16(load_act(p.x, p.x_type, int64_t(tok) * p.x_stride + i));
+    for (int i = threadIdx.x; i < p.IN; i += blockDim.x) {
+        const float v = load_act(p.x, p.x_type, int64_t(tok) * p.x_stride + i);
+        if constexpr (XF) xsf[i] = v;
+        else xs[i] = f16(v);
+    }
     __syncthreads();
     const int r = int(blockIdx.x) * blockDim.x + threadIdx.x;
     if (r >= p.OUT) return;
@@ -568,7 +693,8 @@ __global__ void __launch_bounds__(kThreads) k_gemv_generic(const GemvParams p) {
             const uint32_t c = min(generic_code(p, cr, j), uint32_t(p.K - 1));
             const uint16_t *ce = p.codebook + int64_t(c) * D;
 #pragma unroll
-            for (int u = 0; u < D; ++u) ga = fmaf(h_to_f32(ce[u]), float(xs[j * D + u]), ga);
+            for (int u = 0; u < D; ++u)
+                ga = fmaf(h_to_f32(ce[u]), XF ? xsf[j * D + u] : float(xs[j * D + u]), ga);
         }
         acc = fmaf(h_to_f32(srow[gcur]), ga, acc);
     }
@@ -579,6 +705,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv_generic(const GemvParams p) {
 int launch_gemv_fast_d2(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
 int launch_gemv_fast_d4(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
 int launch_gemv_fast_d8(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
+int launch_gemv_fast_d8x(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
 
 // Launch helper: raises each kernel instance's dynamic-LDS cap as its launches need more.
 template <auto KERN, typename P>

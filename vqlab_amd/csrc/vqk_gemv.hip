@@ -36,9 +36,11 @@ int gemv_fill_params(const vqk_weights *w, const Geom &g, GemvParams *p) {
     return VQK_OK;
 }
 
-size_t gemv_fast_lds(const Geom &g) {
-    const size_t cb = cb_in_lds(g.D, g.BITS) ? (size_t(1) << g.BITS) * g.D * 2 : size_t(kGemvHybBytes);
-    return cb + size_t(g.NB) * (kBlock * g.D + 8) * 2;
+size_t gemv_fast_lds(const Geom &g, bool xf) {
+    const size_t cb = cb_in_lds(g.D, g.BITS) ? (size_t(1) << g.BITS) * g.D * 2
+                                              : size_t(gemv_hyb_bytes(xf));
+    // x: NB blocks of 32 * D values at a 16-byte padded stride
+    return cb + (xf ? size_t(g.NB) * (kBlock * g.D + 4) * 4 : size_t(g.NB) * (kBlock * g.D + 8) * 2);
 }
 
 int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
@@ -47,8 +49,13 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
     Geom g;
     int rc = make_geom(w, &g);
     if (rc) return rc;
+    const bool xf = (x_type & VQK_X_KEEP) != 0;
+    x_type &= ~int32_t(VQK_X_KEEP);
     if (!act_size(x_type) || !out_size(y_type))
         return set_error(VQK_EINVAL, "x/y type must be VQK_F16, VQK_BF16 or VQK_F32");
+    if (xf && g.D != 8)
+        return set_error(VQK_EINVAL, "VQK_X_KEEP is for d=8 modules (the float4-staged kernels); "
+                                     "d=%d kernels take x as fp16", g.D);
     if (!x || !y) return set_error(VQK_EINVAL, "x and y are required");
     if (N < 0 || T < 0 || xkrep < 1 || N != T * xkrep)
         return set_error(VQK_EINVAL, "pairs N=%lld must equal tokens T=%lld x xkrep=%lld",
@@ -66,7 +73,7 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
     p.y_type = y_type;
     p.y_stride = g.OUT;
     const int64_t chunk = (65535 / xkrep) * xkrep;   // grid.y limit, whole tokens per chunk
-    if (g.fast_ok) {
+    if (g.fast_ok && gemv_fast_lds(g, xf) <= size_t(kLdsBytes)) {
         const int rpw = kWave >> p.lpr_log2;
         const int64_t steps_total = N * ((g.OUT + rpw - 1) / rpw);   // wave steps overall
         const int64_t target_waves = 2048;                          // ~8 per CU
@@ -75,7 +82,7 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
         const int64_t per_wg = 4 * rpw * steps;
         p.steps = int32_t(steps);
         p.rows_per_wg = int32_t(per_wg);
-        const size_t smem = gemv_fast_lds(g);
+        const size_t smem = gemv_fast_lds(g, xf);
         for (int64_t n0 = 0; n0 < N; n0 += chunk) {
             const int64_t nn = N - n0 < chunk ? N - n0 : chunk;
             p.pair0 = int32_t(n0);
@@ -83,14 +90,17 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
             switch (g.D) {
                 case 2: rc = launch_gemv_fast_d2(p, g.BITS, g.gpb, grid, smem, st); break;
                 case 4: rc = launch_gemv_fast_d4(p, g.BITS, g.gpb, grid, smem, st); break;
-                default: rc = launch_gemv_fast_d8(p, g.BITS, g.gpb, grid, smem, st); break;
+                default:
+                    rc = xf ? launch_gemv_fast_d8x(p, g.BITS, g.gpb, grid, smem, st)
+                            : launch_gemv_fast_d8(p, g.BITS, g.gpb, grid, smem, st);
+                    break;
             }
             if (rc) return rc;
         }
         return VQK_OK;
     }
-    const size_t smem = size_t(g.IN) * 2;
-    if (smem > 160 * 1024) return set_error(VQK_ENOTIMPL, "IN=%lld too wide", (long long)g.IN);
+    const size_t smem = size_t(g.IN) * (xf ? 4 : 2);
+    if (smem > size_t(kLdsBytes)) return set_error(VQK_ENOTIMPL, "IN=%lld too wide", (long long)g.IN);
     for (int64_t n0 = 0; n0 < N; n0 += chunk) {
         const int64_t nn = N - n0 < chunk ? N - n0 : chunk;
         p.pair0 = int32_t(n0);
@@ -98,7 +108,10 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
         switch (g.D) {
             case 2: rc = launch_with_lds<k_gemv_generic<2>>(grid, dim3(kThreads), smem, st, p); break;
             case 4: rc = launch_with_lds<k_gemv_generic<4>>(grid, dim3(kThreads), smem, st, p); break;
-            default: rc = launch_with_lds<k_gemv_generic<8>>(grid, dim3(kThreads), smem, st, p); break;
+            default:
+                rc = xf ? launch_with_lds<k_gemv_generic<8, true>>(grid, dim3(kThreads), smem, st, p)
+                        : launch_with_lds<k_gemv_generic<8>>(grid, dim3(kThreads), smem, st, p);
+                break;
         }
         if (rc) return rc;
     }

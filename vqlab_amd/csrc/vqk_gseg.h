@@ -34,8 +34,6 @@
 
 namespace vqk {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
 struct SegParams {
     const uint32_t *codes;     // code rows as 32-code blocks of BITS words
     int64_t row_words;         // words per code row (NB * BITS)

@@ -10,8 +10,9 @@ namespace vqk {
 // Fills the weight-dependent fields of a GEMV parameter block.
 int gemv_fill_params(const vqk_weights *w, const Geom &g, GemvParams *p);
 
-// Dynamic LDS bytes of the fast GEMV kernel for geometry g.
-size_t gemv_fast_lds(const Geom &g);
+// Dynamic LDS bytes of the fast GEMV kernel for geometry g (xf: the wide-x
+// instances).
+size_t gemv_fast_lds(const Geom &g, bool xf = false);
 
 // Validates and launches the fused GEMV for N = T * xkrep pairs.
 int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,

@@ -187,7 +187,10 @@ def _switch_apply(x2, eidx, codes, codebook, scales, pack_bits, IN, xkrep, rowtb
                                              T.ptr(e), N, int(xkrep), T.ptr(y), T.act_type(y), wk,
                                              ws.value, T.stream(x2.device)), "VQSwitchLinear")
         else:
-            L.check(L.lib().vqk_moe_expert_gemv(ctypes.byref(w), T.ptr(x2), T.act_type(x2),
+            xt = T.act_type(x2)
+            if o.decode_bf16io and x2.dtype == torch.bfloat16 and codebook.shape[1] == 8:
+                xt |= L.VQK_X_KEEP             # as vqk_switch_apply: d8 takes bf16 x unrounded
+            L.check(L.lib().vqk_moe_expert_gemv(ctypes.byref(w), T.ptr(x2), xt,
                                                 x2.shape[0], T.ptr(e), N, int(xkrep), T.ptr(y),
                                                 T.act_type(y), T.stream(x2.device)), "VQSwitchLinear")
         return y
