@@ -98,6 +98,7 @@ struct DequantArgs {
     uint16_t *out;
     int64_t out_ld;          // elements per output row part (>= IN; columns past IN are zeros)
     int mode;                // kDqF16, kDqBF16 or kDqSplit
+    int cw_log2;             // code columns per workgroup = 1 << cw_log2 (<= 256)
 };
 
 // Code row of output row `orow`, or -1 for a dead skipzero row, an expert id
@@ -131,8 +132,11 @@ __device__ __forceinline__ void dq_entry(const uint16_t *cb, uint32_t c, uint16_
     }
 }
 
-// One thread per code column j, kDqRows output rows at a time (rows
-// blockIdx.y + i * gridDim.y of the stride): each phase -- code rows, codes,
+// One thread per code column j, kDqRows output rows at a time: a workgroup
+// is 2^cw_log2 columns x 256 / 2^cw_log2 row sets (the column count chosen to
+// divide the row: config 5's 640 codes per row left a sixth of 256-wide
+// workgroups idle), row set q taking rows q + i * GY of a stride of GY sets
+// (GY = gridDim.y x row sets per workgroup). Each phase -- code rows, codes,
 // scales, table entries, stores -- is issued for all of them before the next
 // waits, so a thread has kDqRows code-load -> gather chains in flight instead
 // of one (small weights are latency-bound; a large table with random codes is
@@ -145,10 +149,12 @@ constexpr int kDqRows = 4;
 enum : int { kCfPacked = 0, kCfU8 = 1, kCfU16 = 2 };
 template <int D, int CF>
 __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
-    const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int cw = 1 << a.cw_log2;
+    const int nrs = int(blockDim.x) >> a.cw_log2, rs = int(threadIdx.x) >> a.cw_log2;
+    const int64_t j = int64_t(blockIdx.x) * cw + (int(threadIdx.x) & (cw - 1));
     if (j * D >= a.out_ld) return;
     const bool pad = j >= a.NSUB;
-    const int64_t gy = gridDim.y;
+    const int64_t gy = int64_t(gridDim.y) * nrs;
     // where code j sits in a packed row: word wi, shift sh (a field never
     // leaves its 32-code block, so a second word is within the row)
     int64_t wi = 0;
@@ -204,7 +210,7 @@ __global__ void __launch_bounds__(256) k_dequant(DequantArgs a) {
             sc[i] = cr[i] >= 0 ? sc[i] : uint16_t(0);
         }
     };
-    for (int64_t o0 = blockIdx.y; o0 < a.rows; o0 += gy * kDqRows) {
+    for (int64_t o0 = int64_t(blockIdx.y) * nrs + rs; o0 < a.rows; o0 += gy * kDqRows) {
         int64_t cr[kDqRows];
         uint32_t c[kDqRows];
         uint16_t sc[kDqRows];
@@ -301,7 +307,18 @@ static int launch_dequant(const vqk_weights *w, const Geom &g, const uint32_t *e
     a.r0 = r0; a.rows = rows;
     a.out = out;
     if (rows == 0) return VQK_OK;
-    const dim3 grid = rows_grid(a.out_ld / g.D, rows, 4);
+    // the widest of 256 / 128 / 64 columns that leaves the fewest idle lanes
+    const int64_t cols = a.out_ld / g.D;
+    a.cw_log2 = 8;
+    for (int l = 7; l >= 6; --l) {
+        const int64_t waste = (cols + (1 << l) - 1) / (1 << l) * (1 << l) - cols;
+        const int64_t best = (cols + (1 << a.cw_log2) - 1) / (1 << a.cw_log2) * (1 << a.cw_log2) - cols;
+        if (waste < best) a.cw_log2 = l;
+    }
+    const int64_t nrs = 256 >> a.cw_log2;
+    int64_t gy = (rows + kDqRows * nrs - 1) / (kDqRows * nrs);
+    gy = gy < 1 ? 1 : (gy > 65535 ? 65535 : gy);
+    const dim3 grid(unsigned((cols + (1 << a.cw_log2) - 1) >> a.cw_log2), unsigned(gy), 1);
     const int cf = g.packed ? kCfPacked : (g.BITS == 8 ? kCfU8 : kCfU16);
     if (g.D == 2) launch_dq<2>(cf, grid, st, a);
     else if (g.D == 4) launch_dq<4>(cf, grid, st, a);
