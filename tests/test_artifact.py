@@ -211,3 +211,128 @@ def test_skipzero_weights_converts_state_dicts(tmp_path):
     bad[p + ".sz_codes"] = flat[p + ".sz_codes"][1:]
     with pytest.raises(ValueError, match="live rows"):
         skipzero_weights(bad, szmods)
+
+
+# ------------------------------------------------- tensor-parallel split
+def _sz_ondisk(rng, E, OUT, W, NG, dead):
+    """Expanded codes / scales with many dead rows (one expert all dead, one
+    all live) and their on-disk skipzero tensors (torch, CPU)."""
+    codes = rng.integers(0, 2**31, (E, OUT, W), dtype=np.int64).astype(np.uint32)
+    sc = (rng.standard_normal((E, OUT, NG)) * 0.1 + 1).astype(np.float16)
+    live = rng.random((E, OUT)) >= dead
+    live[1, :] = False
+    live[2, :] = True
+    codes[~live] = 0
+    sc[~live] = 0
+    sz = vo.skipzero_compact(codes, sc)
+    t = {".sz_codes": torch.from_numpy(sz["sz_codes"].view(np.int32)),
+         ".sz_scales": torch.from_numpy(sz["sz_scales"]),
+         ".sz_rowmask": torch.from_numpy(sz["sz_rowmask"]),
+         ".sz_shape": torch.from_numpy(sz["sz_shape"])}
+    return codes, sc, live, t
+
+
+@pytest.mark.parametrize("OUT,n", [(96, 2), (96, 4), (102, 2), (64, 1), (128, 8)])
+@pytest.mark.parametrize("leaf", ["gate_proj", "up_proj"])
+def test_skipzero_shard_rows_concat_equal_unsplit(OUT, n, leaf):
+    """skipzero_shard (vq_switch.py:5112-5147) on gate / up: each rank keeps
+    its output slice of every expert's rows, taken through the mask; the
+    ranks' converted modules, expanded and concatenated over OUT, are
+    byte-equal to the unsplit module, and their live rows add up (the
+    reference's test_sz_shard row-split check, on the tensors)."""
+    from vqlab_amd.vq_switch import skipzero_shard, skipzero_weights
+    rng = np.random.default_rng(OUT * 10 + n)
+    E, W, NG = 8, 24, 8
+    codes, sc, live, t = _sz_ondisk(rng, E, OUT, W, NG, 0.7)
+    p = f"model.layers.3.mlp.switch_mlp.{leaf}"
+    w = {p + k: v for k, v in t.items()}
+    w["model.layers.3.mlp.other"] = torch.ones(3)
+    mods = {p: {"experts": E, "out": OUT, "live_rows": int(live.sum())}}
+    gc, gs, total = [], [], 0
+    for rank in range(n):
+        wr, mr = skipzero_shard(dict(w), mods, rank, n)
+        assert mr[p]["out"] == OUT // n and mr[p]["experts"] == E
+        assert wr[p + ".sz_codes"].shape[0] == mr[p]["live_rows"]
+        assert wr[p + ".sz_shape"].tolist()[:2] == [E, OUT // n]
+        assert wr["model.layers.3.mlp.other"] is w["model.layers.3.mlp.other"]
+        total += mr[p]["live_rows"]
+        out = skipzero_weights(wr, mr)
+        rt = out[p + ".row_table"].numpy()
+        assert rt.shape == (E, OUT // n)
+        c = _np(out[p + ".codes"])
+        gc.append(np.where(rt[..., None] >= 0, c[np.maximum(rt, 0)], 0))
+        gs.append(np.where(rt[..., None] >= 0, _np(out[p + ".vq_scales"])[np.maximum(rt, 0)], 0))
+    assert total == int(live.sum())
+    assert np.array_equal(np.concatenate(gc, axis=1), codes)
+    assert np.array_equal(np.concatenate(gs, axis=1).view(np.uint16), sc.view(np.uint16))
+    # skipzero_weights(shard=) is skipzero_shard then the conversion
+    one = skipzero_weights(list(w.items()), mods, shard=(n - 1, n))
+    assert isinstance(one, list)
+    two = skipzero_weights(*skipzero_shard(dict(w), mods, n - 1, n))
+    assert all(torch.equal(v, two[k]) for k, v in one)
+
+
+def test_skipzero_shard_down_untouched_and_refusals():
+    """down_proj splits on its input axis: its skipzero tensors and entry
+    come back as they were once the cut is checked against the scale groups
+    and 32-code blocks; the refusals of skipzero_shard_modules
+    (vq_switch.py:5036-5075): OUT % n, an unaligned input cut, a down entry
+    without its geometry, a leaf with no split rule, a bad rank."""
+    from vqlab_amd.vq_switch import skipzero_shard
+    rng = np.random.default_rng(5)
+    E, IN = 4, 512
+    _, _, live, t = _sz_ondisk(rng, E, 96, 16, 8, 0.5)
+    geo = {"experts": E, "out": 96, "live_rows": int(live.sum()), "in": IN, "dim": 4,
+           "group": 64, "pack_bits": 12, "k": 4096}
+    dp = "model.layers.0.mlp.switch_mlp.down_proj"
+    wd = {dp + k: v for k, v in t.items()}
+    wr, mr = skipzero_shard(dict(wd), {dp: geo}, 1, 4)    # 128 inputs = 32 codes per rank
+    assert mr[dp] == geo and all(wr[k] is wd[k] for k in wd)
+    with pytest.raises(ValueError, match="not aligned"):
+        skipzero_shard(dict(wd), {dp: geo}, 0, 8)          # 16 codes per rank
+    with pytest.raises(ValueError, match="not aligned"):
+        skipzero_shard(dict(wd), {dp: geo}, 0, 3)
+    skipzero_shard(dict(wd), {dp: dict(geo, pack_bits=0)}, 0, 8)   # unpacked: groups only
+    with pytest.raises(KeyError, match="geometry"):
+        skipzero_shard(dict(wd), {dp: {"experts": E, "out": 96}}, 0, 2)
+    g = "model.layers.0.mlp.switch_mlp.gate_proj"
+    with pytest.raises(ValueError, match="does not divide"):
+        skipzero_shard({g + k: v for k, v in t.items()}, {g: geo}, 0, 5)
+    o = "model.layers.0.mlp.switch_mlp.gate_up_proj"
+    with pytest.raises(ValueError, match="no tensor split rule"):
+        skipzero_shard({o + k: v for k, v in t.items()}, {o: geo}, 0, 2)
+    with pytest.raises(ValueError, match="bad rank"):
+        skipzero_shard({g + k: v for k, v in t.items()}, {g: geo}, 2, 2)
+
+
+def test_load_artifact_rank_shards(tmp_path):
+    """load_artifact(shard=(rank, n)) and the config's vq_skipzero.shard:
+    the skipzero up_proj of the fixture comes back with the rank's 64 of its
+    128 rows per expert, row tables that expand to the slices of the
+    unsplit one; every other module is built whole."""
+    from vqlab_amd import artifact
+    cfg, mods = af.write(tmp_path, "sz_pack")
+    full = artifact.load_artifact(tmp_path, device="cpu")
+    p = next(iter(cfg["vq_skipzero"]["modules"]))
+    rt_full = full.modules[p].row_table.numpy()
+    for rank in range(2):
+        a = artifact.load_artifact(tmp_path, device="cpu", shard=(rank, 2))
+        m = a.modules[p]
+        assert m.output_dims == 64 and m.row_table.shape == (2, 64)
+        want = (rt_full[:, rank * 64:(rank + 1) * 64] >= 0)
+        assert np.array_equal(m.row_table.numpy() >= 0, want)
+        cf = _np(full.modules[p].codes)
+        cr = _np(m.codes)
+        rt = m.row_table.numpy()
+        sl = rt_full[:, rank * 64:(rank + 1) * 64]
+        assert np.array_equal(cr[rt[want]], cf[sl[want]])
+        for q, mod in a.modules.items():
+            if q != p and hasattr(mod, "output_dims"):
+                assert mod.output_dims == full.modules[q].output_dims
+    c2 = json.loads((tmp_path / "config.json").read_text())
+    c2["vq_skipzero"]["shard"] = {"rank": 1, "n": 2}
+    (tmp_path / "config.json").write_text(json.dumps(c2))
+    b = artifact.load_artifact(tmp_path, device="cpu")
+    assert b.modules[p].output_dims == 64
+    assert torch.equal(b.modules[p].row_table,
+                       artifact.load_artifact(tmp_path, device="cpu", shard=(1, 2)).modules[p].row_table)

@@ -25,6 +25,7 @@ import json
 import pathlib
 import re
 
+import numpy as np
 import torch
 
 from . import vq_pack
@@ -193,14 +194,139 @@ def _layout_match(modules, prefix):
     return hits[0]
 
 
-def convert_skipzero(weights, modules):
+# --------------------------------------------------- tensor-parallel split
+# Leaves split on their output rows (each rank keeps its slice of every
+# expert's rows) and on their input axis (rows stay whole), as the
+# reference's skipzero_shard does (vq_switch.py:5025-5026).
+SZ_ROW_SPLIT = ("gate_proj", "up_proj")
+SZ_IN_SPLIT = ("down_proj",)
+
+
+def skipzero_live(rowmask, E, OUT) -> np.ndarray:
+    """Bit-packed uint8 [E, ceil(OUT/8)] live-row mask (little bit order) ->
+    bool [E, OUT] (vq_switch.py:5029-5033); host side, the mask is small."""
+    rm = rowmask.cpu().numpy() if isinstance(rowmask, torch.Tensor) else np.asarray(rowmask)
+    rm = np.ascontiguousarray(rm, np.uint8).reshape(int(E), -1)
+    return np.unpackbits(rm, axis=-1, bitorder="little")[:, : int(OUT)].astype(bool)
+
+
+def _check_rank(rank, n):
+    if not (isinstance(n, int) and n >= 1 and isinstance(rank, int) and 0 <= rank < n):
+        raise ValueError(f"skipzero shard: bad rank/n {rank}/{n}")
+
+
+def skipzero_shard_modules(modules, rank, n, rowmask):
+    """Per-rank vq_skipzero entries for an n-way tensor split
+    (vq_switch.py:5036-5075): gate_proj / up_proj get out = OUT / n and
+    live_rows = the rank's live rows; down_proj entries come back unchanged
+    once the input-axis cut is checked to fall on scale-group (and, packed,
+    32-code block) boundaries, which needs the entry's vq_modules geometry
+    (in, dim, group, pack_bits). `rowmask(key)` returns a module's
+    sz_rowmask. ValueError for OUT % n != 0, an unaligned input cut or a
+    leaf with no split rule; KeyError for a down_proj entry without its
+    geometry."""
+    _check_rank(rank, n)
+    out = {}
+    for key, m in modules.items():
+        leaf = key.rsplit(".", 1)[-1]
+        E, OUT = int(m["experts"]), int(m["out"])
+        if leaf in SZ_ROW_SPLIT:
+            if OUT % n:
+                raise ValueError(f"skipzero shard: {key} OUT={OUT} does not divide into {n} ranks")
+            lo, hi = rank * OUT // n, (rank + 1) * OUT // n
+            live = skipzero_live(rowmask(key), E, OUT)[:, lo:hi]
+            out[key] = dict(m, out=OUT // n, live_rows=int(live.sum()))
+        elif leaf in SZ_IN_SPLIT:
+            try:
+                IN, D, G = int(m["in"]), int(m["dim"]), int(m.get("group", 64))
+            except KeyError:
+                raise KeyError(f"skipzero shard: {key} needs its vq_modules geometry "
+                               f"(in, dim, group, pack_bits) to check the input-axis cut") from None
+            pb = int(m.get("pack_bits") or 0)
+            cut = IN // n
+            ok = IN % n == 0 and cut % G == 0 and cut % D == 0 and (not pb or (cut // D) % 32 == 0)
+            if not ok:
+                raise ValueError(f"skipzero shard: {key} IN={IN} split {n} ways is not aligned to "
+                                 f"group {G}" + (f" and 32-code blocks (d={D}, {pb}-bit words)"
+                                                 if pb else ""))
+            out[key] = dict(m)
+        else:
+            raise ValueError(f"skipzero shard: no tensor split rule for {key} (leaf {leaf!r})")
+    return out
+
+
+def _shard_rows(parts, E, OUT, rank, n):
+    """One row-split module's on-disk skipzero tensors (suffix -> tensor) ->
+    the rank's: compact rows of its output slice (taken through the mask, in
+    the compact order), the sliced mask and the shape record."""
+    lo, hi = rank * OUT // n, (rank + 1) * OUT // n
+    live = skipzero_live(parts[".sz_rowmask"], E, OUT)
+    pos = (np.cumsum(live.reshape(-1)) - 1).reshape(E, OUT)
+    keep = torch.from_numpy(pos[:, lo:hi][live[:, lo:hi]].astype(np.int64))
+    out = dict(parts)
+    for suf in (".sz_codes", ".sz_scales"):
+        t = parts[suf]
+        out[suf] = t.index_select(0, keep.to(t.device))
+    mask = parts[".sz_rowmask"]
+    rm = torch.from_numpy(np.packbits(live[:, lo:hi], axis=-1, bitorder="little"))
+    out[".sz_rowmask"] = rm.to(mask.device) if isinstance(mask, torch.Tensor) else rm
+    if ".sz_shape" in parts:
+        shp = torch.as_tensor(parts[".sz_shape"]).to(torch.int32).clone()
+        shp.view(-1)[1] = hi - lo
+        out[".sz_shape"] = shp
+    return out
+
+
+def skipzero_shard(weights, modules, rank, n):
+    """Rank `rank` of an n-way tensor split of on-disk skipzero tensors,
+    before convert_skipzero (the reference's skipzero_shard,
+    vq_switch.py:5112-5147): gate_proj / up_proj keep the rank's output rows
+    of every expert (sz_codes / sz_scales rows taken through the mask,
+    sz_rowmask and sz_shape sliced); down_proj is left as it is (its input
+    axis is cut like any expanded module's). Returns (weights of the same
+    kind as given, per-rank modules as skipzero_shard_modules)."""
+    _check_rank(rank, n)
+    pairs = list(weights.items()) if isinstance(weights, dict) else list(weights)
+    d = dict(pairs)
+    pre = [k[: -len(".sz_rowmask")] for k in d if k.endswith(".sz_rowmask")]
+    keyed = {}
+    for q in pre:
+        key = next((k for k in modules if k == q), None)
+        if key is None:
+            want = _strip(q)
+            hits = [k for k in modules if _strip(k) == want]
+            if len(hits) != 1:
+                raise KeyError(f"skipzero tensors for {q!r} match {len(hits)} vq_skipzero entries")
+            key = hits[0]
+        keyed[q] = key
+    by_key = {key: q for q, key in keyed.items()}
+    smods = skipzero_shard_modules({key: modules[key] for key in by_key}, rank, n,
+                                   lambda key: d[by_key[key] + ".sz_rowmask"])
+    for q, key in keyed.items():
+        if key.rsplit(".", 1)[-1] not in SZ_ROW_SPLIT:
+            continue
+        m = modules[key]
+        parts = {suf: d[q + suf] for suf in SZ_SUFFIXES if q + suf in d}
+        for suf, t in _shard_rows(parts, int(m["experts"]), int(m["out"]), rank, n).items():
+            d[q + suf] = t
+    mods = dict(modules)
+    mods.update(smods)
+    out = [(k, d[k]) for k, _ in pairs]
+    return (dict(out) if isinstance(weights, dict) else out), mods
+
+
+def convert_skipzero(weights, modules, shard=None):
     """On-disk skipzero tensors -> what VQSwitchLinear(row_table=...) loads
     (the reference's skipzero_weights, vq_switch.py:4988-5013): each module's
     {p}.sz_* tensors become {p}.codes / {p}.vq_scales (compact rows) and
     {p}.row_table; every other tensor passes through unchanged, and weights
     without skipzero tensors come back as given. `weights` is a dict or a
     list of (key, tensor) pairs (the same kind is returned); `modules` maps
-    module prefixes to their vq_skipzero entries (experts, out)."""
+    module prefixes to their vq_skipzero entries (experts, out). `shard` =
+    (rank, n) applies skipzero_shard first, with the unsplit modules."""
+    if shard is not None and any(k.endswith(".sz_rowmask") for k in
+                                 (weights if isinstance(weights, dict) else dict(weights))):
+        weights, modules = skipzero_shard(weights, modules, *shard)
     pairs = list(weights.items()) if isinstance(weights, dict) else list(weights)
     groups, kept = {}, []
     for key, val in pairs:
@@ -221,7 +347,7 @@ def convert_skipzero(weights, modules):
     return dict(kept) if isinstance(weights, dict) else kept
 
 
-def _build(path, kind, spec, rd, sz_mods, device, out_dtype):
+def _build(path, kind, spec, rd, sz_mods, device, out_dtype, shard=None):
     q = _tensor_prefix(path, rd.smap)
     g = int(spec["group"])
     k, d = int(spec["k"]), int(spec["dim"])
@@ -250,6 +376,14 @@ def _build(path, kind, spec, rd, sz_mods, device, out_dtype):
         E = int(szm.get("experts", spec["experts"]))
         OUT = int(szm.get("out", spec["out"]))
         parts = {suf: rd.get(q + suf) for suf in SZ_SUFFIXES if q + suf in rd}
+        if shard is not None:
+            # the rank's output rows (gate / up); down_proj stays whole once
+            # its input cut is checked (vq_switch.py:5112-5147)
+            entry = dict(spec, experts=E, out=OUT)
+            skipzero_shard_modules({path: entry}, *shard, lambda _: parts[".sz_rowmask"])
+            if path.rsplit(".", 1)[-1] in SZ_ROW_SPLIT:
+                parts = _shard_rows(parts, E, OUT, *shard)
+                OUT //= shard[1]
         codes, sc, table = skipzero_module(q, parts, E, OUT)
         _expect(q + ".sz_codes", codes, (codes.shape[0], cols), cdt)
         _expect(q + ".sz_scales", sc, (codes.shape[0], IN // g), (torch.float16,))
@@ -331,21 +465,29 @@ class Artifact:
             attach(model, p, m)
 
 
-def load_artifact(path, device="cuda", only=None) -> Artifact:
+def load_artifact(path, device="cuda", only=None, shard=None) -> Artifact:
     """Builds every VQ module `path`'s config.json declares (or those whose
     config path is in `only`), reading each module's tensors from its shard
-    and moving them to `device` one module at a time."""
+    and moving them to `device` one module at a time. `shard` = (rank, n)
+    (default: the config's vq_skipzero.shard {"rank", "n"}, as the
+    reference's loader reads it) builds rank `rank` of an n-way tensor split
+    of the skipzero modules: gate_proj / up_proj with the rank's OUT / n
+    output rows of every expert; down_proj whole, after checking that its
+    input axis cuts on scale-group and code-block boundaries."""
     root = pathlib.Path(path)
     cfg = read_config(root)
     rd = _Reader(shard_map(root))
-    sz_mods = (cfg.get("vq_skipzero") or {}).get("modules") or {}
+    szc = cfg.get("vq_skipzero") or {}
+    sz_mods = szc.get("modules") or {}
+    if shard is None and szc.get("shard"):
+        shard = (int(szc["shard"]["rank"]), int(szc["shard"]["n"]))
     out_dtype = _model_dtype(cfg)
     mods, used = {}, set()
     try:
         for p, kind, spec in module_specs(cfg):
             if only is not None and p not in only:
                 continue
-            mods[p] = _build(p, kind, spec, rd, sz_mods, device, out_dtype)
+            mods[p] = _build(p, kind, spec, rd, sz_mods, device, out_dtype, shard)
             q = _tensor_prefix(p, rd.smap)
             used.update(k for k in rd.smap if k.startswith(q + "."))
     finally:

@@ -218,12 +218,21 @@ def skipzero_row_table(rowmask, E, OUT):
     return t.to(dev) if dev is not None else t
 
 
-def skipzero_weights(weights, modules):
+def skipzero_weights(weights, modules, shard=None):
     """On-disk skipzero tensors -> what VQSwitchLinear(row_table=...) loads
     (vq_switch.py:4988-5013); the conversion lives with the artifact loader
-    (artifact.convert_skipzero), which applies the same per-module checks."""
+    (artifact.convert_skipzero), which applies the same per-module checks.
+    `shard` = (rank, n) takes the rank's tensor-parallel slice first
+    (artifact.skipzero_shard, vq_switch.py:5112-5147)."""
     from .artifact import convert_skipzero
-    return convert_skipzero(weights, modules)
+    return convert_skipzero(weights, modules, shard)
+
+
+def skipzero_shard(weights, modules, rank, n):
+    """Rank `rank` of an n-way split of on-disk skipzero tensors
+    (vq_switch.py:5112-5147); see artifact.skipzero_shard."""
+    from .artifact import skipzero_shard as _shard
+    return _shard(weights, modules, rank, n)
 
 
 # ---------------------------------------------------------------- module
