@@ -57,17 +57,20 @@ extern "C" {
 #define VQK_VIA_F16 0x100
 
 /* Wide-activation flag, OR'd into the x_type of vqk_moe_expert_gemv /
- * vqk_dense_gemv for d = 8 modules only (VQK_EINVAL otherwise): x enters the
- * products unrounded -- bf16 and fp32 activations widened exactly to fp32,
- * each codebook half widened to fp32, fp32 multiply-adds -- instead of being
- * narrowed to fp16 first. It is the arithmetic of the reference's
- * float4-staged d8 decode kernels (vq_switch.py:1440-1458, 1576-1586, and
- * _SRC_FUSED_PACKED_D8 after 1316), which VQ_DECODE_BF16IO feeds bf16 x
- * uncast (vq_switch.py:4412-4417, 5306); its d2 / d4 decode kernels stage x
- * as fp16 and round it in-kernel, and its grouped prefill converts bf16 x to
- * fp16 on stage-in even under VQ_GEMMSEG_BF16IO (vq_switch.py:4364-4372), so
- * those paths take no flag. vqk_switch_apply sets it by itself (see
- * vqk_options.decode_bf16io). No other entry point accepts it. */
+ * vqk_dense_gemv for d = 4 and d = 8 modules (VQK_EINVAL at d = 2): x enters
+ * the products unrounded -- bf16 and fp32 activations widened exactly to
+ * fp32, each codebook half widened to fp32, fp32 multiply-adds -- instead of
+ * being narrowed to fp16 first. It is the arithmetic of the reference's
+ * float-staged decode kernels -- the unpacked d4 kernel for K <= 1024
+ * (_SRC_FUSED, vq_switch.py:106-150) and the d8 kernels for K > 1024
+ * (153-237, 1316-1354, 1424-1660) -- which VQ_DECODE_BF16IO feeds bf16 x
+ * uncast (vq_switch.py:4412-4417, 5306); its other decode kernels (d2,
+ * packed or K > 1024 d4, d8 with K <= 1024) stage x as fp16 and round it
+ * in-kernel, and its grouped prefill converts bf16 x to fp16 on stage-in
+ * even under VQ_GEMMSEG_BF16IO (vq_switch.py:4364-4372). vqk_switch_apply
+ * sets it by that rule (see vqk_options.decode_bf16io), and
+ * vqk_linear_apply for d8 linears, which the reference runs through
+ * decode-then-matmul in x's type. No other entry point accepts it. */
 #define VQK_X_KEEP 0x200
 
 /* One VQ-coded linear, or a stack of E expert linears sharing one codebook
@@ -303,8 +306,10 @@ int vqk_gemmseg_fits(int32_t D, int64_t K, int32_t G, int32_t pack_bits,
  *                      runs the fused GEMV (default 32)
  *   decode_bf16io      VQ_DECODE_BF16IO: 0 (default) = the fused routed path
  *                      rounds its outputs through fp16 (VQK_VIA_F16); 1 = once
- *                      into y's type, and at d = 8 bf16 x enters the GEMV
- *                      unrounded (VQK_X_KEEP)
+ *                      into y's type, and where the reference's kernel
+ *                      stages x as float (unpacked d4 K <= 1024, d8
+ *                      K > 1024) bf16 x enters the GEMV unrounded
+ *                      (VQK_X_KEEP)
  *   prefill_bf16io     VQ_GEMMSEG_BF16IO: the single output rounding for the
  *                      grouped GEMM path; x is still converted to fp16 on
  *                      stage-in, as the reference's does (vq_switch.py:
@@ -346,7 +351,10 @@ int vqk_switch_apply(const vqk_weights *w, const void *x, int32_t x_type,
  * (vqk_dense_gemv) for at most dense_fused_max_n rows when the shape has a
  * fused kernel (vqk_dense_fits), else the decode-then-GEMM path
  * (vqk_dense_gemm). Outputs are rounded once into y's type, as the
- * reference's dense kernels write x's dtype directly. */
+ * reference's dense kernels write x's dtype directly. The GEMV takes d2 / d4
+ * x as fp16, as the reference's halfN-staged dense kernels do, and d8 x
+ * unrounded (VQK_X_KEEP; the reference has no fused d8 dense kernel and
+ * multiplies in x's type). */
 int vqk_linear_apply_workspace(const vqk_weights *w, int64_t N, const vqk_options *o,
                                size_t *bytes);
 int vqk_linear_apply(const vqk_weights *w, const void *x, int32_t x_type, int64_t N,

@@ -379,10 +379,10 @@ def test_options_crowded_rule_is_switchable(L):
         assert (ws.value > 0) == grouped
 
 
-def test_wide_x_flag_is_d8_gemv_only(L):
-    """VQK_X_KEEP (x enters the d=8 GEMV unrounded) has the header's value;
-    a d=4 module, whose reference kernels stage x as fp16, and the grouped
-    GEMM refuse it before anything reaches a device."""
+def test_wide_x_flag_is_d4_d8_gemv_only(L):
+    """VQK_X_KEEP (x enters the d=4 / d=8 GEMV unrounded) has the header's
+    value; a d=2 module, whose reference kernels all stage x as fp16, and the
+    grouped GEMM refuse it before anything reaches a device."""
     import ctypes
     txt = (ROOT / "include" / "vqk.h").read_text()
     m = re.search(r"#define\s+VQK_X_KEEP\s+(0x[0-9a-fA-F]+)", txt)
@@ -390,15 +390,16 @@ def test_wide_x_flag_is_d8_gemv_only(L):
     assert L.VQK_X_KEEP & (L.VQK_VIA_F16 | 0xff) == 0
     w = L.VQKWeights()
     w.codes, w.code_cols, w.code_type, w.pack_bits = 1 << 20, 16 * 12, L.VQK_U32, 12
-    w.codebook, w.K, w.D, w.group = 1 << 24, 4096, 4, 64
-    w.scales, w.E, w.OUT, w.IN = 1 << 28, 8, 256, 2048
+    w.codebook, w.K, w.D, w.group = 1 << 24, 4096, 2, 64
+    w.scales, w.E, w.OUT, w.IN = 1 << 28, 8, 256, 1024
     xt = L.VQK_BF16 | L.VQK_X_KEEP
     rc = L.lib().vqk_moe_expert_gemv(ctypes.byref(w), 1 << 32, xt, 1, 1 << 33, 1, 1, 1 << 34,
                                      L.VQK_F32, None)
-    assert rc == L.VQK_EINVAL and "d=8" in L.last_error()
+    assert rc == L.VQK_EINVAL and "d=2" in L.last_error()
     w.E = 1
     rc = L.lib().vqk_dense_gemv(ctypes.byref(w), 1 << 32, xt, 0, 1 << 34, L.VQK_F32, None)
-    assert rc == L.VQK_EINVAL and "d=8" in L.last_error()
+    assert rc == L.VQK_EINVAL and "d=2" in L.last_error()
+    w.code_cols, w.D, w.IN = 16 * 12, 4, 2048
     ws = ctypes.c_size_t()
     L.check(L.lib().vqk_grouped_gemm_workspace(ctypes.byref(w), 64, ctypes.byref(ws)))
     rc = L.lib().vqk_grouped_gemm(ctypes.byref(w), 1 << 32, xt, 64, 1 << 33, 64, 1, 1 << 34,

@@ -277,30 +277,45 @@ def _wide_x(rng, IN):
     return torch.from_numpy(np.stack([big, tiny]).astype(np.float32)).to("cuda", torch.bfloat16)
 
 
+def _float_staged(D, K, packed):
+    """The reference's kernels that take bf16 x unrounded under
+    VQ_DECODE_BF16IO: unpacked d4 with K <= 1024 (`_SRC_FUSED`,
+    vq_switch.py:106-150, 3172-3175), d8 with K > 1024 (`_D8_TG_MAX_K`,
+    2781; 153-237, 1316-1354, 1424-1660)."""
+    return (D == 8 and K > 1024) or (D == 4 and not packed and K <= 1024)
+
+
 @pytest.mark.parametrize("case", [
-    # (E, OUT, IN, K, G, packed): c3 gate/up rows (14-bit table partly in
+    # (D, E, OUT, IN, K, G, packed): c3 gate/up rows (14-bit table partly in
     # LDS, 4 scale groups per block); a 12-bit table in LDS with groups of two
     # blocks; 13 bits at 64 blocks per row (the fp16 kernels' LDS cannot hold
-    # that table part and row: they take the generic kernel); ragged unpacked
-    # rows (generic kernel)
-    (6, 1024, 4096, 16384, 64, True),
-    (4, 512, 2048, 4096, 512, True),
-    (3, 128, 16384, 8192, 64, True),
-    (3, 300, 1000, 256, 8, False),
+    # that table part and row: they take the generic kernel); d8 with a
+    # 256-entry table (the reference's half-staged d8 kernel: the dispatch
+    # rounds) on ragged unpacked rows (generic kernel); unpacked d4 with
+    # uint16 and uint8 codes (the reference's float-staged d4 kernel); packed
+    # ragged d4 (half-staged in the reference; generic wide-x kernel here)
+    (8, 6, 1024, 4096, 16384, 64, True),
+    (8, 4, 512, 2048, 4096, 512, True),
+    (8, 3, 128, 16384, 8192, 64, True),
+    (8, 3, 300, 1000, 256, 8, False),
+    (4, 6, 512, 2048, 1024, 64, False),
+    (4, 4, 256, 1024, 256, 64, False),
+    (4, 3, 200, 1000, 1024, 8, True),
 ])
-def test_expert_gemv_d8_wide_x(case):
+def test_expert_gemv_wide_x(case):
     """VQK_X_KEEP: bf16 x beyond fp16's range and below its normal range
-    enters the d8 GEMV unrounded, fp32 products with the widened table, as
-    the reference's float4-staged d8 kernels take it under VQ_DECODE_BF16IO
-    (vq_switch.py:1440-1458, 4412-4417). Bar: |y - ref| <= 3e-5 * (|x| @ |W|^T)
-    against the float64 fused formula (oracle weights="exact"), an fp32
-    accumulation bar that fp16 staging of either row misses (checked)."""
+    enters the GEMV unrounded, fp32 products with the widened table, as the
+    reference's float-staged kernels take it under VQ_DECODE_BF16IO
+    (vq_switch.py:4412-4417). Bar: |y - ref| <= 3e-5 * (|x| @ |W|^T) against
+    the float64 fused formula (oracle weights="exact"), an fp32 accumulation
+    bar that fp16 staging of either row misses (checked). The dispatch sets
+    the flag exactly where the reference's kernel stages x as float."""
     import ctypes
     from vqlab_amd import _lib as L, _torch as TT, vq_switch as VS
-    E, OUT, IN, K, G, packed = case
+    D, E, OUT, IN, K, G, packed = case
     print(f"wide x {case}", flush=True)
-    rng = np.random.default_rng(sum(case[:5]))
-    m = make_module(rng, E, OUT, IN, 8, K, G=G, packed=packed)
+    rng = np.random.default_rng(sum(case[:6]))
+    m = make_module(rng, E, OUT, IN, D, K, G=G, packed=packed)
     codes, cb, sc = to_device(m)
     x = _wide_x(rng, IN)
     k = 3
@@ -327,18 +342,48 @@ def test_expert_gemv_d8_wide_x(case):
     i = np.unravel_index(np.argmax(err - bar), err.shape)
     assert np.isfinite(y).all() and (err <= bar).all(), (i, y[i], ref[i], bar[i])
     # the fp16-staged kernel misses the bar: row 0 overflows, row 1 loses bits
-    y16 = run(L.VQK_BF16).cpu().numpy().astype(np.float64)
+    y16t = run(L.VQK_BF16)
+    y16 = y16t.cpu().numpy().astype(np.float64)
     assert not np.isfinite(y16[:k]).all()
     assert (np.abs(y16[k:] - ref[k:]) > bar[k:]).any()
-    # the dispatch sets the flag for bf16 x under decode_bf16io (one output
-    # rounding), and the out_dtype form runs the same kernel
+    # the dispatch under decode_bf16io: the flag where the reference stages x
+    # as float, fp16 staging elsewhere; the out_dtype form runs the same kernel
     o = L.options(decode_bf16io=1, crowded_grouped=0)
     yo = VS._switch_apply(x, eidx, codes, cb, sc, m["pack_bits"], IN, k, out_dtype=torch.float32,
                           opts=o)
-    assert torch.equal(yo, yt)
     yb = VS._switch_apply(x, eidx, codes, cb, sc, m["pack_bits"], IN, k, opts=o)
     assert yb.dtype == torch.bfloat16
-    assert (np.abs(_np(yb) - ref) <= bar + np.abs(ref) * 2.0 ** -8).all()
+    if _float_staged(D, K, packed):
+        assert torch.equal(yo, yt)
+        assert (np.abs(_np(yb) - ref) <= bar + np.abs(ref) * 2.0 ** -8).all()
+    else:
+        assert torch.equal(yo.view(torch.int32), y16t.view(torch.int32))   # bits: row 0 holds NaN
+        assert not np.isfinite(_np(yb)[:k]).all()
+
+
+@pytest.mark.parametrize("N", [1, 4, 32])
+def test_dense_linear_d8_takes_bf16_x_unrounded(N):
+    """VQLinear at d8: the reference has no fused d8 dense kernel (dense_fits
+    refuses d8, vq_switch.py:3290-3306) and multiplies in x's dtype at every N
+    (vq_dense.py:288-294); the GEMV rows (N <= 32) take bf16 x unrounded too,
+    so activations beyond fp16's range stay finite. Bar as above."""
+    from vqlab_amd.vq_dense import VQLinear
+    print(f"dense d8 N={N}", flush=True)
+    rng = np.random.default_rng(70 + N)
+    OUT, IN, K = 384, 2048, 4096
+    m = make_module(rng, 1, OUT, IN, 8, K)
+    codes, cb, sc = to_device(m)
+    lin = VQLinear(codes[0], cb, sc[0], group_size=64, pack_bits=m["pack_bits"], in_features=IN)
+    x = torch.cat([_wide_x(rng, IN) for _ in range((N + 1) // 2)])[:N]
+    y = lin(x)
+    assert y.dtype == torch.bfloat16
+    xf = x.float().cpu().numpy()
+    ref = vo.expert_gemv(xf, np.zeros(N, np.int64), m["codes"], m["codebook"], m["scales"], 64,
+                         weights="exact")
+    absref = vo.expert_gemv(np.abs(xf), np.zeros(N, np.int64), m["codes"], np.abs(m["codebook"]),
+                            m["scales"], 64, weights="exact")
+    assert torch.isfinite(y).all()
+    assert (np.abs(_np(y) - ref) <= 3e-5 * absref + np.abs(ref) * 2.0 ** -8).all()
 
 
 def test_switch_linear_module_and_errors():

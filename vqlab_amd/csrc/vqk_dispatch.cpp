@@ -44,6 +44,16 @@ bool switch_grouped(const vqk_weights *w, const Geom &g, int64_t N, const vqk_op
     return vqk_gemmseg_fits(g.D, g.K, g.G, w->pack_bits, g.IN) != 0;
 }
 
+// The reference's decode kernels that stage x as float, and so take bf16 x
+// unrounded under VQ_DECODE_BF16IO (vq_switch.py:4412-4417): the unpacked d4
+// kernel for K <= 1024 (`_SRC_FUSED`, vq_switch.py:106-150, chosen at
+// 3172-3175) and every d8 kernel past the threadgroup-table limit K > 1024
+// (`_D8_TG_MAX_K`, 2781; kernels at 153-237, 1316-1354, 1424-1660). The rest
+// (d2, packed or large-K d4, d8 with K <= 1024) stage halfN and round.
+bool float_staged(const Geom &g) {
+    return (g.D == 8 && g.K > 1024) || (g.D == 4 && !g.packed && g.K <= 1024);
+}
+
 bool linear_fused(const Geom &g, int64_t N, const vqk_options &o) {
     return N <= o.dense_fused_max_n && vqk_dense_fits(g.K, g.IN, g.G, g.D) != 0;
 }
@@ -101,9 +111,7 @@ int vqk_switch_apply(const vqk_weights *w, const void *x, int32_t x_type, int64_
     const int32_t yt = via ? (y_type | VQK_VIA_F16) : y_type;
     if (grouped)
         return vqk_grouped_gemm(w, x, x_type, T, eidx, N, xkrep, y, yt, workspace, ws_bytes, stream);
-    // the d8 decode kernels take that bf16 x unrounded (float4 staging,
-    // vq_switch.py:4412-4417); d2 / d4 ones stage it as fp16
-    const int32_t xt = keep && g.D == 8 ? (x_type | VQK_X_KEEP) : x_type;
+    const int32_t xt = keep && float_staged(g) ? (x_type | VQK_X_KEEP) : x_type;
     return vqk_moe_expert_gemv(w, x, xt, T, eidx, N, xkrep, y, yt, stream);
 }
 
@@ -128,7 +136,14 @@ int vqk_linear_apply(const vqk_weights *w, const void *x, int32_t x_type, int64_
     if (rc) return rc;
     if (N < 0) return set_error(VQK_EINVAL, "N=%lld", (long long)N);
     const vqk_options o = resolved(opt);
-    if (linear_fused(g, N, o)) return vqk_dense_gemv(w, x, x_type, N, y, y_type, stream);
+    if (linear_fused(g, N, o)) {
+        // the reference has no fused d8 dense kernel (dense_fits refuses d8,
+        // vq_switch.py:3290-3306): its d8 linears run decode-then-matmul in
+        // x's type at every N (vq_dense.py:288-294), so bf16 / fp32 x is
+        // taken unrounded here too
+        const int32_t xt = g.D == 8 && x_type != VQK_F16 ? (x_type | VQK_X_KEEP) : x_type;
+        return vqk_dense_gemv(w, x, xt, N, y, y_type, stream);
+    }
     return vqk_dense_gemm(w, x, x_type, N, y, y_type, workspace, ws_bytes, stream);
 }
 

@@ -28,11 +28,11 @@
 // aligned, NB > 64, unusual scale groups) run on the generic kernel: one
 // thread per row, walking its codes.
 //
-// Wide-x instances (XF, d = 8 only, x_type flag VQK_X_KEEP): x is staged in
-// LDS as fp32 -- bf16 and fp32 activations exactly -- and each table entry's
-// halves are widened to fp32 and multiplied with fp32 FMAs, the arithmetic of
-// the reference's float4-staged d8 kernels (vq_switch.py:1440-1458,
-// 1576-1586, and the packed d8 thread-per-row kernel after 1316) that
+// Wide-x instances (XF, d = 4 and 8, x_type flag VQK_X_KEEP): x is staged
+// in LDS as fp32 -- bf16 and fp32 activations exactly -- and each table
+// entry's halves are widened to fp32 and multiplied with fp32 FMAs, the
+// arithmetic of the reference's float-staged kernels (the d4 `_SRC_FUSED`,
+// vq_switch.py:106-150; the d8 ones at 153-237, 1316-1354, 1424-1660) that
 // VQ_DECODE_BF16IO feeds bf16 x unrounded (vq_switch.py:4412-4417). Lanes
 // read their block's activations from LDS per code (256 fp32 values per
 // block would not fit in registers), and a table too large for LDS keeps
@@ -706,6 +706,8 @@ int launch_gemv_fast_d2(const GemvParams &p, int bits, int gpb, dim3 grid, size_
 int launch_gemv_fast_d4(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
 int launch_gemv_fast_d8(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
 int launch_gemv_fast_d8x(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
+int launch_gemv_fast_d4x(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem, hipStream_t st);
+bool gemv_fast_d4x_has(int bits);   // a fast wide-x d=4 instance exists for this width
 
 // Launch helper: raises each kernel instance's dynamic-LDS cap as its launches need more.
 template <auto KERN, typename P>

@@ -53,9 +53,9 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
     x_type &= ~int32_t(VQK_X_KEEP);
     if (!act_size(x_type) || !out_size(y_type))
         return set_error(VQK_EINVAL, "x/y type must be VQK_F16, VQK_BF16 or VQK_F32");
-    if (xf && g.D != 8)
-        return set_error(VQK_EINVAL, "VQK_X_KEEP is for d=8 modules (the float4-staged kernels); "
-                                     "d=%d kernels take x as fp16", g.D);
+    if (xf && g.D == 2)
+        return set_error(VQK_EINVAL, "VQK_X_KEEP is for d=4 and d=8 modules (the float-staged "
+                                     "kernels); d=2 kernels take x as fp16");
     if (!x || !y) return set_error(VQK_EINVAL, "x and y are required");
     if (N < 0 || T < 0 || xkrep < 1 || N != T * xkrep)
         return set_error(VQK_EINVAL, "pairs N=%lld must equal tokens T=%lld x xkrep=%lld",
@@ -73,7 +73,9 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
     p.y_type = y_type;
     p.y_stride = g.OUT;
     const int64_t chunk = (65535 / xkrep) * xkrep;   // grid.y limit, whole tokens per chunk
-    if (g.fast_ok && gemv_fast_lds(g, xf) <= size_t(kLdsBytes)) {
+    // wide x at d=4: fast instances for the unpacked widths, else the generic kernel
+    const bool fast_x = !xf || g.D == 8 || gemv_fast_d4x_has(g.BITS);
+    if (g.fast_ok && fast_x && gemv_fast_lds(g, xf) <= size_t(kLdsBytes)) {
         const int rpw = kWave >> p.lpr_log2;
         const int64_t steps_total = N * ((g.OUT + rpw - 1) / rpw);   // wave steps overall
         const int64_t target_waves = 2048;                          // ~8 per CU
@@ -89,7 +91,10 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
             const dim3 grid(unsigned((g.OUT + per_wg - 1) / per_wg), unsigned(nn), 1);
             switch (g.D) {
                 case 2: rc = launch_gemv_fast_d2(p, g.BITS, g.gpb, grid, smem, st); break;
-                case 4: rc = launch_gemv_fast_d4(p, g.BITS, g.gpb, grid, smem, st); break;
+                case 4:
+                    rc = xf ? launch_gemv_fast_d4x(p, g.BITS, g.gpb, grid, smem, st)
+                            : launch_gemv_fast_d4(p, g.BITS, g.gpb, grid, smem, st);
+                    break;
                 default:
                     rc = xf ? launch_gemv_fast_d8x(p, g.BITS, g.gpb, grid, smem, st)
                             : launch_gemv_fast_d8(p, g.BITS, g.gpb, grid, smem, st);
@@ -107,7 +112,10 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
         const dim3 grid(unsigned((g.OUT + kThreads - 1) / kThreads), unsigned(nn), 1);
         switch (g.D) {
             case 2: rc = launch_with_lds<k_gemv_generic<2>>(grid, dim3(kThreads), smem, st, p); break;
-            case 4: rc = launch_with_lds<k_gemv_generic<4>>(grid, dim3(kThreads), smem, st, p); break;
+            case 4:
+                rc = xf ? launch_with_lds<k_gemv_generic<4, true>>(grid, dim3(kThreads), smem, st, p)
+                        : launch_with_lds<k_gemv_generic<4>>(grid, dim3(kThreads), smem, st, p);
+                break;
             default:
                 rc = xf ? launch_with_lds<k_gemv_generic<8, true>>(grid, dim3(kThreads), smem, st, p)
                         : launch_with_lds<k_gemv_generic<8>>(grid, dim3(kThreads), smem, st, p);

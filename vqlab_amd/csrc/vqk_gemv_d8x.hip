@@ -1,6 +1,7 @@
-// Wide-x fast VQ GEMV instances for d=8 (x_type flag VQK_X_KEEP): x staged
-// as fp32, fp32 products with the widened table entries. Same widths and
-// scale groups as the fp16-x instances.
+// Wide-x fast VQ GEMV instances (x_type flag VQK_X_KEEP): x staged as fp32,
+// fp32 products with the widened table entries. d=8: the widths and scale
+// groups of the fp16-x instances; d=4: the unpacked uint8 / uint16 rows (the
+// reference's float-staged d4 kernel takes unpacked codes only).
 #include "vqk_gemv.h"
 
 namespace vqk {
@@ -25,6 +26,22 @@ int launch_gemv_fast_d8x(const GemvParams &p, int bits, int gpb, dim3 grid, size
     }
 #undef VQK_CASE
     return set_error(VQK_ENOTIMPL, "no fast wide-x d=8 kernel for bits=%d, %d groups/block", bits, gpb);
+}
+
+template <int BITS, int GPB>
+static int go_d4x(const GemvParams &p, dim3 grid, size_t smem, hipStream_t st) {
+    return launch_with_lds<k_gemv_fast<4, BITS, GPB, true>>(grid, dim3(kThreads), smem, st, p);
+}
+
+bool gemv_fast_d4x_has(int bits) { return bits == 8 || bits == 16; }
+
+int launch_gemv_fast_d4x(const GemvParams &p, int bits, int gpb, dim3 grid, size_t smem,
+                         hipStream_t st) {
+    if (bits == 8 && gpb == 1) return go_d4x<8, 1>(p, grid, smem, st);
+    if (bits == 8 && gpb == 2) return go_d4x<8, 2>(p, grid, smem, st);
+    if (bits == 16 && gpb == 1) return go_d4x<16, 1>(p, grid, smem, st);
+    if (bits == 16 && gpb == 2) return go_d4x<16, 2>(p, grid, smem, st);
+    return set_error(VQK_ENOTIMPL, "no fast wide-x d=4 kernel for bits=%d, %d groups/block", bits, gpb);
 }
 
 }  // namespace vqk

@@ -162,6 +162,15 @@ def _gemmseg(x2, eidx, codes, codebook, scales, pack_bits, IN, xkrep, rowtbl=Non
     return y
 
 
+def _float_staged(codebook, pack_bits) -> bool:
+    """The reference's decode kernels that stage x as float and take bf16 x
+    unrounded under VQ_DECODE_BF16IO: unpacked d4 with K <= 1024, d8 with
+    K > 1024 (vq_switch.py:106-150, 2781, 3172-3185); libvqk's
+    vqk_switch_apply applies the same rule."""
+    K, D = int(codebook.shape[0]), int(codebook.shape[1])
+    return (D == 8 and K > 1024) or (D == 4 and not pack_bits and K <= 1024)
+
+
 def _switch_apply(x2, eidx, codes, codebook, scales, pack_bits, IN, xkrep, rowtbl=None,
                   out_dtype=None, opts=None):
     """VQSwitchLinear's dispatch through vqk_switch_apply with the module
@@ -188,8 +197,8 @@ def _switch_apply(x2, eidx, codes, codebook, scales, pack_bits, IN, xkrep, rowtb
                                              ws.value, T.stream(x2.device)), "VQSwitchLinear")
         else:
             xt = T.act_type(x2)
-            if o.decode_bf16io and x2.dtype == torch.bfloat16 and codebook.shape[1] == 8:
-                xt |= L.VQK_X_KEEP             # as vqk_switch_apply: d8 takes bf16 x unrounded
+            if o.decode_bf16io and x2.dtype == torch.bfloat16 and _float_staged(codebook, pack_bits):
+                xt |= L.VQK_X_KEEP             # as vqk_switch_apply does
             L.check(L.lib().vqk_moe_expert_gemv(ctypes.byref(w), T.ptr(x2), xt,
                                                 x2.shape[0], T.ptr(e), N, int(xkrep), T.ptr(y),
                                                 T.act_type(y), T.stream(x2.device)), "VQSwitchLinear")
