@@ -405,3 +405,44 @@ def test_wide_x_flag_is_d4_d8_gemv_only(L):
     rc = L.lib().vqk_grouped_gemm(ctypes.byref(w), 1 << 32, xt, 64, 1 << 33, 64, 1, 1 << 34,
                                   L.VQK_F32, 1 << 35, ws.value, None)
     assert rc == L.VQK_EINVAL and "type" in L.last_error()
+
+
+def test_empty_calls_need_no_pointers(L):
+    """A call with no rows, pairs or tokens returns VQK_OK without reading a
+    pointer (an empty tensor's pointer is NULL) or touching a device: the
+    GEMVs, the GEMMs, both dispatchers, the dequant and the MoE layer."""
+    import ctypes
+    w = L.VQKWeights()
+    w.codes, w.code_cols, w.code_type, w.pack_bits = 1 << 20, 16 * 12, L.VQK_U32, 12
+    w.codebook, w.K, w.D, w.group = 1 << 24, 4096, 4, 64
+    w.scales, w.E, w.OUT, w.IN = 1 << 28, 8, 256, 2048
+    lib, bf = L.lib(), L.VQK_BF16
+    o = L.options()
+    assert lib.vqk_moe_expert_gemv(ctypes.byref(w), None, bf, 0, None, 0, 1, None, bf, None) == L.VQK_OK
+    assert lib.vqk_grouped_gemm(ctypes.byref(w), None, bf, 0, None, 0, 1, None, bf, None, 0,
+                                None) == L.VQK_OK
+    assert lib.vqk_switch_apply(ctypes.byref(w), None, bf, 0, None, 0, 1, None, bf, None, 0,
+                                ctypes.byref(o), None) == L.VQK_OK
+    assert lib.vqk_dequant(ctypes.byref(w), 0, 0, None, None) == L.VQK_OK
+    assert lib.vqk_dequant_experts(ctypes.byref(w), None, 0, None, None) == L.VQK_OK
+    w.E = 1
+    assert lib.vqk_dense_gemv(ctypes.byref(w), None, bf, 0, None, bf, None) == L.VQK_OK
+    assert lib.vqk_dense_gemm(ctypes.byref(w), None, bf, 0, None, bf, None, 0, None) == L.VQK_OK
+    assert lib.vqk_linear_apply(ctypes.byref(w), None, bf, 0, None, bf, None, 0, ctypes.byref(o),
+                                None) == L.VQK_OK
+    # rows with NULL pointers are still refused
+    assert lib.vqk_dense_gemv(ctypes.byref(w), None, bf, 1, None, bf, None) == L.VQK_EINVAL
+    assert lib.vqk_dequant(ctypes.byref(w), 0, 1, None, None) == L.VQK_EINVAL
+
+    def proj(E, OUT, IN, base):
+        p = L.VQKWeights()
+        p.codes, p.code_cols, p.code_type, p.pack_bits = base, (IN // 4 + 31) // 32 * 12, L.VQK_U32, 12
+        p.codebook, p.K, p.D, p.group = base + (1 << 26), 4096, 4, 64
+        p.scales, p.E, p.OUT, p.IN = base + (1 << 27), E, OUT, IN
+        return p
+    ws_ = [proj(256, 512, 2048, 1 << 30), proj(256, 512, 2048, 2 << 30), proj(256, 2048, 512, 3 << 30)]
+    d = L.VQKMoeDesc()
+    d.gate, d.up, d.down = (ctypes.pointer(p) for p in ws_)
+    d.top_k, d.norm_topk = 8, 1
+    assert lib.vqk_moe_decode_layer(ctypes.byref(d), None, bf, 0, None, None, bf, None, None, None,
+                                    0, None) == L.VQK_OK

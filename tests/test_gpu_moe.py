@@ -491,3 +491,25 @@ def test_moe_one_launch_special_logits(case):
     ref, _, _ = vo.moe_layer(x.float().cpu().numpy(), lg[None], _spec(projs["gate"]),
                              _spec(projs["up"]), _spec(projs["down"]), k, h_round=np.float16)
     assert_close(y.float().cpu().numpy(), ref, what=f"special logits {case}")
+
+
+def test_empty_batches():
+    """No tokens in: every module returns an empty result of the right shape
+    and launches nothing (empty tensors have NULL pointers)."""
+    from vqlab_amd.vq_dense import VQLinear
+    rng = np.random.default_rng(61)
+    E, H, I, k = 16, 256, 128, 4
+    blk, projs, _, _ = _block(rng, E, H, I, 4, 1024, k, shared=True)
+    x = torch.zeros((0, H), dtype=torch.bfloat16, device="cuda")
+    lg = torch.zeros((0, E), dtype=torch.float32, device="cuda")
+    y, ids, w = blk.fused(x, lg, return_route=True)
+    assert y.shape == (0, H) and ids.shape == (0, k) and w.shape == (0, k)
+    assert blk.composed(x, lg).shape == (0, H)
+    g = blk.switch_mlp.gate_proj
+    yg = g(x[:, None, None, :], torch.zeros((0, k), dtype=torch.int32, device="cuda"))
+    assert yg.shape == (0, k, 1, I)
+    m = projs["down"]
+    codes, cb, sc = to_device(m)
+    lin = VQLinear(codes[0], cb, sc[0], group_size=64, pack_bits=m["pack_bits"], in_features=I)
+    assert lin(torch.zeros((0, I), dtype=torch.bfloat16, device="cuda")).shape == (0, H)
+    torch.cuda.synchronize()

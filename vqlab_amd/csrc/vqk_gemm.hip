@@ -465,10 +465,12 @@ static int launch_gemm(const GemmParams &p, const Geom &g, dim3 grid, hipStream_
     }
 }
 
-static int check_acts(const void *x, int32_t x_type, const void *y, int32_t y_type) {
+// Types always; x and y only when there are rows (an empty call touches
+// neither, so NULL -- an empty tensor's pointer -- is accepted then).
+static int check_acts(const void *x, int32_t x_type, const void *y, int32_t y_type, int64_t rows) {
     if (!act_size(x_type) || !out_size(y_type))
         return set_error(VQK_EINVAL, "x/y type must be VQK_F16, VQK_BF16 or VQK_F32");
-    if (!x || !y) return set_error(VQK_EINVAL, "x and y are required");
+    if ((!x || !y) && rows > 0) return set_error(VQK_EINVAL, "x and y are required");
     return VQK_OK;
 }
 
@@ -602,7 +604,7 @@ int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_t 
     if (rc) return rc;
     if (g.E != 1) return set_error(VQK_EINVAL, "dense GEMM takes one linear (E=1), got E=%lld",
                                    (long long)g.E);
-    if ((rc = check_acts(x, x_type, y, y_type))) return rc;
+    if ((rc = check_acts(x, x_type, y, y_type, N))) return rc;
     if (N < 0 || N > INT32_MAX) return set_error(VQK_EINVAL, "N=%lld", (long long)N);
     if (N == 0) return VQK_OK;
     if (N <= kSegDenseMaxN && seg_fits(g, w, x)) {
@@ -639,7 +641,7 @@ int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_
     Geom g;
     int rc = make_geom(w, &g);
     if (rc) return rc;
-    if ((rc = check_acts(x, x_type, y, y_type))) return rc;
+    if ((rc = check_acts(x, x_type, y, y_type, N))) return rc;
     if (!eidx && N > 0) return set_error(VQK_EINVAL, "eidx is required");
     if (N < 0 || T < 0 || xkrep < 1 || N != T * xkrep)
         return set_error(VQK_EINVAL, "pairs N=%lld must equal tokens T=%lld x xkrep=%lld",
@@ -647,11 +649,11 @@ int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_
     if (N > INT32_MAX / 2) return set_error(VQK_ENOTIMPL, "N=%lld pairs is too many", (long long)N);
     if (g.E > kMaxSortExperts)
         return set_error(VQK_ENOTIMPL, "grouped GEMM sorts at most %d experts", kMaxSortExperts);
+    if (N == 0) return VQK_OK;
     size_t need = 0;
     vqk_grouped_gemm_workspace(w, N, &need);
     if (!workspace || ws_bytes < need)
         return set_error(VQK_ENOSPACE, "workspace %zu B < %zu B", ws_bytes, need);
-    if (N == 0) return VQK_OK;
     const bool seg = seg_fits(g, w, x);
     const int tok = seg ? seg_tile_rows(w, N, g.E) : kSegTok;
     const int64_t mt = group_max_tiles(N, g.E, tok);

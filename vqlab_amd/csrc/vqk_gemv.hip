@@ -56,7 +56,7 @@ int launch_gemv(const vqk_weights *w, const void *x, int32_t x_type, int64_t T,
     if (xf && g.D == 2)
         return set_error(VQK_EINVAL, "VQK_X_KEEP is for d=4 and d=8 modules (the float-staged "
                                      "kernels); d=2 kernels take x as fp16");
-    if (!x || !y) return set_error(VQK_EINVAL, "x and y are required");
+    if ((!x || !y) && N > 0) return set_error(VQK_EINVAL, "x and y are required");
     if (N < 0 || T < 0 || xkrep < 1 || N != T * xkrep)
         return set_error(VQK_EINVAL, "pairs N=%lld must equal tokens T=%lld x xkrep=%lld",
                          (long long)N, (long long)T, (long long)xkrep);

@@ -1833,10 +1833,10 @@ int vqk_moe_decode_layer(const vqk_moe_desc *m, const void *x, int32_t x_type, i
     if (rc) return rc;
     if (!act_size(x_type) || !out_size(y_type))
         return set_error(VQK_EINVAL, "x/y type must be VQK_F16, VQK_BF16 or VQK_F32");
+    if (T == 0) return VQK_OK;              // an empty batch touches no pointer
     if (!x || !y || !logits) return set_error(VQK_EINVAL, "x, logits and y are required");
     if (!workspace || ws_bytes < pl.lay.total)
         return set_error(VQK_ENOSPACE, "workspace %zu B < %zu B", ws_bytes, pl.lay.total);
-    if (T == 0) return VQK_OK;
     MoeParams &p = pl.p;
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     p.ids = reinterpret_cast<int32_t *>(ws + pl.lay.ids);

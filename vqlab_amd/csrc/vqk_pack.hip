@@ -370,7 +370,7 @@ int vqk_dequant(const vqk_weights *w, int64_t r0, int64_t rows, uint16_t *out, v
     Geom g;
     int rc = make_geom(w, &g);
     if (rc) return rc;
-    if (!out) return set_error(VQK_EINVAL, "vqk_dequant: out is NULL");
+    if (!out && rows > 0) return set_error(VQK_EINVAL, "vqk_dequant: out is NULL");
     if (r0 < 0 || rows < 0 || r0 + rows > g.E * g.OUT)
         return set_error(VQK_EINVAL, "rows [%lld, %lld) outside the module's %lld rows",
                          (long long)r0, (long long)(r0 + rows), (long long)(g.E * g.OUT));
@@ -382,7 +382,7 @@ int vqk_dequant_experts(const vqk_weights *w, const uint32_t *eidx, int64_t ne, 
     Geom g;
     int rc = make_geom(w, &g);
     if (rc) return rc;
-    if (!out || (!eidx && ne > 0) || ne < 0)
+    if ((!out && ne > 0) || (!eidx && ne > 0) || ne < 0)
         return set_error(VQK_EINVAL, "vqk_dequant_experts: bad arguments");
     return launch_dequant(w, g, eidx, 0, ne * g.OUT, out, hipStream_t(stream));
 }
