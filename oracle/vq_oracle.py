@@ -43,7 +43,8 @@ Pinning (what checks each function; see tests/test_oracle.py):
                    output, gate logits of +-1000 give 2x and 1x) in both
                    rounding modes.
   bf16_round,      torch's own float32 -> bfloat16 / float16 conversions
-  fp16_round       over 200k random bit patterns, bf16 ties and specials.
+  fp16_round,      over 200k random bit patterns, bf16 ties and specials
+  f32_to_bf16_bits (bit patterns, signed zeros included; NaN by its rule).
   skipzero         reference golden sha256 prefixes (sz_codes, sz_scales,
                    sz_rowmask, sz_shape) + cumsum brute force for the table.
   tile_meta        the reference test's double loop, restated.
@@ -285,14 +286,22 @@ def sigmoid(v):
     return 1.0 / (1.0 + np.exp(-v))
 
 
+def f32_to_bf16_bits(u) -> np.ndarray:
+    """float32 bit patterns (uint32) -> bfloat16 bit patterns (uint16): round
+    to nearest even on the bits; a NaN keeps its sign and top payload bits
+    with the quiet bit set."""
+    u = np.asarray(u, np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    return np.where(nan, (u >> 16) | 0x40, r).astype(np.uint16)
+
+
 def bf16_round(v) -> np.ndarray:
     """Values -> the float64 values of their bfloat16 roundings: one RNE of
     the float32 value to 8 significand bits (what `.astype(bfloat16)` does to
     an fp32 array); NaN stays NaN."""
-    u = np.asarray(v, np.float64).astype(np.float32).view(np.uint32).astype(np.uint64)
-    nan = (u & 0x7FFFFFFF) > 0x7F800000
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
-    r = np.where(nan, (u >> 16) | 0x40, r)
+    u = np.asarray(v, np.float64).astype(np.float32).view(np.uint32)
+    r = f32_to_bf16_bits(u)
     return (r.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 

@@ -266,6 +266,31 @@ def test_expert_gemv_unpacked_and_bad_ids():
     assert (y[2] == 0).all()
 
 
+def test_f32_to_bf16_conversion_bits():
+    """The library's fp32 -> bf16 conversion (every bf16 output and weight)
+    against the oracle's bit formulation: every sign and exponent with the
+    mantissas at and around each rounding boundary (ties to even, carries into
+    the exponent, the largest finite values, denormals), signalling and quiet
+    NaN payloads, and 2^20 random patterns."""
+    from vq_cases import hooks
+    from vqlab_amd import _torch as TT
+    rng = np.random.default_rng(5)
+    se = (np.arange(512, dtype=np.uint32) << 23)
+    mant = np.uint32([0, 1, 0x7FFF, 0x8000, 0x8001, 0xFFFF, 0x10000, 0x17FFF, 0x18000, 0x18001,
+                      0x3FFFFF, 0x400000, 0x400001, 0x7F7FFF, 0x7F8000, 0x7FFFFF])
+    mant = np.concatenate([mant, rng.integers(0, 1 << 23, 48, dtype=np.uint64).astype(np.uint32)])
+    grid = (se[:, None] | mant[None, :]).reshape(-1)
+    rand = rng.integers(0, 2**32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    u = np.concatenate([grid, rand])
+    x = torch.from_numpy(u.view(np.int32)).cuda().view(torch.float32)
+    y = torch.empty(u.size, dtype=torch.int16, device="cuda")
+    assert hooks().vqk__test_f32_to_bf16(x.data_ptr(), y.data_ptr(), u.size, TT.stream(x.device)) == 0
+    got = y.cpu().numpy().view(np.uint16)
+    want = vo.f32_to_bf16_bits(u)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, [(hex(int(u[i])), hex(int(got[i])), hex(int(want[i]))) for i in bad[:5]]
+
+
 # ------------------------------------------------- wide x (VQK_X_KEEP, d=8)
 def _wide_x(rng, IN):
     """Two bf16 token rows that fp16 staging cannot hold: row 0 reaches

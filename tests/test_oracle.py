@@ -471,6 +471,13 @@ def test_rounding_helpers_match_torch():
     tb = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
     assert np.array_equal(vo.bf16_round(v)[fin], tb[fin].astype(np.float64))
     assert np.isnan(vo.bf16_round(v)[~fin]).all()
+    # the bit patterns too (signed zeros, infinities), and NaN keeps sign and
+    # top payload with the quiet bit (torch returns one canonical NaN instead)
+    tbits = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    ob = vo.f32_to_bf16_bits(v.view(np.uint32))
+    assert np.array_equal(ob[fin], tbits[fin])
+    nan_in = np.uint32([0x7F800001, 0xFF800001, 0x7FC00000, 0x7FFFFFFF, 0xFFBFFFFF, 0x7F80FFFF])
+    assert vo.f32_to_bf16_bits(nan_in).tolist() == [0x7FC0, 0xFFC0, 0x7FC0, 0x7FFF, 0xFFFF, 0x7FC0]
     th = torch.from_numpy(v).to(torch.float16).float().numpy()
     with np.errstate(invalid="ignore"):
         assert np.array_equal(vo.fp16_round(v)[fin], th[fin].astype(np.float64))

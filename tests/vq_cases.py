@@ -84,7 +84,9 @@ def hooks():
     vqk__test_l1_spins(n) -> previous bound of the one-launch layer's waits;
     vqk__test_l1_mode(m) -> previous mode (0 one launch where it applies,
     1 never); vqk__test_moe_path(desc*, T, int32*) -> status, the path a layer
-    call takes (0 two fused kernels, 1 sliced GEMVs, 2 grouped, 3 one launch)."""
+    call takes (0 two fused kernels, 1 sliced GEMVs, 2 grouped, 3 one launch);
+    vqk__test_f32_to_bf16(x*, y*, n, stream) -> status, the library's fp32 ->
+    bf16 conversion applied to n device values."""
     global _HOOKS
     if _HOOKS is None:
         import ctypes
@@ -94,7 +96,10 @@ def hooks():
                                 ("vqk__test_l1_mode", ctypes.c_int, [ctypes.c_int]),
                                 ("vqk__test_moe_path", ctypes.c_int32,
                                  [ctypes.POINTER(L.VQKMoeDesc), ctypes.c_int64,
-                                  ctypes.POINTER(ctypes.c_int32)])):
+                                  ctypes.POINTER(ctypes.c_int32)]),
+                                ("vqk__test_f32_to_bf16", ctypes.c_int,
+                                 [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                  ctypes.c_void_p])):
             f = getattr(lib, name)
             f.restype, f.argtypes = res, args
         _HOOKS = lib

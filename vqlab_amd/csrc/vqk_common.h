@@ -86,11 +86,14 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
 }
 
 // Round to nearest even; NaN stays NaN (quieted).
+// fp32 -> bf16, round to nearest even, NaN kept NaN with its top payload
+// bits and the quiet bit set: gfx950's v_cvt_pk_bf16_f32 (what the compiler
+// emits for this cast), which gives exactly the integer formulation
+// ((u + 0x7fff + lsb) >> 16; NaN: (u >> 16) | 0x40) on every one of the 2^32
+// inputs, denormals included (vqk__test_f32_to_bf16 and its GPU test check
+// the special classes).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return uint16_t(u >> 16);
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ float h_to_f32(uint16_t h) {

@@ -1,8 +1,11 @@
-// Measurement probe (test hook, not part of include/vqk.h): the random-gather
-// rate an MI355X sustains from an L2-resident table -- the access the decode
-// kernels make for codebook entries beyond their LDS part. Each lane reads
-// `inflight` random 16-byte entries per round, then consumes them.
-// bench.py --workload gather reports the rates at several waves per CU.
+// Measurement probe and test hooks (not part of include/vqk.h).
+// vqk__probe_gather: the random-gather rate an MI355X sustains from an
+// L2-resident table -- the access the decode kernels make for codebook
+// entries beyond their LDS part. Each lane reads `inflight` random 16-byte
+// entries per round, then consumes them. bench.py --workload gather reports
+// the rates at several waves per CU.
+// vqk__test_f32_to_bf16: the library's fp32 -> bf16 conversion (every bf16
+// output and weight goes through it), element by element.
 #include "vqk_common.h"
 
 namespace vqk {
@@ -26,6 +29,11 @@ __global__ void __launch_bounds__(256) k_probe_gather(const u32x4 *table, uint32
         for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].w;
     }
     sink[blockIdx.x * 256u + threadIdx.x] = acc;
+}
+
+__global__ void __launch_bounds__(256) k_test_f32_to_bf16(const float *x, uint16_t *y, int64_t n) {
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256)
+        y[i] = f32_to_bf16(x[i]);
 }
 
 }  // namespace vqk
@@ -54,3 +62,12 @@ int vqk__probe_gather(const void *table, uint32_t table_bytes, int wgs, int infl
 }
 
 }  // extern "C"
+
+extern "C" int vqk__test_f32_to_bf16(const float *x, uint16_t *y, int64_t n, void *stream) {
+    if (n < 0 || ((!x || !y) && n > 0)) return vqk::set_error(VQK_EINVAL, "bad arguments");
+    if (n == 0) return VQK_OK;
+    const int64_t blocks = (n + 255) / 256;
+    const dim3 grid{unsigned(blocks < 4096 ? blocks : 4096), 1u, 1u}, block{256u, 1u, 1u};
+    hipLaunchKernelGGL(vqk::k_test_f32_to_bf16, grid, block, 0, hipStream_t(stream), x, y, n);
+    return vqk::hip_status(hipGetLastError(), "bf16 conversion launch");
+}
