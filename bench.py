@@ -1,7 +1,7 @@
 """Benchmark of the VQ MoE decode layer on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload c1|c2|c3|c3b4|c4|c4t16|c4survey|c4t16survey|c5|gather]
+                    [--workload c1|c2|c3|c3b4|c4|c4t16|c4capped|c4t16capped|c5|gather]
 
 Default workload: a Qwen3.6-35B-A3B-shaped MoE
 decode layer -- hidden 2048, 256 experts of intermediate 512, top-8 softmax
@@ -17,7 +17,7 @@ step's own logits. The timed steps are captured once in a HIP graph and
 replayed; HIP events on the launch stream bracket the replay.
 
 value = packed-weight GB/s: bytes of the codes and scales of the experts the
-router touched (SURVEY 8(d) first term), summed over every layer call, over
+router touched, summed over every layer call, over
 the timed wall time. roofline uses the layer call's total algorithmic bytes
 (codes + scales + codebooks + activations) over its event-timed duration.
 cpu_baseline: the reference's decode-then-matmul of the same layer on the
@@ -75,14 +75,15 @@ WORKLOADS = {
                   layers=2, dead=0.2, kind="mtp",
                   desc="MTP verify batch on the config-3 layer, T=16, 20% skipzero rows "
                        "(BASELINE configs[3])"),
-    # config 4 on SURVEY 8(d)'s routing: each touched expert gets 1..min(8, T)
-    # of the batch's tokens, no token repeats an expert (mtp_logits)
-    "c4survey": dict(H=4096, E=512, I=1024, k=10, shared=True, d=8, K=16384, bits=14, T=64,
-                     layers=2, dead=0.2, kind="mtp", routing="survey",
+    # config 4 on capped routing, the MTP verify batch's: each touched expert
+    # gets 1..min(8, T) of the batch's tokens, no token repeats an expert
+    # (mtp_logits)
+    "c4capped": dict(H=4096, E=512, I=1024, k=10, shared=True, d=8, K=16384, bits=14, T=64,
+                     layers=2, dead=0.2, kind="mtp", routing="capped",
                      desc="MTP verify batch on the config-3 layer, T=64, 20% skipzero rows, "
                           "each touched expert 1..8 tokens (BASELINE configs[3])"),
-    "c4t16survey": dict(H=4096, E=512, I=1024, k=10, shared=True, d=8, K=16384, bits=14, T=16,
-                        layers=2, dead=0.2, kind="mtp", routing="survey",
+    "c4t16capped": dict(H=4096, E=512, I=1024, k=10, shared=True, d=8, K=16384, bits=14, T=16,
+                        layers=2, dead=0.2, kind="mtp", routing="capped",
                         desc="MTP verify batch on the config-3 layer, T=16, 20% skipzero rows, "
                              "each touched expert 1..8 tokens (BASELINE configs[3])"),
     # measurement probe: the random-gather rate of an L2-resident table
@@ -152,8 +153,9 @@ def expert_bytes(w):
 
 def mtp_logits(rng, T, E, k, cap=8):
     """Router logits [T, E] (fp32) whose top-k is an MTP verify batch's routing
-    as SURVEY 8(d) draws it: experts are taken in random order, each with a
-    uniform count of 1..min(cap, T) tokens, until the T*k pairs are placed;
+    (config 4: experts receive 1..8 tokens each): experts are taken in random
+    order, each with a uniform count of 1..min(cap, T) tokens, until the T*k
+    pairs are placed;
     each expert's tokens are the least-loaded ones that still need experts
     (never a token twice), so every token gets exactly k distinct experts.
     Selected logits lie in [4, 5), the rest are N(0, 1) clipped below 3."""
@@ -423,7 +425,7 @@ def run_mtp(torch, dev, a, w):
         layers.append(VQSparseMoeBlock(VQSwitchGLU(gp, up, dn), k, True, sh, sg))
     total = a.warmup + a.steps
     xs = [torch.randn((T, H), device=dev, generator=g).to(torch.bfloat16) for _ in range(L)]
-    if w.get("routing") == "survey":
+    if w.get("routing") == "capped":
         rng = np.random.default_rng(4321)
         logits = torch.from_numpy(np.stack([np.stack([mtp_logits(rng, T, E, k) for _ in range(L)])
                                             for _ in range(total)])).to(dev)
@@ -729,8 +731,8 @@ def _summary(name, body):
 
 
 # every BASELINE config beside the headline: (workload, timed steps)
-EXTRA_WORKLOADS = [("c1", 20), ("c3", 20), ("c3b4", 10), ("c4t16", 10), ("c4t16survey", 10),
-                   ("c4", 8), ("c4survey", 8), ("c5", 5)]
+EXTRA_WORKLOADS = [("c1", 20), ("c3", 20), ("c3b4", 10), ("c4t16", 10), ("c4t16capped", 10),
+                   ("c4", 8), ("c4capped", 8), ("c5", 5)]
 
 
 def extra_workloads(torch, dev, a):

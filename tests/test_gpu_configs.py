@@ -138,11 +138,11 @@ def _oracle_specs(blk, d=D3, bits=BITS3):
 def _check_layer(blk, T, seed, k=TOPK3, rows=None, E=E3, H=H3, routing="iid"):
     """One fused layer call on T tokens; the oracle checks tokens `rows`
     (all by default) in both rounding modes, and the routing exactly.
-    routing "survey": logits whose top-k gives each touched expert 1..8 of
+    routing "capped": logits whose top-k gives each touched expert 1..8 of
     the batch's tokens (bench.mtp_logits), else i.i.d. N(0, 1)."""
     rng = np.random.default_rng(seed)
     x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to("cuda", torch.bfloat16)
-    if routing == "survey":
+    if routing == "capped":
         from bench import mtp_logits
         lg = mtp_logits(rng, T, E, k)
     else:
@@ -236,15 +236,15 @@ def test_c4_verify_batch_full_shape(c4_layer, T):
 
 
 @pytest.mark.parametrize("T", [16, 64])
-def test_c4_verify_batch_survey_routing(c4_layer, T):
-    """Config 4 on the survey's MTP routing: each touched expert receives
+def test_c4_verify_batch_capped_routing(c4_layer, T):
+    """Config 4 on its MTP verify routing: each touched expert receives
     1..min(8, T) of the batch's tokens and no token repeats an expert (about
     34 touched experts at T = 16, 140 at T = 64, against ~370 for i.i.d.
     logits at T = 64), so the grouped tiles hold several rows each. The
     oracle checks 12 tokens at T = 64, all at T = 16."""
-    print(f"c4 survey routing T={T}", flush=True)
+    print(f"c4 capped routing T={T}", flush=True)
     rows = None if T <= 16 else [0, 3, 9, 15, 20, 27, 33, 38, 44, 51, 57, 63]
-    _check_layer(c4_layer, T, 4100 + T, rows=rows, routing="survey")
+    _check_layer(c4_layer, T, 4100 + T, rows=rows, routing="capped")
 
 
 # ------------------------------------------------------------------ c5

@@ -78,7 +78,7 @@ def test_skipzero_matches_reference_golden(fx, gold):
 def test_widths_at_baseline_shapes():
     assert vo.bits_for_k(256) == 8 and vo.bits_for_k(4096) == 12
     assert vo.bits_for_k(16384) == 14 and vo.bits_for_k(65536) == 16
-    # SURVEY shapes: c2 gate/up NSUB 512 -> 192, down NSUB 128 -> 48;
+    # benchmark shapes: c2 gate/up NSUB 512 -> 192, down NSUB 128 -> 48;
     # c3 NSUB 512 -> 224, 128 -> 56; c5 NSUB 640 at 16 bits == 640 u16.
     assert vo.words_per_row(512, 12) == 192 and vo.words_per_row(128, 12) == 48
     assert vo.words_per_row(512, 14) == 224 and vo.words_per_row(128, 14) == 56
@@ -579,11 +579,11 @@ def test_embed_rows_is_gather_of_full_dequant():
     assert np.array_equal(got.view(np.uint16), full[ids].view(np.uint16))
 
 
-def test_mtp_logits_follow_the_survey_routing():
+def test_mtp_logits_follow_the_capped_routing():
     """bench.mtp_logits (the config-4 benchmark's and tests' MTP routing):
     under the oracle's routing every token gets k distinct experts, every
-    touched expert 1..min(8, T) tokens, and the touched-expert count is the
-    survey's (~140 of 512 at T = 64)."""
+    touched expert 1..min(8, T) tokens, and about 140 of 512 experts are
+    touched at T = 64."""
     from bench import mtp_logits
     rng = np.random.default_rng(21)
     for T, lo, hi in ((4, 8, 40), (16, 25, 60), (64, 110, 170)):
