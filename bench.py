@@ -1,7 +1,7 @@
 """Benchmark of the VQ MoE decode layer on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload c1|c2|c3|c3b4|c4|c4t16|c4capped|c4t16capped|c5|gather]
+                    [--workload c1|c2|c3|c3b4|c4|c4t16|c4capped|c4t16capped|c5|gather|stream]
 
 Default workload: a Qwen3.6-35B-A3B-shaped MoE
 decode layer -- hidden 2048, 256 experts of intermediate 512, top-8 softmax
@@ -40,6 +40,11 @@ fp32 matvec on the host, one thread and all cores.
 --workload c5: dense VQ prefill, x [2048, 5120]
 through VQLinear 5120->17408 then 17408->5120 (d8, K=65536 uint16 codes);
 value = TFLOP/s of the two GEMMs, roofline against the fp16 MFMA peak.
+
+--workload gather / stream: measurement probes (libvqk test hooks outside the
+ABI): the random 16-byte gather rate from an L2-resident table, and the
+fastest one-launch streaming read of config 1's weight bytes (the floor of a
+GEMV that reads them in one launch).
 """
 from __future__ import annotations
 
@@ -89,6 +94,10 @@ WORKLOADS = {
     # measurement probe: the random-gather rate of an L2-resident table
     "gather": dict(kind="gather",
                    desc="random 16-byte gathers from a 256 KB / 1 MB L2-resident table (probe)"),
+    # measurement probe: one launch that only streams config 1's weight bytes
+    "stream": dict(kind="stream", bytes=4096 * 2048 + 4096 * 64 * 2, layers=120,
+                   desc="streaming read of config 1's codes + scales (8.9 MB) per launch, "
+                        "120 rotating buffers (probe)"),
     "c5": dict(N=2048, H=5120, F=17408, d=8, K=65536, kind="prefill",
                desc="Dense Qwen3.8-27B-shaped VQ prefill: 5120x17408 then 17408x5120, "
                     "x [2048, 5120] (BASELINE configs[4])"),
@@ -797,8 +806,43 @@ def run_gather(torch, dev, a, w):
             "cpu_baseline": None}, 0.0, 1
 
 
+def run_stream(torch, dev, a, w):
+    """The fastest one-launch read of config 1's weight bytes (libvqk's
+    vqk__probe_stream test hook: 16-byte loads, one word written per
+    workgroup), launched back to back in a HIP graph over rotating buffers
+    like the c1 workload: the floor of a decode GEMV that must read those
+    bytes in one launch, at several grid sizes."""
+    import ctypes
+    from vqlab_amd import _lib as LB, _torch as TT
+    lib = LB.lib()
+    lib.vqk__probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
+                                      ctypes.c_void_p]
+    nb, L = w["bytes"], w["layers"]
+    bufs = [torch.randint(0, 2**31 - 1, (nb // 4,), dtype=torch.int32, device=dev) for _ in range(L)]
+    sink = torch.empty(8192, dtype=torch.int32, device=dev)
+    rows = []
+    for wgs in (512, 1024, 2048, 4096, 8192):
+        def step(s, wgs=wgs):
+            st = TT.stream(dev)
+            for b in bufs:
+                LB.check(lib.vqk__probe_stream(TT.ptr(b), nb, wgs, TT.ptr(sink), st))
+        steps = max(1, a.steps // 10)
+        _, ev_ms = _graph_time(torch, step, 2, steps, dev)
+        us = ev_ms * 1e3 / (steps * L)
+        rows.append({"workgroups": wgs, "us_per_launch": round(us, 3), "GBps": round(nb / us / 1e3, 1)})
+        log(rows[-1])
+    best = min(rows, key=lambda r: r["us_per_launch"])
+    return {"metric": "us per launch of a streaming read of config 1's weight bytes",
+            "value": best["us_per_launch"], "unit": "us", "higher_is_better": False, "dtype": "u32",
+            "config": {"workload": w["desc"], "bytes": nb, "buffers": L},
+            "grids": rows,
+            "roofline": {"bound": "hbm", "achieved": best["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(best["GBps"] / HBM_PEAK_GBS, 4)},
+            "cpu_baseline": None}, 0.0, 1
+
+
 RUNNERS = {"layer": run_layer, "mtp": run_mtp, "prefill": run_prefill, "dense_gemv": run_dense_gemv,
-           "gather": run_gather}
+           "gather": run_gather, "stream": run_stream}
 
 
 def main():
