@@ -194,15 +194,35 @@ def _draw_layers(n, seed):
     return cases
 
 
-_LAYERS = _draw_layers(12, 20261203)
+def _draw_batched_layers(n, seed):
+    """Batched calls (8-48 tokens: 16-384 routed pairs, the fused, sliced and
+    grouped compositions), tables of every size, experts up to 32 of H up to
+    1024 x I up to 512."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = int(rng.choice([2, 4, 8]))
+        K = int(rng.choice([16, 256, 1000, 4096, 16384]))
+        H = 256 * int(rng.integers(1, 5))
+        I = 256 * int(rng.integers(1, 3))
+        shared = bool(rng.random() < 0.5)
+        k = int(rng.integers(1, 9))
+        E = int(rng.integers(max(k, 4), 33))
+        T = int(rng.integers(8, 49))
+        cases.append((100 + i, E, H, I, D, K, k, shared, bool(rng.random() < 0.7), T))
+    return cases
+
+
+_LAYERS = _draw_layers(12, 20261203) + _draw_batched_layers(6, 20261204)
 
 
 @pytest.mark.parametrize("geom", _LAYERS,
                          ids=[f"{g[0]}-d{g[4]}K{g[5]}E{g[1]}H{g[2]}I{g[3]}k{g[6]}T{g[9]}"
                               + ("s" if g[7] else "") for g in _LAYERS])
 def test_sweep_moe_layer(geom):
-    """The fused layer (routing, gate/up, SwiGLU, down, combine) and the
-    composed per-projection path over random layer geometries."""
+    """The layer call (routing, gate/up, SwiGLU, down, combine, on whichever
+    path the plan picks) and the composed per-projection path over random
+    layer geometries."""
     from vqlab_amd import moe
     i, E, H, I, D, K, k, shared, norm, T = geom
     print(f"sweep moe layer {geom}", flush=True)
