@@ -858,8 +858,9 @@ def main():
                     help="c4 workloads: the layer entry point, or torch glue around grouped calls")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(see DESIGN.md, 'How the path would shard').", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU would "
+              "hold its own experts or row shards and run these kernels on its share).",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     sys.path.insert(0, ROOT)
