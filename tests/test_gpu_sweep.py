@@ -5,8 +5,8 @@ The parametrised tests elsewhere pin the BASELINE shapes and the edge cases
 named one by one; this sweep draws the module format at random -- d 2 / 4 / 8,
 K log-uniform in [2, 65536] (powers of two and not), packed (K = 2^bits) or
 byte codes, scale groups of 8..256 columns or one per row, IN of one group up to 2048,
-OUT from 1, up to 6 experts, 1-4 tokens, fp16 / bf16 / fp32 activations and
-skipzero row tables -- so that every kernel instance the host can pick
+OUT from 1, up to 6 experts, 1-4 tokens, fp16 / bf16 / fp32 activations (a
+third of them at an unaligned base) and skipzero row tables -- so that every kernel instance the host can pick
 (fast or generic GEMV, LDS or L2 tables, the register-decode segment kernel,
 decode-then-GEMM with padded and staged operands) meets formats no
 hand-written case names. Bars: bit-exact for the dequantised weight, rtol
@@ -62,8 +62,21 @@ def _module(case):
     return rng, m
 
 
-def _x(rng, N, IN, xdt):
-    return torch.from_numpy(rng.standard_normal((N, IN)).astype(np.float32)).to("cuda", _DT[xdt])
+def _x(rng, N, IN, xdt, shift=0):
+    """N(0, 1) activations; shift > 0 places the rows `shift` elements into a
+    larger buffer, so x's base is not 16-byte aligned (the staging paths for
+    unaligned rows)."""
+    v = torch.from_numpy(rng.standard_normal((N, IN)).astype(np.float32)).to("cuda", _DT[xdt])
+    if not shift:
+        return v
+    buf = torch.zeros(N * IN + shift, dtype=v.dtype, device="cuda")
+    buf[shift:] = v.reshape(-1)
+    return buf[shift:].view(N, IN)
+
+
+def _shift(case):
+    """Every third case takes x at an element offset of 1-3."""
+    return case[0] % 3 if case[0] % 3 else 0
 
 
 def _np(t):
@@ -107,7 +120,7 @@ def test_sweep_expert_gemv(case):
     _, D, K, packed, G, IN, OUT, E, T, k, xdt, dead = case
     codes, cb, sc = to_device(m)
     ids = _route(rng, T, E, k)
-    x = _x(rng, T, IN, xdt)
+    x = _x(rng, T, IN, xdt, _shift(case))
     e = torch.from_numpy(ids).cuda()
     y = VS._fused(x, e, codes, cb, sc, pack_bits=m["pack_bits"], xkrep=k)
     assert y.shape == (T * k, OUT) and y.dtype == x.dtype
@@ -127,7 +140,7 @@ def test_sweep_dense_gemv(case):
     rng, m = _module(case)
     _, D, K, packed, G, IN, OUT, E, T, k, xdt, dead = case
     codes, cb, sc = to_device(m)
-    x = _x(rng, T, IN, xdt)
+    x = _x(rng, T, IN, xdt, _shift(case))
     y = VS._dense_fused(x, codes[0], cb, sc[0], pack_bits=m["pack_bits"], in_features=IN)
     assert y.shape == (T, OUT) and y.dtype == x.dtype
     w = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], G)
@@ -144,7 +157,7 @@ def test_sweep_grouped_gemm(case):
     # a prefill-sized routing over the same experts: 3..40 tokens
     Tg = int(rng.integers(3, 41))
     ids = _route(rng, Tg, E, k)
-    x = _x(rng, Tg, IN, xdt)
+    x = _x(rng, Tg, IN, xdt, _shift(case))
     e = torch.from_numpy(ids).cuda()
     y = VS._gemmseg(x, e, codes, cb, sc, m["pack_bits"], IN, k)
     assert y.shape == (Tg * k, OUT) and y.dtype == x.dtype
@@ -164,7 +177,7 @@ def test_sweep_dense_gemm(case):
     _, D, K, packed, G, IN, OUT, E, T, k, xdt, dead = case
     codes, cb, sc = to_device(m)
     N = int(rng.integers(65, 200))              # above the register-decode cutoff
-    x = _x(rng, N, IN, xdt)
+    x = _x(rng, N, IN, xdt, _shift(case))
     y = VD._decode_matmul(x, codes[0], cb, sc[0], G, OUT, IN, m["pack_bits"])
     assert y.shape == (N, OUT) and y.dtype == x.dtype
     w = vo.dequant(m["codes"][0], m["codebook"], m["scales"][0], G)
