@@ -186,6 +186,42 @@ def test_sweep_dense_gemm(case):
     assert_close(_np(y), vo.decode_matmul(_np(x), wr), what=f"dense gemm {case}")
 
 
+@pytest.mark.parametrize("case", _LIN, ids=_LIN_IDS)
+def test_sweep_switch_apply_rounding(case):
+    """vqk_switch_apply with bf16 x, on whichever path its options pick: with
+    the defaults its rows are that path's fp32 rows rounded to fp16 and then
+    to bf16 (the reference's default decode arithmetic); with the bf16-I/O
+    options they are the fp32 rows rounded once to bf16, the GEMV keeping x
+    exact on the float-staged formats (unpacked d4 K <= 1024, d8 K > 1024)."""
+    import ctypes
+    from vqlab_amd import _lib as L, _torch as Tt, vq_switch as VS
+    print(f"sweep switch_apply {case}", flush=True)
+    rng, m = _module(case)
+    _, D, K, packed, G, IN, OUT, E, T, k, xdt, dead = case
+    codes, cb, sc = to_device(m)
+    pb = m["pack_bits"]
+    ids = _route(rng, T, E, k)
+    x = _x(rng, T, IN, "bf16", _shift(case))
+    e = torch.from_numpy(ids).cuda()
+    bits = lambda t: t.view(torch.int16)
+    dflt, bio = L.options(), L.options(decode_bf16io=1, prefill_bf16io=1)
+    yd = VS._switch_apply(x, e, codes, cb, sc, pb, IN, k, opts=dflt)
+    y32 = VS._switch_apply(x, e, codes, cb, sc, pb, IN, k, out_dtype=torch.float32, opts=dflt)
+    assert torch.equal(bits(yd), bits(y32.to(torch.float16).to(torch.bfloat16)))
+    yio = VS._switch_apply(x, e, codes, cb, sc, pb, IN, k, opts=bio)
+    yk = VS._switch_apply(x, e, codes, cb, sc, pb, IN, k, out_dtype=torch.float32, opts=bio)
+    assert torch.equal(bits(yio), bits(yk.to(torch.bfloat16)))
+    # which path ran: a workspace means the grouped GEMM, which narrows x to fp16
+    keep = []
+    w = Tt.weights(codes, cb, sc, G, pb, IN, keep=keep)
+    ws = ctypes.c_size_t()
+    L.check(L.lib().vqk_switch_apply_workspace(ctypes.byref(w), T * k, ctypes.byref(bio), ctypes.byref(ws)))
+    exact_x = ws.value == 0 and VS._float_staged(cb, pb)
+    ref = vo.expert_gemv(_np(x) if exact_x else _x16(x), ids, m["codes"], m["codebook"], m["scales"], G,
+                         xkrep=k, weights="exact")
+    assert_close(_np(yk), ref, what=f"switch_apply bf16io {case}")
+
+
 def _draw_layers(n, seed):
     """Layer geometries inside the fused kernels' block limits (NSUB a multiple
     of 32 codes, (top_k + shared) x down blocks <= 64); a format the fused
