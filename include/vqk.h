@@ -166,7 +166,10 @@ int vqk_moe_expert_gemv(const vqk_weights *w, const void *x, int32_t x_type,
  * host argsort at vq_switch.py:5383-5388 and the tile build at 4590-4610),
  * and each expert tile's weights are decoded bit-exactly straight into fp16
  * matrix-core operands (codebook in LDS, or its first part in LDS and the
- * rest gathered from L2), fp32 accumulation. */
+ * rest gathered from L2), fp32 accumulation. The sort picks the tile rows on
+ * device (16, or for d8 tables beyond LDS under a thin routing 4 or 8, the
+ * larger where it saves decoding an expert's rows twice). The workspace is
+ * 16-byte aligned. */
 int vqk_grouped_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes);
 int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type,
                      int64_t T, const uint32_t *eidx, int64_t N, int64_t xkrep,
@@ -186,8 +189,8 @@ int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type,
  * is not a multiple of 64 (rows zero-padded). vqk_dense_gemm_workspace gives a
  * size that holds the whole weight as one panel for any activation type; a
  * smaller workspace that still holds the staged x plus 128 weight rows runs
- * in more panels, less (or none) is VQK_ENOSPACE. No host synchronisation,
- * no allocation, no state kept between calls. */
+ * in more panels, less (or none) is VQK_ENOSPACE; it is 16-byte aligned. No
+ * host synchronisation, no allocation, no state kept between calls. */
 int vqk_dense_gemm_workspace(const vqk_weights *w, int64_t N, size_t *bytes);
 int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type,
                    int64_t N, void *y, int32_t y_type, void *workspace,

@@ -112,6 +112,11 @@ def test_dense_gemm_empty_and_refusals():
                                   L.VQK_BF16, Tt.ptr(small), 1024, Tt.stream()) == L.VQK_ENOSPACE
     assert L.lib().vqk_dense_gemm(ctypes.byref(w1), Tt.ptr(xb), L.VQK_BF16, 100, Tt.ptr(yb),
                                   L.VQK_BF16, None, 0, Tt.stream()) == L.VQK_ENOSPACE
+    # a workspace that is not 16-byte aligned is refused before any launch
+    big = torch.empty(ws.value + 16, dtype=torch.uint8, device="cuda")
+    assert L.lib().vqk_dense_gemm(ctypes.byref(w1), Tt.ptr(xb), L.VQK_BF16, 100, Tt.ptr(yb),
+                                  L.VQK_BF16, ctypes.c_void_p(big.data_ptr() + 4), ws.value,
+                                  Tt.stream()) == L.VQK_EINVAL
 
 
 @pytest.mark.parametrize("panel_rows", [128, 256, 1024])
@@ -380,6 +385,27 @@ def test_grouped_gemm_sort_builds_oracle_tiles():
     assert_close(yn[valid], ref, what="sort case")
 
 
+def _narrow_rows(ids, E):
+    """The device sort's choice for narrow tiles (restated): 8-row tiles when
+    they cut the tile count by more than 1/21, else 4 (ids outside [0, E) in
+    one bucket of their own)."""
+    cnt = np.bincount(np.where((ids >= 0) & (ids < E), ids, E), minlength=E + 1)
+    t4, t8 = int(((cnt + 3) // 4).sum()), int(((cnt + 7) // 8).sum())
+    return 8 if 21 * t8 < 20 * t4 else 4
+
+
+def _sort_records(work, N, E):
+    """(tile records, tile count, tile rows chosen) from a grouped call's
+    workspace: order [N] int32, records [room][3], then the count and the
+    rows (256-byte aligned sections; room for 4-row tiles)."""
+    wb = work.cpu().numpy()
+    al = lambda v: (v + 255) & ~255
+    room = (N + 3) // 4 + min(N, E + 1)
+    tm = wb[al(4 * N):al(4 * N) + 12 * room].view(np.int32).reshape(-1, 3)
+    nt, rows = (int(v) for v in wb[al(4 * N) + al(12 * room):][:8].view(np.int32))
+    return tm[:nt], nt, rows
+
+
 def test_grouped_gemm_narrow_tiles():
     """A d8 K16384 routing with <= 2 pairs per expert on average sorts into
     tiles of <= 4 rows (the oracle's tile_meta at 4), one expert on every
@@ -411,17 +437,72 @@ def test_grouped_gemm_narrow_tiles():
     L.check(L.lib().vqk_grouped_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, T, Tt.ptr(e), N, k,
                                      Tt.ptr(y), L.VQK_F32, Tt.ptr(work), ws.value, Tt.stream()))
     torch.cuda.synchronize()
-    wb = work.cpu().numpy()
-    al = lambda v: (v + 255) & ~255
-    room = (N + 3) // 4 + min(N, E + 1)
     _, _, _, rs = vo.sort_routing(ids, 1)
     ref_tm = vo.tile_meta(rs, E, 4)
-    tm = wb[al(4 * N):al(4 * N) + 12 * len(ref_tm)].view(np.int32).reshape(-1, 3)
-    nt = int(wb[al(4 * N) + al(12 * room):][:4].view(np.int32)[0])
+    tm, nt, rows = _sort_records(work, N, E)
+    assert rows == 4 == _narrow_rows(ids, E)
     assert nt == len(ref_tm) and np.array_equal(tm, ref_tm)
     assert (ref_tm[ref_tm[:, 0] == 5][:, 2] == [4, 4, 3]).all()
     ref = vo.expert_gemv(_x16(x), ids, m["codes"], m["codebook"], m["scales"], 64, xkrep=k)
     assert_close(_np(y), ref, what="narrow tiles")
+    sz, rt = skipzero(m)
+    zc = torch.from_numpy(sz["sz_codes"].view(np.int32)).cuda()
+    zs = torch.from_numpy(sz["sz_scales"]).cuda()
+    yc = VS._gemmseg(x, e, zc, cb, zs, m["pack_bits"], IN, k, torch.from_numpy(rt).cuda(),
+                     out_dtype=torch.float32)
+    dead = rt[ids] < 0
+    assert dead.any() and (_np(yc)[dead] == 0).all()
+    assert torch.equal(yc[torch.from_numpy(~dead).cuda()], y[torch.from_numpy(~dead).cuda()])
+
+
+@pytest.mark.parametrize("skew", ["capped", "mixed"])
+def test_grouped_gemm_narrow_tiles_of_eight(skew):
+    """Routings that put 5-8 pairs on most touched experts ("capped", as an
+    MTP verify batch drawn with 1..8 tokens per expert) make the sort choose
+    8-row tiles (one decode of each expert's rows instead of two); "mixed"
+    adds a tail of single-pair experts and one expert on every token (tiles of
+    8, 8, ..., rest). Tile records equal the oracle's tile_meta at the chosen
+    size, the choice equals the restated rule, outputs match the oracle, and a
+    skipzero row table on the same routing gives the same live rows."""
+    from vqlab_amd import _lib as L, _torch as Tt, vq_switch as VS
+    from vq_cases import skipzero
+    print(f"grouped gemm 8-row tiles {skew}", flush=True)
+    rng = np.random.default_rng(52 if skew == "capped" else 53)
+    E, OUT, IN, T, k = 160, 640, 1024, 40, 8               # N = 320 <= 2 E: narrow
+    m = make_module(rng, E, OUT, IN, 8, 16384, dead_frac=0.2)
+    codes, cb, sc = to_device(m)
+    if skew == "capped":
+        ids = _routes(rng, T, k, E, lo=5, hi=8)
+    else:
+        ids = _routes(rng, T, k, E, lo=4, hi=8)
+        for t in range(T):                               # expert 7 on every token
+            if 7 not in ids[t]:
+                ids[t, 1] = 7
+    assert all(len(np.unique(r)) == k for r in ids)
+    ids = ids.reshape(-1)
+    N = T * k
+    assert N <= 2 * E and _narrow_rows(ids, E) == 8     # narrow tiles, and 8 rows pay
+    x = _x(rng, T, IN)
+    e = torch.from_numpy(ids.astype(np.int32)).cuda()
+    keep = []
+    w = Tt.weights(codes, cb, sc, 64, m["pack_bits"], IN, keep=keep)
+    ws = ctypes.c_size_t()
+    L.check(L.lib().vqk_grouped_gemm_workspace(ctypes.byref(w), N, ctypes.byref(ws)))
+    work = torch.zeros(ws.value, dtype=torch.uint8, device="cuda")
+    y = torch.empty((N, OUT), dtype=torch.float32, device="cuda")
+    L.check(L.lib().vqk_grouped_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, T, Tt.ptr(e), N, k,
+                                     Tt.ptr(y), L.VQK_F32, Tt.ptr(work), ws.value, Tt.stream()))
+    torch.cuda.synchronize()
+    _, _, _, rs = vo.sort_routing(ids, 1)
+    ref_tm = vo.tile_meta(rs, E, 8)
+    tm, nt, rows = _sort_records(work, N, E)
+    assert rows == 8
+    assert nt == len(ref_tm) and np.array_equal(tm, ref_tm)
+    assert ref_tm[:, 2].max() > 4 and len(ref_tm) < len(vo.tile_meta(rs, E, 4))
+    if skew == "mixed":
+        assert (ref_tm[ref_tm[:, 0] == 7][:, 2] == [8] * (T // 8) + ([T % 8] if T % 8 else [])).all()
+    ref = vo.expert_gemv(_x16(x), ids, m["codes"], m["codebook"], m["scales"], 64, xkrep=k)
+    assert_close(_np(y), ref, what=f"8-row tiles {skew}")
     sz, rt = skipzero(m)
     zc = torch.from_numpy(sz["sz_codes"].view(np.int32)).cuda()
     zs = torch.from_numpy(sz["sz_scales"]).cuda()
@@ -452,6 +533,11 @@ def test_grouped_gemm_errors():
     assert lib.vqk_grouped_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, 4, Tt.ptr(e), 8, 3,
                                 Tt.ptr(y), L.VQK_BF16, Tt.ptr(work), ws.value,
                                 Tt.stream()) == L.VQK_EINVAL
+    # a workspace that is not 16-byte aligned is refused before any launch
+    big = torch.empty(ws.value + 16, dtype=torch.uint8, device="cuda")
+    assert lib.vqk_grouped_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, 4, Tt.ptr(e), 8, 2,
+                                Tt.ptr(y), L.VQK_BF16, ctypes.c_void_p(big.data_ptr() + 8),
+                                ws.value, Tt.stream()) == L.VQK_EINVAL
     assert lib.vqk_grouped_gemm(ctypes.byref(w), Tt.ptr(x), L.VQK_BF16, 4, Tt.ptr(e), 8, 2,
                                 Tt.ptr(y), L.VQK_BF16, Tt.ptr(work), ws.value,
                                 Tt.stream()) == L.VQK_OK

@@ -260,14 +260,30 @@ __global__ void __launch_bounds__(kSortThreads) k_group_sort(const uint32_t *eid
     int *tls = cnt + NBK;          // [NBK] tiles per bucket, then tile starts
     int *cur = tls + NBK;          // [NBK] scatter cursors
     int *tmp = cur + NBK;          // [kSortThreads]
+    int *red = tmp + kSortThreads; // [2] tile totals of the two narrow sizes
     const int tid = threadIdx.x;
     for (int b = tid; b < NBK; b += kSortThreads) cnt[b] = 0;
+    if (tid < 2) red[tid] = 0;
     __syncthreads();
     for (int n = tid; n < N; n += kSortThreads) {
         const uint32_t e = eidx[n];
         atomicAdd(&cnt[e < uint32_t(E) ? int(e) : E], 1);
     }
     __syncthreads();
+    if (BM == kSegTokNarrow) {
+        // narrow tiles: 8 rows where that cuts the tile count (every tile
+        // decodes its expert's weights once) by more than the ~5 % that the
+        // 8-row tile's smaller LDS part of the table costs per tile
+        int t4 = 0, t8 = 0;
+        for (int b = tid; b < NBK; b += kSortThreads) {
+            t4 += (cnt[b] + kSegTokNarrow - 1) / kSegTokNarrow;
+            t8 += (cnt[b] + kSegTokMid - 1) / kSegTokMid;
+        }
+        atomicAdd(&red[0], t4);
+        atomicAdd(&red[1], t8);
+        __syncthreads();
+        if (21 * red[1] < 20 * red[0]) BM = kSegTokMid;
+    }
     for (int b = tid; b < NBK; b += kSortThreads) tls[b] = (cnt[b] + BM - 1) / BM;
     __syncthreads();
     // keep the counts: cur = counts for now
@@ -286,7 +302,10 @@ __global__ void __launch_bounds__(kSortThreads) k_group_sort(const uint32_t *eid
                 tmeta[3 * ti + 2] = min(BM, c - t * BM);
             }
         }
-        if (b == NBK - 1) *ntiles = min(max_tiles, tls[b] + nt);
+        if (b == NBK - 1) {
+            ntiles[0] = min(max_tiles, tls[b] + nt);
+            ntiles[1] = BM;                    // the tile rows chosen
+        }
     }
     __syncthreads();
     for (int b = tid; b < NBK; b += kSortThreads) cur[b] = cnt[b];
@@ -389,6 +408,8 @@ static int dense_decode_gemm(const vqk_weights *w, const Geom &g, const void *x,
         return set_error(VQK_ENOSPACE, "dense GEMM workspace %zu B < %zu B (%s%lld weight rows)",
                          ws_bytes, xb + kPanelMin * row_b, stage ? "staged x + " : "",
                          (long long)kPanelMin);
+    if (reinterpret_cast<uintptr_t>(workspace) & 15)
+        return set_error(VQK_EINVAL, "dense GEMM workspace must be 16-byte aligned");
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     const uint16_t *a = static_cast<const uint16_t *>(x);
     int rc;
@@ -517,7 +538,7 @@ int seg_sort(const uint32_t *eidx, int64_t N, int64_t E, int tok, void *ws, hipS
     int32_t *order = reinterpret_cast<int32_t *>(b);
     int32_t *tmeta = reinterpret_cast<int32_t *>(b + sort_order_bytes(N));
     int32_t *ntiles = reinterpret_cast<int32_t *>(b + sort_order_bytes(N) + sort_meta_bytes(N, E));
-    const size_t sort_lds = sizeof(int) * (3 * size_t(E + 1) + kSortThreads);
+    const size_t sort_lds = sizeof(int) * (3 * size_t(E + 1) + kSortThreads + 2);
     hipLaunchKernelGGL(k_group_sort, dim3(1), dim3(kSortThreads), sort_lds, st, eidx, int(N), int(E),
                        tok, int(mt), order, tmeta, ntiles);
     return hip_status(hipGetLastError(), "group sort launch");
@@ -564,15 +585,16 @@ int seg_run(const vqk_weights *w, const SegCall &c, const void *sort_ws, hipStre
     }
     const int64_t nxb = (g.OUT + kSegRows - 1) / kSegRows;
     const int64_t nxp = (g.OUT + kPersistWaves * 32 - 1) / (kPersistWaves * 32);
-    if (sort_ws && tok == kSegTokNarrow && g.D == 8 && !cb_in_lds(8, g.BITS) &&
-        nxp * tiles <= INT32_MAX) {
+    if (sort_ws && tok == kSegTokNarrow && g.D == 8 && !cb_in_lds(8, g.BITS)) {
         // one workgroup per CU walking (tile, row block) items: the table
-        // part is staged once per CU, not once per item
+        // part is staged once per CU, not once per item. The sort chose 4- or
+        // 8-row tiles; the kernel reads its choice.
         const dim3 grid(unsigned(big_grid(nxp * tiles)), 1, 1);
         return launch_seg_persist_d8(sp, g.BITS, g.gpb, grid, st);
     }
+    // the 16-row kernel: dense rows, or sorted tiles of any size (<= 16 rows)
     const dim3 grid{unsigned(nxb), unsigned(tiles), unsigned(ks)};
-    return launch_seg(sp, g, tok, grid, st);
+    return launch_seg(sp, g, kSegTok, grid, st);
 }
 
 }  // namespace vqk
@@ -654,6 +676,8 @@ int vqk_grouped_gemm(const vqk_weights *w, const void *x, int32_t x_type, int64_
     vqk_grouped_gemm_workspace(w, N, &need);
     if (!workspace || ws_bytes < need)
         return set_error(VQK_ENOSPACE, "workspace %zu B < %zu B", ws_bytes, need);
+    if (reinterpret_cast<uintptr_t>(workspace) & 15)
+        return set_error(VQK_EINVAL, "grouped GEMM workspace must be 16-byte aligned");
     const bool seg = seg_fits(g, w, x);
     const int tok = seg ? seg_tile_rows(w, N, g.E) : kSegTok;
     const int64_t mt = group_max_tiles(N, g.E, tok);

@@ -88,6 +88,13 @@ constexpr int kSegTok = 16;        // tokens per tile
 // each expert (an MTP verify batch: ~1.25 per expert): the smaller x chunk
 // leaves more of the 160 KB to a d8 table too large for LDS.
 constexpr int kSegTokNarrow = 4;
+// ... or of at most kSegTokMid: a routing that puts several pairs on each of
+// fewer experts (an MTP batch drawn with 1..8 tokens per touched expert)
+// would split them into two or more 4-row tiles, each decoding the expert's
+// weights again. The device sort picks between the two per call (fewer
+// decoded rows against the smaller LDS part of the table) and records its
+// choice after the tile count; k_seg_persist follows it.
+constexpr int kSegTokMid = 8;
 // Waves of the persistent kernel's workgroup (one per CU): two per SIMD, so
 // one wave's table reads are in flight while the other decodes; an item is
 // 32 rows per wave.
@@ -162,9 +169,10 @@ __device__ __forceinline__ h8 step_entries_hyb(const uint32_t (&w)[BITS], int s,
 // LDS entries of a table too large for LDS that the kernel stages: what the
 // x chunk (TOK x (128 D + 8) halves) leaves of the 160 KB -- 124 KB of a d8
 // table (7936 of K16384's entries; 151 KB, 9664 entries, with 4-token
-// tiles), all of a d4 K16384 table, 144 KB of a d2 one.
+// tiles; 143 KB, 9152 entries, with 8-token tiles), all of a d4 K16384
+// table, 144 KB of a d2 one.
 __host__ __device__ constexpr int seg_hyb_entries(int D, int TOK = kSegTok) {
-    return (D == 8 ? (TOK == kSegTokNarrow ? 151 : 124) * 1024
+    return (D == 8 ? (TOK == kSegTokNarrow ? 151 : (TOK == kSegTokMid ? 143 : 124)) * 1024
                    : (D == 4 ? 128 * 1024 : 144 * 1024)) / (2 * D);
 }
 
@@ -404,8 +412,8 @@ __global__ void __launch_bounds__(kSegWaves * 64) k_seg_mfma(const SegParams p) 
 // ahead; each step issues those loads (discarded unless an item ends) so that
 // every step sends the same loads and the compiler's load-count waits never
 // stall a step on the prefetch issued in it.
-template <int BITS, int GPB, int TOK, int NW = kPersistWaves>
-__global__ void __launch_bounds__(NW * 64) k_seg_persist(const SegParams p) {
+template <int BITS, int GPB, int TOK, int NW>
+__device__ __forceinline__ void seg_persist_body(const SegParams &p, int ntiles) {
     constexpr int D = 8;
     constexpr int NT = NW * 64;                 // threads
     constexpr int ROWS = NW * 32;               // weight rows per item
@@ -426,7 +434,7 @@ __global__ void __launch_bounds__(NW * 64) k_seg_persist(const SegParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ln = lane & 15, lg = lane >> 4;
     const int nxb = (p.OUT + ROWS - 1) / ROWS;
-    const int items = *p.ntiles * nxb;          // uniform
+    const int items = ntiles * nxb;             // uniform
     const int G = int(gridDim.x), i0 = int(blockIdx.x);
     if (i0 >= items) return;                    // uniform, before any barrier
     const int mine = (items - i0 + G - 1) / G;
@@ -633,6 +641,16 @@ __global__ void __launch_bounds__(NW * 64) k_seg_persist(const SegParams p) {
         if (!step(j, w0, s0, l0, w1, s1, l1)) break;
         if (!step(j + 1, w1, s1, l1, w0, s0, l0)) break;
     }
+}
+
+// The persistent kernel over narrow tiles, with the tile size the sort chose
+// for this routing: the tile count and that size, read as one 8-byte load
+// (ntiles[1]: kSegTokMid, else kSegTokNarrow).
+template <int BITS, int GPB, int NW = kPersistWaves>
+__global__ void __launch_bounds__(NW * 64) k_seg_persist(const SegParams p) {
+    const int2 nt = *reinterpret_cast<const int2 *>(p.ntiles);
+    if (nt.y == kSegTokMid) seg_persist_body<BITS, GPB, kSegTokMid, NW>(p, nt.x);
+    else seg_persist_body<BITS, GPB, kSegTokNarrow, NW>(p, nt.x);
 }
 
 // LDS bytes of k_seg_mfma<D, BITS, GPB, cbl, tok>.

@@ -1,5 +1,6 @@
 // k_seg_mfma instances for d = 8: every packed width 2..16 (8 / 16 also
-// serve unpacked uint8 / uint16 rows) x the scale-group layouts of the GEMV.
+// serve unpacked uint8 / uint16 rows) x the scale-group layouts of the GEMV;
+// k_seg_persist for the widths whose table is beyond LDS.
 #include "vqk_gseg.h"
 
 namespace vqk {
@@ -10,18 +11,13 @@ int go(const SegParams &p, dim3 grid, hipStream_t st) {
     constexpr bool CBL = cb_in_lds(8, BITS);
     return launch_with_lds<k_seg_mfma<8, BITS, GPB, CBL>>(grid, dim3(kSegWaves * 64), seg_lds(8, BITS, CBL), st, p);
 }
-// 4-token tiles: only where the table is beyond LDS (the x chunk's room goes
-// to table entries); other widths run the 16-token kernel on those tiles.
-template <int BITS, int GPB>
-int go_narrow(const SegParams &p, dim3 grid, hipStream_t st) {
-    static_assert(!cb_in_lds(8, BITS), "narrow tiles only pay for tables beyond LDS");
-    return launch_with_lds<k_seg_mfma<8, BITS, GPB, false, kSegTokNarrow>>(
-        grid, dim3(kSegWaves * 64), seg_lds(8, BITS, false, kSegTokNarrow), st, p);
-}
+// the sort's tiles hold up to 4 or up to 8 rows (its choice, read by the
+// kernel): LDS for the larger of the two layouts
 template <int BITS, int GPB>
 int go_persist(const SegParams &p, dim3 grid, hipStream_t st) {
-    return launch_with_lds<k_seg_persist<BITS, GPB, kSegTokNarrow>>(
-        grid, dim3(kPersistWaves * 64), seg_lds(8, BITS, false, kSegTokNarrow), st, p);
+    constexpr size_t a = seg_lds(8, BITS, false, kSegTokNarrow), b = seg_lds(8, BITS, false, kSegTokMid);
+    return launch_with_lds<k_seg_persist<BITS, GPB>>(grid, dim3(kPersistWaves * 64), a > b ? a : b,
+                                                     st, p);
 }
 }  // namespace
 
@@ -41,20 +37,10 @@ int launch_seg_persist_d8(const SegParams &p, int bits, int gpb, dim3 grid, hipS
     }
 }
 
+// Tiles of at most 16 rows (dense rows or a 16-row sort); narrow sorts run
+// the persistent kernel (launch_seg_persist_d8).
 int launch_seg_d8(const SegParams &p, int bits, int gpb, int tok, dim3 grid, hipStream_t st) {
-    if (tok == kSegTokNarrow) {
-        switch (bits * 16 + gpb) {
-            case 209: return go_narrow<13, 1>(p, grid, st);
-            case 212: return go_narrow<13, 4>(p, grid, st);
-            case 225: return go_narrow<14, 1>(p, grid, st);
-            case 228: return go_narrow<14, 4>(p, grid, st);
-            case 241: return go_narrow<15, 1>(p, grid, st);
-            case 244: return go_narrow<15, 4>(p, grid, st);
-            case 257: return go_narrow<16, 1>(p, grid, st);
-            case 260: return go_narrow<16, 4>(p, grid, st);
-            default: break;
-        }
-    }
+    if (tok != kSegTok) return set_error(VQK_EINVAL, "segment kernel tiles of %d rows", tok);
     switch (bits * 16 + gpb) {
         case 33: return go<2, 1>(p, grid, st);
         case 36: return go<2, 4>(p, grid, st);

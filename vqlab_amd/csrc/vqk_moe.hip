@@ -1682,7 +1682,8 @@ static int launch_moe_grouped(const vqk_moe_desc *m, const MoePlan &pl, uint8_t 
     int rc = hip_status(hipGetLastError(), "routing launch");
     if (rc) return rc;
     // one sort for the three routed projections: its tile rows must suit
-    // every kernel run over it (the 16-row kernels take 4-row tiles too)
+    // every kernel run over it (the 16-row kernels take the narrow tiles of
+    // either size too)
     const int tok = seg_tile_rows(m->gate, N, p.E);
     if ((rc = seg_sort(reinterpret_cast<const uint32_t *>(p.ids), N, p.E, tok, sort, st))) return rc;
     SegCall c{p.x, p.x_type, nullptr, nullptr, k, g, VQK_F32, N, tok};
