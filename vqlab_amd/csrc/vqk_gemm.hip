@@ -279,8 +279,14 @@ __global__ void __launch_bounds__(kSortThreads) k_group_sort(const uint32_t *eid
             t4 += (cnt[b] + kSegTokNarrow - 1) / kSegTokNarrow;
             t8 += (cnt[b] + kSegTokMid - 1) / kSegTokMid;
         }
-        atomicAdd(&red[0], t4);
-        atomicAdd(&red[1], t8);
+        for (int o = 32; o >= 1; o >>= 1) {     // wave sums, then one add per wave
+            t4 += __shfl_xor(t4, o);
+            t8 += __shfl_xor(t8, o);
+        }
+        if ((tid & 63) == 0) {
+            atomicAdd(&red[0], t4);
+            atomicAdd(&red[1], t8);
+        }
         __syncthreads();
         if (21 * red[1] < 20 * red[0]) BM = kSegTokMid;
     }
