@@ -663,10 +663,11 @@ __host__ __device__ constexpr size_t seg_lds(int D, int BITS, bool cbl, int tok 
 // VQK status (VQK_ENOTIMPL when no instance matches).
 int launch_seg_d2(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st);
 int launch_seg_d4(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st);
-// d8 with tok == kSegTokNarrow (tiles of at most 4 rows) takes the narrow
-// instance where the table is beyond LDS.
+// Tiles of at most 16 rows (tok == kSegTok; sorted narrow tiles run
+// launch_seg_persist_d8).
 int launch_seg_d8(const SegParams &p, int bits, int gpb, int tok, dim3 grid, hipStream_t st);
-// k_seg_persist (sorted 4-row tiles, d8 tables beyond LDS) on `grid` workgroups.
+// k_seg_persist (sorted narrow tiles of <= 4 or <= 8 rows as the sort chose,
+// d8 tables beyond LDS) on `grid` workgroups.
 int launch_seg_persist_d8(const SegParams &p, int bits, int gpb, dim3 grid, hipStream_t st);
 
 }  // namespace vqk

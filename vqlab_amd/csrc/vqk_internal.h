@@ -39,9 +39,10 @@ struct SegCall {
     int32_t xparts;            // xg / xu hold xparts partial rows [xparts][N][IN] to add
 };
 
-// Rows per tile to sort N pairs into for module `w` over E experts: 4 when
-// the routing puts at most ~2 pairs on an expert on average and w's d8 table
-// is beyond LDS (more of it fits beside a 4-row x chunk), else 16.
+// Rows per tile to sort N pairs into for module `w` over E experts:
+// kSegTokNarrow when the routing puts at most ~2 pairs on an expert on
+// average and w's d8 table is beyond LDS (more of it fits beside a narrow x
+// chunk; the sort then picks 4- or 8-row tiles on device), else 16.
 int seg_tile_rows(const vqk_weights *w, int64_t N, int64_t E);
 
 // K slices for the segment kernel over N dense rows of `w`: enough that the

@@ -1463,7 +1463,7 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
     // Otherwise the two fused kernels (partly LDS-staged tables).
     const int64_t N = T * k;
     // grouped: at least one pair per expert on average, or the sparser
-    // routings whose d8 tables take the persistent 4-row-tile path
+    // routings whose d8 tables take the persistent narrow-tile path
     bool grouped = N >= kMoeGroupedMinPairs && (N >= E || seg_tile_rows(m->gate, N, E) < 16) &&
                    seg_ok(m->gate, N) && seg_ok(m->up, N) && seg_ok(m->down, N);
     if (grouped && shared)
