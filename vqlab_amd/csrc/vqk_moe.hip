@@ -1666,11 +1666,52 @@ static int launch_moe_big(const vqk_moe_desc *m, const MoePlan &pl, uint8_t *ws,
     return hip_status(hipGetLastError(), "combine launch");
 }
 
+// The batched layer's second stream, one per device (default priority),
+// created on first use and kept until the process ends, with the events that
+// fork work onto it and join it back: [0] call start, [1] sort done, [2]
+// routed up done, [3] shared expert done.
+constexpr int kMaxSideDevices = 64;
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t e[4] = {};
+};
+static std::mutex g_side_mu;
+static SideStream g_side[kMaxSideDevices];
+
+// The current device's side stream (g_side_mu held), or nullptr when it
+// cannot be created (the layer then runs on the caller's stream alone).
+static SideStream *side_stream_locked() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxSideDevices) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    SideStream &ss = g_side[dev];
+    if (!ss.s) {
+        SideStream n;
+        bool ok = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking) == hipSuccess;
+        for (int i = 0; ok && i < 4; ++i)
+            ok = hipEventCreateWithFlags(&n.e[i], hipEventDisableTiming) == hipSuccess;
+        if (!ok) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        ss = n;
+    }
+    return &ss;
+}
+
 // Many pairs: routing (one wave per token), one counting sort of the pairs by
 // expert, gate and up as grouped GEMMs into fp32 rows, down as a grouped GEMM
 // whose input rows are built as fp16(silu(g) * u) while they are staged, the
 // shared expert as the same kernels over the token rows, and the weighted
-// combine.
+// combine. The shared expert (independent of the routing) and the routed up
+// projection run on the device's second stream beside the routing, the sort
+// and the routed gate and down: a persistent launch leaves CUs idle in its
+// last, partial round of items, and the other stream's workgroups fill them.
+// A mutex holds the whole enqueue sequence, so calls from several host
+// threads never interleave their event records; the fork / join pattern is
+// also what a graph capture of the call records.
 static int launch_moe_grouped(const vqk_moe_desc *m, const MoePlan &pl, uint8_t *ws, hipStream_t st) {
     const MoeParams &p = pl.p;
     const int64_t T = p.T, k = p.top_k, N = T * k;
@@ -1678,32 +1719,47 @@ static int launch_moe_grouped(const vqk_moe_desc *m, const MoePlan &pl, uint8_t 
     float *sgg = reinterpret_cast<float *>(ws + pl.lay.sgg), *sgu = reinterpret_cast<float *>(ws + pl.lay.sgu);
     float *yd = reinterpret_cast<float *>(ws + pl.lay.yd), *ysh = reinterpret_cast<float *>(ws + pl.lay.ysh);
     void *sort = ws + pl.lay.sort;
+    std::lock_guard<std::mutex> lk(g_side_mu);
+    SideStream *ss = side_stream_locked();
+    const hipStream_t sb = ss ? ss->s : st;
+    int rc = VQK_OK;
+    // event i recorded on `from`, waited for by `to` (nothing without a side stream)
+    auto link = [&](int i, hipStream_t from, hipStream_t to) {
+        if (!ss) return VQK_OK;
+        int r = hip_status(hipEventRecord(ss->e[i], from), "hipEventRecord");
+        return r ? r : hip_status(hipStreamWaitEvent(to, ss->e[i], 0), "hipStreamWaitEvent");
+    };
+    // the shared expert is one expert over T rows: its gate / up launches
+    // alone would fill few CUs, so they split K (fp32 partials that the down
+    // launch adds in a fixed order as it stages its input)
+    const int ks = p.shared ? seg_ksplit(m->sh_gate, T) : 1;
+    if ((rc = link(0, st, sb))) return rc;
+    if (p.shared) {
+        SegCall cs{p.x, p.x_type, nullptr, nullptr, 1, sgg, VQK_F32, T, 0, ks};
+        if ((rc = seg_run(m->sh_gate, cs, nullptr, sb))) return rc;
+        cs.y = sgu;
+        if ((rc = seg_run(m->sh_up, cs, nullptr, sb))) return rc;
+    }
     hipLaunchKernelGGL(k_route_tokens, dim3(unsigned(T)), dim3(kWave), 0, st, p);
-    int rc = hip_status(hipGetLastError(), "routing launch");
-    if (rc) return rc;
+    if ((rc = hip_status(hipGetLastError(), "routing launch"))) return rc;
     // one sort for the three routed projections: its tile rows must suit
     // every kernel run over it (the 16-row kernels take the narrow tiles of
     // either size too)
     const int tok = seg_tile_rows(m->gate, N, p.E);
     if ((rc = seg_sort(reinterpret_cast<const uint32_t *>(p.ids), N, p.E, tok, sort, st))) return rc;
+    if ((rc = link(1, st, sb))) return rc;
     SegCall c{p.x, p.x_type, nullptr, nullptr, k, g, VQK_F32, N, tok};
     if ((rc = seg_run(m->gate, c, sort, st))) return rc;
     c.y = u;
-    if ((rc = seg_run(m->up, c, sort, st))) return rc;
+    if ((rc = seg_run(m->up, c, sort, sb))) return rc;
+    if ((rc = link(2, sb, st))) return rc;
     SegCall d{nullptr, VQK_F32, g, u, 1, yd, VQK_F32, N, tok};
     if ((rc = seg_run(m->down, d, sort, st))) return rc;
     if (p.shared) {
-        // the shared expert is one expert over T rows: its gate / up launches
-        // alone would fill few CUs, so they split K (fp32 partials that the
-        // down launch adds in a fixed order as it stages its input)
-        const int ks = seg_ksplit(m->sh_gate, T);
-        SegCall cs{p.x, p.x_type, nullptr, nullptr, 1, sgg, VQK_F32, T, 0, ks};
-        if ((rc = seg_run(m->sh_gate, cs, nullptr, st))) return rc;
-        cs.y = sgu;
-        if ((rc = seg_run(m->sh_up, cs, nullptr, st))) return rc;
         SegCall ds{nullptr, VQK_F32, sgg, sgu, 1, ysh, VQK_F32, T, 0, 0, ks};
-        if ((rc = seg_run(m->sh_down, ds, nullptr, st))) return rc;
+        if ((rc = seg_run(m->sh_down, ds, nullptr, sb))) return rc;
     }
+    if ((rc = link(3, sb, st))) return rc;
     hipLaunchKernelGGL(k_moe_combine, dim3(unsigned((p.H + 255) / 256), unsigned(T)), dim3(256), 0, st,
                        p, static_cast<const float *>(yd), static_cast<const float *>(ysh));
     return hip_status(hipGetLastError(), "combine launch");
