@@ -513,3 +513,56 @@ def test_empty_batches():
     lin = VQLinear(codes[0], cb, sc[0], group_size=64, pack_bits=m["pack_bits"], in_features=I)
     assert lin(torch.zeros((0, I), dtype=torch.bfloat16, device="cuda")).shape == (0, H)
     torch.cuda.synchronize()
+
+
+def test_batched_layer_from_two_host_threads():
+    """The batched (grouped) layer forks its shared expert and routed up
+    projection onto a second per-device stream with events: two host threads,
+    each calling its own block (own workspace) on its own stream 12 times,
+    get the bits of the same calls made one after another."""
+    import threading
+    from vq_cases import PATH_GROUPED, hooks
+    import ctypes
+    print("batched layer from two host threads", flush=True)
+    rng = np.random.default_rng(77)
+    E, H, I, D, K, k, T = 32, 1024, 512, 4, 4096, 4, 24
+    blk, projs, sh, shv = _block(rng, E, H, I, D, K, k, shared=True)
+    blk2, _, _, _ = _block(np.random.default_rng(77), E, H, I, D, K, k, shared=True)
+    keep = []
+    path = ctypes.c_int32()
+    assert hooks().vqk__test_moe_path(ctypes.byref(blk._fused_desc(keep)), T, ctypes.byref(path)) == 0
+    assert path.value == PATH_GROUPED
+    xs = [torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to("cuda", torch.bfloat16)
+          for _ in range(2)]
+    lgs = [torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).cuda() for _ in range(2)]
+    blocks = [blk, blk2]
+    ref = [blocks[i].fused(xs[i], lgs[i]).clone() for i in range(2)]
+    torch.cuda.synchronize()
+    outs = [[], []]
+    errs = []
+
+    def worker(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for _ in range(12):
+                    outs[i].append(blocks[i].fused(xs[i], lgs[i]))
+            s.synchronize()
+        except Exception as ex:          # reported below, in the test's thread
+            errs.append(ex)
+    th = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errs, errs
+    for i in range(2):
+        assert len(outs[i]) == 12
+        for y in outs[i]:
+            assert torch.equal(y.view(torch.int16), ref[i].view(torch.int16))
+    ref0, _, _ = vo.moe_layer(xs[0].float().cpu().numpy(), lgs[0].cpu().numpy(), _spec(projs["gate"]),
+                              _spec(projs["up"]), _spec(projs["down"]), k, h_round=np.float16,
+                              shared={n: _spec(m) for n, m in sh.items()},
+                              shared_gate=torch.from_numpy(shv).to(torch.bfloat16).float().numpy())
+    assert_close(ref[0].float().cpu().numpy(), ref0, what="two threads")
