@@ -1679,10 +1679,12 @@ static std::mutex g_side_mu;
 static SideStream g_side[kMaxSideDevices];
 
 // The current device's side stream (g_side_mu held), or nullptr when it
-// cannot be created (the layer then runs on the caller's stream alone).
-static SideStream *side_stream_locked() {
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxSideDevices) {
+// cannot be created or `st` belongs to another device (the layer then runs
+// on the caller's stream alone).
+static SideStream *side_stream_locked(hipStream_t st) {
+    int dev = -1, sdev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxSideDevices ||
+        (st && (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev))) {
         (void)hipGetLastError();
         return nullptr;
     }
@@ -1720,7 +1722,7 @@ static int launch_moe_grouped(const vqk_moe_desc *m, const MoePlan &pl, uint8_t 
     float *yd = reinterpret_cast<float *>(ws + pl.lay.yd), *ysh = reinterpret_cast<float *>(ws + pl.lay.ysh);
     void *sort = ws + pl.lay.sort;
     std::lock_guard<std::mutex> lk(g_side_mu);
-    SideStream *ss = side_stream_locked();
+    SideStream *ss = side_stream_locked(st);
     const hipStream_t sb = ss ? ss->s : st;
     int rc = VQK_OK;
     // event i recorded on `from`, waited for by `to` (nothing without a side stream)
