@@ -153,3 +153,47 @@ def test_graph_moe_layer(T, path):
         _rand_(lg, rng)
     refill(-1)
     _replays(lambda: blk.fused(x, lg, return_route=True), refill)
+
+
+_FIRST_CAPTURED = r"""
+import sys
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + '/tests')
+import numpy as np, torch
+from test_gpu_graphs import _block, _rand_
+rng = np.random.default_rng(91)
+T, E = 24, 32
+blk = _block(rng, E, 1024, 512, 4, 4096, 4, shared=True)
+x = torch.empty((T, 1024), dtype=torch.bfloat16, device='cuda')
+lg = torch.empty((T, E), dtype=torch.float32, device='cuda')
+_rand_(x, rng); _rand_(lg, rng)
+# the block's workspace comes from an allocation outside the capture
+blk._ws = torch.zeros(1 << 26, dtype=torch.uint8, device='cuda')
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    y = blk.fused(x, lg)            # the process's first batched call: captured
+for rep in range(3):
+    _rand_(x, rng); _rand_(lg, rng)
+    g.replay(); torch.cuda.synchronize()
+    got = y.clone()
+    want = blk.fused(x, lg)         # eager: creates the second stream now
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), rep
+print('FIRST_CAPTURED_OK')
+"""
+
+
+def test_graph_first_batched_call_captured():
+    """A process whose first batched layer call is made inside a graph
+    capture: the library does not create its second stream during the
+    capture (that call runs on the caller's stream alone), and the replays
+    give the bits of eager calls made afterwards on the second stream.
+    Runs in a fresh process, since the second stream lives per process."""
+    import pathlib
+    import subprocess
+    import sys
+    print("graph: first batched call captured (subprocess)", flush=True)
+    root = str(pathlib.Path(__file__).resolve().parents[1])
+    r = subprocess.run([sys.executable, "-c", _FIRST_CAPTURED, root], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0 and "FIRST_CAPTURED_OK" in r.stdout, (r.stdout[-2000:], r.stderr[-2000:])

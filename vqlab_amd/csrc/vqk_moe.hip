@@ -1690,6 +1690,13 @@ static SideStream *side_stream_locked(hipStream_t st) {
     }
     SideStream &ss = g_side[dev];
     if (!ss.s) {
+        // never create it while `st` is being captured into a graph: that
+        // call runs on the caller's stream alone
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
         SideStream n;
         bool ok = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking) == hipSuccess;
         for (int i = 0; ok && i < 4; ++i)
