@@ -50,7 +50,7 @@ def _draw_linear(n, seed):
     return cases
 
 
-_LIN = _draw_linear(32, 20261202)
+_LIN = _draw_linear(64, 20261202)
 _LIN_IDS = [f"{c[0]}-d{c[1]}K{c[2]}{'p' if c[3] else 'u'}G{c[4]}IN{c[5]}OUT{c[6]}E{c[7]}{c[10]}"
             + ("sz" if c[11] else "") for c in _LIN]
 
