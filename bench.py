@@ -1,7 +1,7 @@
 """Benchmark of the VQ MoE decode layer on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload c1|c2|c3|c3b4|c4|c4t16|c4capped|c4t16capped|c5|gather|stream]
+                    [--workload c1|c2|c3|c3b4|c4|c4t16|c4capped|c4t16capped|c5|gather|stream|launch]
 
 Default workload: a Qwen3.6-35B-A3B-shaped MoE
 decode layer -- hidden 2048, 256 experts of intermediate 512, top-8 softmax
@@ -12,7 +12,7 @@ batch 1, bf16 activations. Weights are random (no checkpoints offline), in
 rather than the 256 MB MALL.
 
 A step is one decode token through the 8-layer stack: per layer, one fused
-call (device routing + gate/up/SwiGLU + down/combine, two kernels) with that
+call (device routing + gate/up/SwiGLU + down/combine in one launch) with that
 step's own logits. The timed steps are captured once in a HIP graph and
 replayed; HIP events on the launch stream bracket the replay.
 
@@ -41,10 +41,12 @@ fp32 matvec on the host, one thread and all cores.
 through VQLinear 5120->17408 then 17408->5120 (d8, K=65536 uint16 codes);
 value = TFLOP/s of the two GEMMs, roofline against the fp16 MFMA peak.
 
---workload gather / stream: measurement probes (libvqk test hooks outside the
-ABI): the random 16-byte gather rate from an L2-resident table, and the
-fastest one-launch streaming read of config 1's weight bytes (the floor of a
-GEMV that reads them in one launch).
+--workload gather / stream / launch: measurement probes (libvqk test hooks
+outside the ABI): the random 16-byte gather rate from an L2-resident table,
+the fastest one-launch streaming read of config 1's weight bytes (the floor
+of a GEMV that reads them in one launch), and the cost of one kernel boundary
+(back-to-back launches of a kernel that reads 16 bytes, in a HIP graph: what
+every call of a one-launch layer pays beyond its own work).
 """
 from __future__ import annotations
 
@@ -98,6 +100,9 @@ WORKLOADS = {
     "stream": dict(kind="stream", bytes=4096 * 2048 + 4096 * 64 * 2, layers=120,
                    desc="streaming read of config 1's codes + scales (8.9 MB) per launch, "
                         "120 rotating buffers (probe)"),
+    # measurement probe: back-to-back launches that do (almost) nothing
+    "launch": dict(kind="launch", launches=1000,
+                   desc="1000 back-to-back launches of a 16-byte read in one HIP graph (probe)"),
     "c5": dict(N=2048, H=5120, F=17408, d=8, K=65536, kind="prefill",
                desc="Dense Qwen3.8-27B-shaped VQ prefill: 5120x17408 then 17408x5120, "
                     "x [2048, 5120] (BASELINE configs[4])"),
@@ -841,8 +846,39 @@ def run_stream(torch, dev, a, w):
             "cpu_baseline": None}, 0.0, 1
 
 
+def run_launch(torch, dev, a, w):
+    """The kernel boundary: vqk__probe_stream over one 16-byte buffer (one
+    load, one word written per workgroup), launched back to back on one
+    stream in a HIP graph at several grid sizes. Each launch waits for the
+    previous one to end, as a layer call waits for the layer before it, so
+    the time per launch is what dispatch, the end-of-kernel release and the
+    next start cost together."""
+    import ctypes
+    from vqlab_amd import _lib as LB, _torch as TT
+    lib = LB.lib()
+    lib.vqk__probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
+                                      ctypes.c_void_p]
+    L = w["launches"]
+    buf = torch.zeros(4, dtype=torch.int32, device=dev)
+    sink = torch.empty(1024, dtype=torch.int32, device=dev)
+    rows = []
+    for wgs in (1, 128, 384, 1024):
+        def step(s, wgs=wgs):
+            st = TT.stream(dev)
+            for _ in range(L):
+                LB.check(lib.vqk__probe_stream(TT.ptr(buf), 16, wgs, TT.ptr(sink), st))
+        _, ev_ms = _graph_time(torch, step, 2, 5, dev)
+        rows.append({"workgroups": wgs, "us_per_launch": round(ev_ms * 1e3 / (5 * L), 3)})
+        log(rows[-1])
+    best = min(rows, key=lambda r: r["us_per_launch"])
+    return {"metric": "us per back-to-back launch of a kernel that reads 16 bytes",
+            "value": best["us_per_launch"], "unit": "us", "higher_is_better": False, "dtype": "u32",
+            "config": {"workload": w["desc"], "launches": L},
+            "grids": rows, "roofline": None, "cpu_baseline": None}, 0.0, 1
+
+
 RUNNERS = {"layer": run_layer, "mtp": run_mtp, "prefill": run_prefill, "dense_gemv": run_dense_gemv,
-           "gather": run_gather, "stream": run_stream}
+           "gather": run_gather, "stream": run_stream, "launch": run_launch}
 
 
 def main():
