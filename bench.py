@@ -846,29 +846,37 @@ def run_stream(torch, dev, a, w):
             "cpu_baseline": None}, 0.0, 1
 
 
-def run_launch(torch, dev, a, w):
-    """The kernel boundary: vqk__probe_stream over one 16-byte buffer (one
-    load, one word written per workgroup), launched back to back on one
-    stream in a HIP graph at several grid sizes. Each launch waits for the
-    previous one to end, as a layer call waits for the layer before it, so
-    the time per launch is what dispatch, the end-of-kernel release and the
-    next start cost together."""
+def _launch_us(torch, dev, wgs, launches, reps=5):
+    """µs per launch of vqk__probe_stream over one 16-byte buffer (one load,
+    one word written per workgroup) at `wgs` workgroups, `launches` back to
+    back on one stream, `reps` times over in one HIP graph."""
     import ctypes
     from vqlab_amd import _lib as LB, _torch as TT
     lib = LB.lib()
     lib.vqk__probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
                                       ctypes.c_void_p]
-    L = w["launches"]
     buf = torch.zeros(4, dtype=torch.int32, device=dev)
-    sink = torch.empty(1024, dtype=torch.int32, device=dev)
+    sink = torch.empty(max(wgs, 1), dtype=torch.int32, device=dev)
+
+    def step(s):
+        st = TT.stream(dev)
+        for _ in range(launches):
+            LB.check(lib.vqk__probe_stream(TT.ptr(buf), 16, wgs, TT.ptr(sink), st))
+    _, ev_ms = _graph_time(torch, step, 2, reps, dev)
+    return round(ev_ms * 1e3 / (reps * launches), 3)
+
+
+def run_launch(torch, dev, a, w):
+    """The kernel boundary: vqk__probe_stream over one 16-byte buffer,
+    launched back to back on one stream in a HIP graph at several grid sizes.
+    Each launch waits for the previous one to end, as a layer call waits for
+    the layer before it, so the time per launch is what dispatch, the
+    end-of-kernel release and the next start cost together (plus the probe's
+    own load and store)."""
+    L = w["launches"]
     rows = []
     for wgs in (1, 128, 384, 1024):
-        def step(s, wgs=wgs):
-            st = TT.stream(dev)
-            for _ in range(L):
-                LB.check(lib.vqk__probe_stream(TT.ptr(buf), 16, wgs, TT.ptr(sink), st))
-        _, ev_ms = _graph_time(torch, step, 2, 5, dev)
-        rows.append({"workgroups": wgs, "us_per_launch": round(ev_ms * 1e3 / (5 * L), 3)})
+        rows.append({"workgroups": wgs, "us_per_launch": _launch_us(torch, dev, wgs, L)})
         log(rows[-1])
     best = min(rows, key=lambda r: r["us_per_launch"])
     return {"metric": "us per back-to-back launch of a kernel that reads 16 bytes",
@@ -915,6 +923,14 @@ def main():
     out.update(body)
     if a.workload == "c2" and not a.no_workloads:
         out["workloads"] = extra_workloads(torch, dev, a)
+        try:
+            out["kernel_boundary"] = {
+                "us_per_launch": _launch_us(torch, dev, 384, 1000), "workgroups": 384,
+                "what": "back-to-back launches in a HIP graph of a kernel that loads 16 bytes and "
+                        "stores one word per workgroup, at this layer's grid (--workload launch): "
+                        "the part of each layer call that any dependent launch pays"}
+        except Exception as e:                      # reported, never hidden
+            out["kernel_boundary"] = {"error": f"{type(e).__name__}: {e}"}
     print(json.dumps(out), flush=True)
 
 
