@@ -361,6 +361,20 @@ def test_moe_header_constant_and_paths(L):
         assert p.value == PATH_FUSED
     finally:
         hooks().vqk__test_l1_mode(prev)
+    # with a shared expert (its own E = 1 projections and gate vector): batch
+    # 1 is one launch while the grid fits two workgroups per CU -- top-6 of
+    # 128 (7 pairs: 224 gate/up + 128 down workgroups) -- and two kernels
+    # past it: top-8 (9 pairs, 64 lanes per down row: 288 + 256 > 2 x 256)
+    sh = [proj(1, I, H, 4 << 30), proj(1, I, H, 5 << 30), proj(1, H, I, 6 << 30)]
+    d.sh_gate, d.sh_up, d.sh_down = (ctypes.pointer(w) for w in sh)
+    d.sh_gate_vec, d.sh_gate_vec_type = 7 << 30, L.VQK_BF16
+    L.check(hooks().vqk__test_moe_path(ctypes.byref(d), 1, ctypes.byref(p)))
+    assert p.value == PATH_FUSED, ("shared, 9 pairs", p.value)
+    ws_[0].E = ws_[1].E = ws_[2].E = 128
+    d.top_k = 6
+    for T, want in ((1, PATH_ONE_LAUNCH), (2, PATH_FUSED), (64, PATH_GROUPED)):
+        L.check(hooks().vqk__test_moe_path(ctypes.byref(d), T, ctypes.byref(p)))
+        assert p.value == want, ("shared", T, p.value)
 
 
 def test_options_crowded_rule_is_switchable(L):

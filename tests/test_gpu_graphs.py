@@ -131,16 +131,18 @@ def _block(rng, E, H, I, D, K, k, shared):
         shared=dev(sh) if shared else None, shared_gate=sgv if shared else None)
 
 
-@pytest.mark.parametrize("T,path", [(1, PATH_ONE_LAUNCH), (3, PATH_FUSED), (24, PATH_GROUPED)])
-def test_graph_moe_layer(T, path):
-    """The layer at T = 1 (one launch), T = 3 (two fused kernels) and T = 24
-    with a shared expert (96 routed pairs: device sort, grouped gate/up/down,
-    split-K shared expert, combine): routing and outputs per replay."""
+@pytest.mark.parametrize("T,path,shared", [(1, PATH_ONE_LAUNCH, False), (1, PATH_ONE_LAUNCH, True),
+                                           (3, PATH_FUSED, False), (24, PATH_GROUPED, True)])
+def test_graph_moe_layer(T, path, shared):
+    """The layer at T = 1 (one launch, with and without a shared expert),
+    T = 3 (two fused kernels) and T = 24 with a shared expert (96 routed
+    pairs: device sort, grouped gate/up/down, split-K shared expert,
+    combine): routing and outputs per replay."""
     import ctypes
-    print(f"graph: moe layer T={T}", flush=True)
-    rng = np.random.default_rng(65 + T)
+    print(f"graph: moe layer T={T} shared={shared}", flush=True)
+    rng = np.random.default_rng(65 + T + 7 * shared)
     E, H, I, k = 32, 1024, 512, 4
-    blk = _block(rng, E, H, I, 4, 4096, k, shared=T > 3)
+    blk = _block(rng, E, H, I, 4, 4096, k, shared=shared)
     keep = []
     got = ctypes.c_int32()
     assert hooks().vqk__test_moe_path(ctypes.byref(blk._fused_desc(keep)), T, ctypes.byref(got)) == 0

@@ -378,6 +378,47 @@ def test_moe_one_launch_geometries(geom):
     assert_close(y1.float().cpu().numpy(), ref, what=f"one launch {geom}")
 
 
+_L1_SHARED_GEOMS = [
+    (128, 2048, 512, 4, 4096, 6, True),
+    (48, 512, 448, 2, 512, 5, False),
+    (24, 128, 384, 4, 1024, 3, True),
+]
+
+
+@pytest.mark.parametrize("geom", _L1_SHARED_GEOMS,
+                         ids=[f"d{g[3]}K{g[4]}E{g[0]}I{g[2]}" for g in _L1_SHARED_GEOMS])
+def test_moe_one_launch_shared_expert(geom):
+    """A layer with a shared expert at batch 1 runs as one launch too: the
+    shared pair's gate / up rows go through the hand-off like the routed
+    pairs', its down table sits beside the routed one in the down
+    workgroups' LDS, and each down workgroup takes the shared gate
+    sigmoid(x . v) itself. Call after call on one workspace, the output is
+    the two kernels' bits (the same token alone with the one launch switched
+    off, and inside a T = 2 call) and within the oracle's bar."""
+    from vq_cases import PATH_ONE_LAUNCH, moe_path, two_kernels
+    E, H, I, D, K, k, norm = geom
+    print(f"moe one launch with a shared expert {geom}", flush=True)
+    rng = np.random.default_rng(sum(geom[:6]) + 300)
+    blk, projs, sh, shv = _block(rng, E, H, I, D, K, k, shared=True, norm=norm)
+    assert moe_path(blk, 1) == PATH_ONE_LAUNCH and moe_path(blk, 2) != PATH_ONE_LAUNCH
+    shared = {n: _spec(m) for n, m in sh.items()}
+    sgv = torch.from_numpy(shv).to(torch.bfloat16).float().numpy()
+    for i in range(3):
+        x, lg = _xl(rng, 2, H, E)
+        y1 = blk.fused(x[:1], lg[:1])
+        y2 = blk.fused(x, lg)
+        with two_kernels():
+            yk = blk.fused(x[:1], lg[:1])
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(y1[0]), _bits(y2[0])), f"call {i}: one launch vs T=2"
+        assert np.array_equal(_bits(y1), _bits(yk)), f"call {i}: one launch vs two kernels"
+        ref, _, _ = vo.moe_layer(x[:1].float().cpu().numpy(), lg[:1].cpu().numpy(), _spec(projs["gate"]),
+                                 _spec(projs["up"]), _spec(projs["down"]), k, norm=norm,
+                                 shared=shared, shared_gate=sgv, h_round=np.float16)
+        assert_close(y1.float().cpu().numpy(), ref, what=f"one launch shared {geom} call {i}")
+    blk.status()
+
+
 def _share(ws_size, *blks):
     ws = torch.zeros(ws_size, dtype=torch.uint8, device="cuda")
     for b in blks:

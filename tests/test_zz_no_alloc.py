@@ -97,19 +97,21 @@ def test_noalloc_matches_workspace_entry(case):
 
 
 def test_noalloc_one_launch_geometries_alternate():
-    """The scratch array is shared by every layer: two one-launch geometries
-    alternating through vqk_moe_decode_layer_noalloc (the call number and the
-    hand-off words at fixed header offsets, tags naming the word's header
-    index) give, call after call, the bits of the two-kernel form through a
-    caller workspace; the scratch header reports no error afterwards."""
+    """The scratch array is shared by every layer: three one-launch geometries
+    (one with a shared expert) alternating through
+    vqk_moe_decode_layer_noalloc (the call number and the hand-off words at
+    fixed header offsets, tags naming the word's header index) give, call
+    after call, the bits of the two-kernel form through a caller workspace;
+    the scratch header reports no error afterwards."""
     from vqlab_amd import _lib as L, _torch as Tt
     from vq_cases import PATH_ONE_LAUNCH, moe_path, two_kernels
     print("noalloc: two one-launch geometries alternate", flush=True)
     rng = np.random.default_rng(77)
-    geoms = [(256, 2048, 512, 4, 4096, 8), (64, 1024, 256, 4, 256, 6)]
+    geoms = [(256, 2048, 512, 4, 4096, 8, False), (64, 1024, 256, 4, 256, 6, False),
+             (128, 1024, 256, 4, 1024, 6, True)]
     blks = []
     for g in geoms:
-        blk, *_ = _block(rng, *g, False)
+        blk, *_ = _block(rng, *g)
         assert moe_path(blk, 1) == PATH_ONE_LAUNCH
         keep = []
         blks.append((blk, blk._fused_desc(keep), keep, g))

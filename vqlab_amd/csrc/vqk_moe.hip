@@ -787,16 +787,17 @@ struct DownLane {
 };
 
 // Expert, router weight and first-step weights of this lane's pair for row
-// tile `bx`; `eid(j)` / `wt(j)` give the routing (workspace or LDS).
-template <int BITS, int GPB, typename EID, typename WT>
+// tile `bx`; `eid(j)` / `wt(j)` give the routing and `sgv()` the shared
+// expert's gate (workspace or LDS).
+template <int BITS, int GPB, typename EID, typename WT, typename SGV>
 __device__ __forceinline__ void down_prep(const MoeParams &p, int bx, int t, const DownLane &dl,
-                                          EID eid, WT wt, DownState<BITS, GPB> &ds) {
+                                          EID eid, WT wt, SGV sgv, DownState<BITS, GPB> &ds) {
     const int wave = threadIdx.x >> 6;
     const MoeW &wd = dl.is_shared ? p.sdown : p.down;
     ds.e = -1;
     ds.wj = 0.f;
     if (dl.on) {
-        if (dl.is_shared) { ds.e = 0; ds.wj = p.sg[t]; }
+        if (dl.is_shared) { ds.e = 0; ds.wj = sgv(); }
         else {
             const int id = eid(dl.j);
             ds.e = (id >= 0 && id < p.E) ? id : -1;
@@ -986,14 +987,16 @@ __global__ void __launch_bounds__(moe_waves_down(W) * kWave) k_moe_down(const Mo
     }
     DownState<BITS, GPB> ds;
     down_prep<BITS, GPB>(p, int(blockIdx.x), t, dl, [&](int) { return id; },
-                         [&](int) { return wt; }, ds);
+                         [&](int) { return wt; }, [&] { return p.sg[t]; }, ds);
     down_stage_cb<D, CBN, cb_in_lds(D, BITS), moe_waves_down(W) * kWave>(p, smem);
     down_run<D, BITS, GPB, W>(p, int(blockIdx.x), t, smem, dl, ds, hf);
 }
 
 // ------------------------------------------------------------ one launch
-// Both phases of a layer in one launch, for tables that fit LDS, no shared
-// expert, and a grid that is resident at once (two workgroups per CU):
+// Both phases of a layer in one launch, for tables that fit LDS (with a
+// shared expert: its down table beside the routed one, its gate taken by each
+// down workgroup's routing wave) and a grid that is resident at once (two
+// workgroups per CU):
 // workgroups [0, G1) run the gate/up phase as k_moe_up does, and
 // [G1, G1 + G2) the down phase of one row tile of one token. A down
 // workgroup routes its token itself (the same routine, hence the same
@@ -1014,6 +1017,7 @@ struct L1Lds {
     RouteLds rl;
     int ids[kMaxTopK];
     float wts[kMaxTopK];
+    float sg;            // down workgroups: the shared expert's gate (layers with one)
     uint64_t call_bad;   // down workgroups: call number | (error word set at the start) << 32
 };
 // Waves of a down workgroup that decode rows (all of them stage, route and
@@ -1024,17 +1028,25 @@ struct L1Lds {
 // 10.33 us per config-2 layer against 10.0 for eight over 128.
 constexpr int kL1DownWaves = 8;
 
-template <int D, int BITS, int GPB>
+template <int D, int BITS, int GPB, bool SH>
 __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds &ll, int cbi) {
     constexpr int CBN = 1 << BITS;                 // the whole table (the host checks it fits)
     constexpr int XH = kBlock * D, XS = XH + 8;
     constexpr int NT = 2 * kThreads;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int bx = cbi % p.l1_gx2, t = cbi / p.l1_gx2;
+    // LDS: the routed down table, the SwiGLU rows at a fixed offset (their
+    // reads and writes after the hand-off keep constant address offsets),
+    // then a shared expert's down table; the instance without a shared
+    // expert (SH false) carries none of its code (a runtime flag cost 0.03-0.05
+    // us per config-2 layer)
     f16 *xs = reinterpret_cast<f16 *>(smem + CBN * D * 2);
+    const int sh_off = CBN * D * 2 + p.P * p.NB2 * XS * 2;
     // the last wave routes (the gate/up workgroup beside it on the CU routes
     // on its wave 0, and two routing waves on one SIMD slow both: 9.99 ->
-    // 9.83 us per config-2 layer); the others stage the down table
+    // 9.83 us per config-2 layer) and, with a shared expert, takes its gate
+    // with the routine the gate/up workgroup 0 uses (the same bits); the
+    // others stage the down tables (routed, then shared)
     uint64_t ev = 0, er = 0;
     if (wave == NT / kWave - 1) {
         int e_pair, my_idx = -1;
@@ -1045,12 +1057,19 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
             ll.ids[lane] = (my_idx >= 0 && my_idx < p.E) ? my_idx : -1;
             ll.wts[lane] = my_w;
         }
+        if constexpr (SH) {
+            const float acc = shared_gate_dot(p.x, p.x_type, p.sg_vec, p.sg_type, p.H, t);
+            if (lane == 0) ll.sg = 1.f / (1.f + __expf(-acc));
+        }
     } else {
         if (tid == 0) {
             ev = l1_load(p.l1_epoch);
             er = l1_load(p.l1_err);
         }
         stage_codebook_fixed<D, CBN, NT - kWave, 0>(p.down.codebook, p.down.K, reinterpret_cast<h2 *>(smem));
+        if constexpr (SH)
+            stage_codebook_fixed<D, CBN, NT - kWave, 0>(p.sdown.codebook, p.sdown.K,
+                                                        reinterpret_cast<h2 *>(smem + sh_off));
     }
     wait_vmem();
     if (tid == 0) {
@@ -1063,7 +1082,7 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
     const bool dec = wave < kL1DownWaves;
     if (dec) {
         down_prep<BITS, GPB>(p, bx, t, dl, [&](int j) { return ll.ids[j]; }, [&](int j) { return ll.wts[j]; },
-                             ds);
+                             [&] { return ll.sg; }, ds);
         // the weights land here, before the polls: left to itself the
         // compiler sinks these loads past the poll loop and the barrier (it is
         // short of registers), which put a whole memory latency between the
@@ -1082,7 +1101,7 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
     struct EntW { uint32_t w[D / 2]; };
     EntW ent[kBlock];
     {
-        const Ent *cbe = reinterpret_cast<const Ent *>(smem);
+        const Ent *cbe = reinterpret_cast<const Ent *>(smem + ((SH && dl.is_shared) ? sh_off : 0));
         const bool live = dec && ds.cr >= 0;
 #pragma unroll
         for (int i = 0; i < kBlock; ++i) {
@@ -1165,7 +1184,7 @@ __device__ __forceinline__ void l1_down(const MoeParams &p, uint8_t *smem, L1Lds
     }
 }
 
-template <int D, int BITS, int GPB>
+template <int D, int BITS, int GPB, bool SH>
 __global__ void __launch_bounds__(2 * kThreads, 4) k_moe_layer1(const MoeParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ L1Lds ll;
@@ -1197,7 +1216,7 @@ __global__ void __launch_bounds__(2 * kThreads, 4) k_moe_layer1(const MoeParams 
             }
         }
     } else {
-        l1_down<D, BITS, GPB>(p, smem, ll, b - p.l1_g1);
+        l1_down<D, BITS, GPB, SH>(p, smem, ll, b - p.l1_g1);
     }
 }
 
@@ -1482,12 +1501,13 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
                          pl->smem1, pl->smem2);
     pl->lay = moe_layout(T, k, P, gg.OUT, gg.IN, pl->path, E, pl->split);
     // One launch: batch 1, gate/up and down workgroups resident together, two
-    // per CU (LDS and 128 VGPRs each), tables in LDS, no shared expert, one
-    // format, the stamps and words within the header.
+    // per CU (LDS and 128 VGPRs each), tables in LDS (a shared expert's down
+    // table beside the routed one), one format, the stamps and words within
+    // the header.
     pl->l1 = false;
     pl->smem_l1 = 0;
     pl->l1_nwg = 0;
-    if (T == 1 && g_l1_mode.load() == 0 && pl->path == kMoeFused && !pl->split && full1 && full2 && !shared &&
+    if (T == 1 && g_l1_mode.load() == 0 && pl->path == kMoeFused && !pl->split && full1 && full2 &&
         gg.D == gd.D && gg.BITS == gd.BITS && gg.gpb == gd.gpb && l1_instance(gg.D, gg.BITS, gg.gpb) &&
         E <= kL1Slots * kWave && pl->grid1.z == 1 && gg.OUT % 2 == 0 && p.rows_per_wg1 % 2 == 0 &&
         int64_t(P) * gg.OUT / 2 <= kL1MaxWords) {
@@ -1496,7 +1516,7 @@ static int moe_plan(const vqk_moe_desc *m, int64_t T, MoePlan *pl) {
         const int64_t gx2 = (gd.OUT + rows2 - 1) / rows2;
         const int64_t g1 = int64_t(pl->grid1.x) * pl->grid1.y;
         const int64_t nwg = g1 + gx2 * T;
-        const size_t sm = std::max(pl->smem1, cb2 + xs2);
+        const size_t sm = std::max(pl->smem1, (shared ? 2 : 1) * cb2 + xs2);
         if (nwg <= std::min<int64_t>(2 * ncu, kL1MaxWg) && 2 * (sm + sizeof(L1Lds) + 256) <= 160 * 1024) {
             pl->l1 = true;
             pl->smem_l1 = sm;
@@ -1560,7 +1580,8 @@ static int launch_moe_down_wide(const MoeParams &p, int d, int bits, int gpb, di
 
 template <int D, int BITS, int GPB>
 static int go_layer1(const MoeParams &p, dim3 grid, size_t smem, hipStream_t st) {
-    return launch_with_lds<k_moe_layer1<D, BITS, GPB>>(grid, dim3(2 * kThreads), smem, st, p);
+    if (p.shared) return launch_with_lds<k_moe_layer1<D, BITS, GPB, true>>(grid, dim3(2 * kThreads), smem, st, p);
+    return launch_with_lds<k_moe_layer1<D, BITS, GPB, false>>(grid, dim3(2 * kThreads), smem, st, p);
 }
 #define VQK_L1_CASE(D, B, G) if (d == D && bits == B && gpb == G) return go_layer1<D, B, G>(p, grid, smem, st);
 static int launch_moe_layer1(const MoeParams &p, int d, int bits, int gpb, dim3 grid, size_t smem,
