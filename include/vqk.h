@@ -215,7 +215,8 @@ int vqk_dense_gemm(const vqk_weights *w, const void *x, int32_t x_type,
  * rest is scratch whose contents do not matter. One workspace may serve any
  * number of layers, geometries and T, one call at a time: calls sharing a
  * workspace must not overlap. A batch-1 call whose tables fit LDS (a shared
- * expert allowed, E <= 256, d 2 or 4 with 8-12-bit codes) runs as ONE launch whose
+ * expert allowed, E <= 256, d 2 or 4 with 8-12-bit codes, a grid of at most
+ * two workgroups per compute unit) runs as ONE launch whose
  * workgroups hand the SwiGLU rows to each other through the header, with a
  * call number kept there between calls. Its waits are bounded (~45 ms): a wait
  * that runs out -- only possible when other work holds the GPU's compute
