@@ -492,18 +492,20 @@ def test_moe_one_launch_gives_up_loudly():
 _T1_LOGITS = ["ties", "all_equal", "ten_finite", "signed_zeros", "nan_mix", "few_valid"]
 
 
+@pytest.mark.parametrize("shared", [False, True], ids=["routed", "shared"])
 @pytest.mark.parametrize("case", _T1_LOGITS)
-def test_moe_one_launch_special_logits(case):
+def test_moe_one_launch_special_logits(case, shared):
     """Batch-1 routing inside the one-launch layer (every workgroup routes the
-    token itself) on tied, all-equal, -inf, +-0 and NaN logits: the same
-    experts and weights as the oracle (ties to the lower id; NaN never chosen,
-    a selection left without a non-NaN logit is id -1 / weight 0), outputs
-    within the bar, and bit for bit the two-kernel form."""
+    token itself) on tied, all-equal, -inf, +-0 and NaN logits, with and
+    without a shared expert: the same experts and weights as the oracle (ties
+    to the lower id; NaN never chosen, a selection left without a non-NaN
+    logit is id -1 / weight 0, the shared expert still added), outputs within
+    the bar, and bit for bit the two-kernel form."""
     from vq_cases import PATH_ONE_LAUNCH, moe_path, two_kernels
-    print(f"moe one launch special logits {case}", flush=True)
+    print(f"moe one launch special logits {case} shared={shared}", flush=True)
     rng = np.random.default_rng(33)
     E, H, I, D, K, k = 64, 1024, 256, 4, 256, 6
-    blk, projs, _, _ = _block(rng, E, H, I, D, K, k)
+    blk, projs, sh, shv = _block(rng, E, H, I, D, K, k, shared=shared)
     assert moe_path(blk, 1) == PATH_ONE_LAUNCH
     lg = (np.round(rng.standard_normal(E) * 2) / 2).astype(np.float32)
     if case == "all_equal":
@@ -529,9 +531,12 @@ def test_moe_one_launch_special_logits(case):
     assert np.array_equal(ids.cpu().numpy(), rids), (ids.cpu().numpy(), rids)
     assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-6)
     assert np.array_equal(_bits(y), _bits(yk))
+    shs = {n: _spec(m) for n, m in sh.items()} if shared else None
+    sgv = torch.from_numpy(shv).to(torch.bfloat16).float().numpy() if shared else None
     ref, _, _ = vo.moe_layer(x.float().cpu().numpy(), lg[None], _spec(projs["gate"]),
-                             _spec(projs["up"]), _spec(projs["down"]), k, h_round=np.float16)
-    assert_close(y.float().cpu().numpy(), ref, what=f"special logits {case}")
+                             _spec(projs["up"]), _spec(projs["down"]), k, shared=shs, shared_gate=sgv,
+                             h_round=np.float16)
+    assert_close(y.float().cpu().numpy(), ref, what=f"special logits {case} shared={shared}")
 
 
 def test_empty_batches():
