@@ -453,18 +453,20 @@ def test_moe_one_launch_geometries_share_a_workspace():
     ba.status()
 
 
-def test_moe_one_launch_gives_up_loudly():
+@pytest.mark.parametrize("shared", [False, True], ids=["routed", "shared"])
+def test_moe_one_launch_gives_up_loudly(shared):
     """A one-launch wait that runs out never computes through: the
     affected rows come out NaN and the header's error word is set (all
     kernels still end normally -- the give-up is forced from the host with a
     zero wait bound). Later one-launch calls on that workspace give NaN rows
     until reset; vqk_moe_layer_status reports it; after reset the layer
-    gives the two-kernel form's bits again."""
+    gives the two-kernel form's bits again. With and without a shared
+    expert (its words travel with the routed ones)."""
     from vq_cases import PATH_ONE_LAUNCH, l1_spins, moe_path, two_kernels
-    print("moe one launch: forced give-up", flush=True)
+    print(f"moe one launch: forced give-up, shared={shared}", flush=True)
     rng = np.random.default_rng(32)
     E, H, I, D, K, k = 64, 1024, 256, 4, 256, 6
-    blk, projs, _, _ = _block(rng, E, H, I, D, K, k)
+    blk, projs, _, _ = _block(rng, E, H, I, D, K, k, shared=shared)
     assert moe_path(blk, 1) == PATH_ONE_LAUNCH
     x, lg = _xl(rng, 1, H, E)
     y0 = blk.fused(x, lg)
